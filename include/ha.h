@@ -1,0 +1,139 @@
+/*
+ * ha.h: C ABI of the MI355X hybrid-attention engine (gated-delta + gated causal GQA token mixers with
+ * prefix-cache snapshot/resume), the drop-in replacement for the hot path of the reference's WebGPU engine.
+ *
+ * Reference interface replaced (paths relative to the reference repository):
+ *   Engine constructor state and buffers      web/public/engine/engine.js:89-111
+ *   the linear_attention / full_attention
+ *     branches of Engine.plan()               web/public/engine/engine.js:253-276
+ *   Engine.forward({cache, keepCache,
+ *     timestamps}) incl. resume and snapshot  web/public/engine/engine.js:313-375
+ *   snapshot.release()                        web/public/engine/engine.js:361
+ *   manifest config + per-layer tensors       convert/export_engine.py:46-65,83
+ *
+ * Conventions
+ *   - Every function returns HA_OK (0) or a negative ha_status; ha_last_error() then returns a message for the
+ *     calling thread. The Node binding turns a non-zero status into a thrown Error, as the reference throws.
+ *   - All tensor arguments of ha_forward are DEVICE pointers (HBM). ha_device_alloc / ha_copy_* are provided for
+ *     callers without their own allocator.
+ *   - One engine is bound to one HIP stream; calls on one engine must not overlap (the reference is not
+ *     re-entrant either and its worker serialises calls, web/public/js/worker.js:249-253).
+ *   - A snapshot is only valid with the engine that made it.
+ */
+#ifndef HA_H
+#define HA_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HA_ABI_VERSION 1
+
+typedef struct ha_engine ha_engine;
+typedef struct ha_snapshot ha_snapshot;
+
+typedef enum ha_status {
+  HA_OK = 0,
+  HA_ERR_ARG = -1,      /* bad argument, shape or config */
+  HA_ERR_CONTEXT = -2,  /* P + L exceeds max_ctx (engine.js:316 "context ... exceeds") */
+  HA_ERR_HANDLE = -3,   /* invalid, foreign or released engine / snapshot handle */
+  HA_ERR_DEVICE = -4,   /* a HIP runtime call failed (engine.js:373 collects device errors) */
+  HA_ERR_NOMEM = -5,    /* device or host allocation failed */
+  HA_ERR_PARAM = -6     /* unknown tensor name or wrong element count (engine.js:177 "no tensor ...") */
+} ha_status;
+
+typedef enum ha_layer_kind {
+  HA_LINEAR_ATTENTION = 0, /* manifest layer_types "linear_attention" */
+  HA_FULL_ATTENTION = 1    /* manifest layer_types "full_attention" */
+} ha_layer_kind;
+
+typedef enum ha_dtype { HA_F32 = 0, HA_F16 = 1 } ha_dtype;
+
+typedef enum ha_recurrence {
+  HA_CHUNKED = 0,   /* prefill form: chunks of 64 rows at absolute positions, MFMA products (default) */
+  HA_SEQUENTIAL = 1 /* token-by-token fp32 rule with the state in registers (decode / resume) */
+} ha_recurrence;
+
+/* Engine shape. Field names follow the manifest config keys (export_engine.py:83). */
+typedef struct ha_config {
+  int n_layers;
+  const unsigned char* layer_kind; /* [n_layers] ha_layer_kind */
+  int batch;                       /* independent sequences per forward (the reference is batch 1) */
+  int max_ctx;                     /* LT, K/V cache rows per sequence (engine.js:92: 4096) */
+  /* gated-delta layers: linear_num_key_heads (= value heads), linear_key_head_dim, linear_value_head_dim,
+     linear_conv_kernel_dim */
+  int H, DK, DV, conv_k;
+  int lin_stride;   /* row stride (elements) of the fused in_proj rows qkv | z | a | b (8256 in the engine) */
+  int lin_dtype;    /* ha_dtype of linear-layer input rows and outputs */
+  int lin_gnorm;    /* 1: output the gated RMSNorm (GNORM, the engine's layer output); 0: the raw core output */
+  /* full-attention layers: num_attention_heads, num_key_value_heads, head_dim, rotary_dim */
+  int HQ, HK, HD, rot_dim;
+  int full_stride;  /* row stride of the fused qkv rows [q|gate] x HQ | k x HK | v x HK (5120) */
+  int full_dtype;   /* ha_dtype of full-layer input rows and outputs; the K/V cache is f16 */
+  float rope_theta; /* 1e7 */
+  float eps;        /* rms_norm_eps; must be 1e-6, the value the reference kernels hard-code */
+} ha_config;
+
+/* Per-call options of ha_forward (engine.js:313 options). NULL means all defaults (zeros). */
+typedef struct ha_forward_opts {
+  int recurrence;  /* ha_recurrence for the gated-delta layers */
+  int timestamps;  /* 1: time the whole forward with HIP events; result in gpu_ms (engine.js:331-348) */
+  int sync;        /* 1: wait for the stream before returning */
+  float gpu_ms;    /* out: forward time when timestamps = 1 (implies a wait) */
+  float* layer_ms; /* optional out [n_layers]: per-layer GPU ms (the reference's profile(), engine.js:292-307) */
+} ha_forward_opts;
+
+const char* ha_last_error(void);
+int ha_abi_version(void);
+
+/* Engine.create / constructor (engine.js:63-111): validates the config, allocates the working state, history
+   and K/V buffers and the RoPE table on HIP device `device`, and creates the engine's stream. */
+int ha_create(const ha_config* cfg, int device, ha_engine** out);
+int ha_destroy(ha_engine* e);
+
+/* Bind the engine to an existing HIP stream (hipStream_t passed as void*), e.g. a framework's current stream.
+   NULL rebinds the engine's own stream. */
+int ha_set_stream(ha_engine* e, void* stream);
+
+/* Upload one per-layer tensor under its manifest name (export_engine.py:55-58,64-65), as f32 host data:
+     linear layers: "conv" [C][conv_k] with C = 2*H*DK + H*DV, "neg_exp_A" [H], "dt_bias" [H], "gnorm" [DV]
+     full layers:   "q_norm" [HD], "k_norm" [HD] (stored as 1 + w, as the manifest stores them)
+   count is the number of floats. Unset tensors default to zeros (conv, neg_exp_A, dt_bias) or ones (norms). */
+int ha_set_param(ha_engine* e, int layer, const char* name, const float* host, size_t count);
+
+/* One forward over L new rows per sequence (engine.js:313-375, token-mixer part).
+     layer_in[i]:  [batch][L][lin_stride] (linear) or [batch][L][full_stride] (full) rows in that kind's dtype
+     layer_out[i]: [batch][L][H*DV] or [batch][L][HQ*HD] in that kind's dtype
+   resume: continue from this snapshot (engine.js:325-327); NULL starts from an empty context
+   keep:   if non-NULL, receives a new snapshot of the context after this call (engine.js:349-362)
+   Returns HA_ERR_CONTEXT if P + L > max_ctx. Layers run in order on the engine's stream. */
+int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* layer_out, const ha_snapshot* resume,
+               ha_snapshot** keep, ha_forward_opts* opts);
+
+/* Snapshot queries. P is the number of tokens the snapshot covers (engine.js:352 snap.P). */
+int ha_snapshot_tokens(const ha_snapshot* s, int* P);
+/* Position of the stored recurrent state (a multiple of 64 after chunked forwards, P after sequential ones) and
+   the number of raw rows kept for replay and conv history, [state_pos - (conv_k-1), P). */
+int ha_snapshot_layout(const ha_snapshot* s, int* state_pos, int* tail_rows);
+/* Copy one part of a snapshot to host memory: "state" f32 [batch][H][DK][DV] (linear layer), "tail" rows
+   [batch][tail_rows][lin_stride] in lin_dtype (linear), "K" / "V" f16 [batch][HK][P][HD] (full). */
+int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* host, size_t bytes);
+/* Free the snapshot's device memory (snapshot.release(), engine.js:361). Idempotent. */
+int ha_snapshot_release(ha_snapshot* s);
+/* Release (if needed) and free the handle itself. */
+int ha_snapshot_destroy(ha_snapshot* s);
+
+/* Device memory helpers for callers without their own HIP allocator (the Node binding). */
+int ha_device_alloc(ha_engine* e, size_t bytes, void** dptr);
+int ha_device_free(ha_engine* e, void* dptr);
+int ha_copy_to_device(ha_engine* e, void* dst, const void* host, size_t bytes);
+int ha_copy_to_host(ha_engine* e, void* host, const void* src, size_t bytes);
+int ha_synchronize(ha_engine* e);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HA_H */

@@ -1,0 +1,510 @@
+// Host side of the MI355X hybrid-attention engine: the C ABI declared in include/ha.h.
+//
+// Mirrors the reference engine's host logic for the token mixers (web/public/engine/engine.js):
+//   constructor buffers (engine.js:89-107)        -> ha_create: per-layer state, raw-row tail, K/V cache, RoPE table
+//   plan() linear / full branches (253-276)       -> ha_forward: layer-kind dispatch, one stream, layers in order
+//   forward() resume (325-328)                    -> the snapshot's state / tail feed the kernels; K/V rows copied
+//   forward() snapshot (349-362)                  -> ha_forward(keep): new device buffers sized to the context
+//   context guard (316), missing tensor (177)     -> HA_ERR_CONTEXT, HA_ERR_PARAM
+//
+// Gated-delta layers keep, instead of the reference's 3-row conv history, the raw rows from 3 before the stored
+// state position up to P. The stored state sits at the last chunk boundary (chunked forwards) so that a resumed
+// call replays the rows of the open chunk with exactly the arithmetic a single full forward would use; this makes
+// prefix + suffix bit-identical to one forward for any split.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ha.h"
+#include "ha_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HA_HIP(expr)                                                                          \
+  do {                                                                                        \
+    hipError_t e_ = (expr);                                                                   \
+    if (e_ != hipSuccess) return fail(HA_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr uint32_t kEngineMagic = 0x4841454eu, kSnapMagic = 0x48415350u, kDeadMagic = 0xdeadbeefu;
+constexpr int kKC = 4;                          // conv kernel the kernels are built for
+constexpr int kTailCap = ha::kChunk - 1 + kKC;  // at most 63 open rows + 3 history rows (+1 spare)
+std::atomic<uint64_t> g_engine_ids{1};
+
+struct Layer {
+  int kind = 0;
+  float* conv = nullptr;
+  float* negA = nullptr;
+  float* dtb = nullptr;
+  float* gnorm = nullptr;
+  float* qn = nullptr;
+  float* kn = nullptr;
+  float* S = nullptr;     // [B][H][DK][DV] working state
+  void* tail = nullptr;   // [B][kTailCap][lin_stride] working raw-row tail
+  _Float16* K = nullptr;  // [B][HK][LT][HD]
+  _Float16* V = nullptr;
+};
+
+size_t dtype_size(int dt) { return dt == HA_F16 ? 2 : 4; }
+
+}  // namespace
+
+struct ha_engine {
+  uint32_t magic = kEngineMagic;
+  uint64_t id = 0;
+  ha_config cfg{};
+  std::vector<unsigned char> kinds;
+  int device = 0;
+  hipStream_t own = nullptr, stream = nullptr;
+  std::vector<Layer> layers;
+  float* rope = nullptr;
+  void* zero_tail = nullptr;  // [B][3][lin_stride] zeros: the history of an empty context
+  _Float16* Q = nullptr;      // [B][HQ][max_ctx][HD] prepared queries
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  std::vector<hipEvent_t> lev;
+  int C = 0;
+  bool any_linear = false, any_full = false;
+};
+
+struct ha_snapshot {
+  uint32_t magic = kSnapMagic;
+  const ha_engine* owner = nullptr;
+  uint64_t owner_id = 0;
+  int P = 0, s0 = 0, tail_rows = 0;
+  bool released = false;
+  struct Part {
+    float* S = nullptr;
+    void* tail = nullptr;
+    _Float16* K = nullptr;
+    _Float16* V = nullptr;
+  };
+  std::vector<Part> layers;
+};
+
+namespace {
+
+bool engine_ok(const ha_engine* e) { return e && e->magic == kEngineMagic; }
+
+int check_config(const ha_config* c) {
+  if (!c) return fail(HA_ERR_ARG, "config is NULL");
+  if (c->n_layers <= 0 || !c->layer_kind) return fail(HA_ERR_ARG, "n_layers must be > 0 with a layer_kind array");
+  if (c->batch <= 0 || c->max_ctx <= 0) return fail(HA_ERR_ARG, "batch and max_ctx must be > 0");
+  if (std::fabs(c->eps - 1e-6f) > 1e-12f) return fail(HA_ERR_ARG, "eps must be 1e-6 (the value the kernels use)");
+  bool lin = false, full = false;
+  for (int i = 0; i < c->n_layers; i++) {
+    if (c->layer_kind[i] == HA_LINEAR_ATTENTION) lin = true;
+    else if (c->layer_kind[i] == HA_FULL_ATTENTION) full = true;
+    else return fail(HA_ERR_ARG, "layer " + std::to_string(i) + ": unknown layer kind " + std::to_string(c->layer_kind[i]));
+  }
+  if (lin) {
+    if (c->H <= 0 || c->DK != 128 || c->DV != 128 || c->conv_k != kKC)
+      return fail(HA_ERR_ARG, "linear_attention layers need d_k = d_v = 128, conv kernel 4 and H > 0");
+    const int C = 2 * c->H * c->DK + c->H * c->DV;
+    if (c->lin_stride < C + c->H * c->DV + 2 * c->H)
+      return fail(HA_ERR_ARG, "lin_stride smaller than the fused row qkv | z | a | b");
+    if (c->lin_dtype != HA_F32 && c->lin_dtype != HA_F16) return fail(HA_ERR_ARG, "lin_dtype must be HA_F32 or HA_F16");
+  }
+  if (full) {
+    if (c->HD != 256 || c->HK <= 0 || c->HQ <= 0 || c->HQ % c->HK || c->HQ / c->HK != 4)
+      return fail(HA_ERR_ARG, "full_attention layers need head_dim 256 and 4 query heads per KV head");
+    if (c->rot_dim <= 0 || c->rot_dim > 64 || (c->rot_dim & (c->rot_dim - 1)) || c->rot_dim < 2)
+      return fail(HA_ERR_ARG, "rotary_dim must be a power of two in [2, 64]");
+    if (c->full_stride < c->HQ * 2 * c->HD + 2 * c->HK * c->HD)
+      return fail(HA_ERR_ARG, "full_stride smaller than the fused row [q|gate] x HQ | k | v");
+    if (c->full_dtype != HA_F32 && c->full_dtype != HA_F16) return fail(HA_ERR_ARG, "full_dtype must be HA_F32 or HA_F16");
+    if (!(c->rope_theta > 0.0f)) return fail(HA_ERR_ARG, "rope_theta must be > 0");
+  }
+  return HA_OK;
+}
+
+template <typename T>
+int dalloc(T** p, size_t bytes) {
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(p), bytes ? bytes : 16);
+  if (e != hipSuccess) { *p = nullptr; return fail(HA_ERR_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e)); }
+  return HA_OK;
+}
+
+int fill_f32(float* d, size_t n, float v) {
+  std::vector<float> h(n, v);
+  HA_HIP(hipMemcpy(d, h.data(), n * sizeof(float), hipMemcpyHostToDevice));
+  return HA_OK;
+}
+
+void free_engine(ha_engine* e) {
+  if (!e) return;
+  (void)hipSetDevice(e->device);
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  for (auto& l : e->layers) {
+    for (void* p : {(void*)l.conv, (void*)l.negA, (void*)l.dtb, (void*)l.gnorm, (void*)l.qn, (void*)l.kn, (void*)l.S,
+                    l.tail, (void*)l.K, (void*)l.V})
+      if (p) (void)hipFree(p);
+  }
+  if (e->rope) (void)hipFree(e->rope);
+  if (e->zero_tail) (void)hipFree(e->zero_tail);
+  if (e->Q) (void)hipFree(e->Q);
+  for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
+  for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
+  if (e->own) (void)hipStreamDestroy(e->own);
+  e->magic = kDeadMagic;
+  delete e;
+}
+
+void free_snapshot_buffers(ha_snapshot* s) {
+  for (auto& p : s->layers) {
+    for (void* q : {(void*)p.S, p.tail, (void*)p.K, (void*)p.V})
+      if (q) (void)hipFree(q);
+    p = ha_snapshot::Part{};
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ha_last_error(void) { return g_err.c_str(); }
+int ha_abi_version(void) { return HA_ABI_VERSION; }
+
+int ha_create(const ha_config* cfg, int device, ha_engine** out) {
+  if (!out) return fail(HA_ERR_ARG, "out is NULL");
+  *out = nullptr;
+  int rc = check_config(cfg);
+  if (rc) return rc;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(HA_ERR_DEVICE, "no HIP device is visible");
+  if (device < 0 || device >= ndev) return fail(HA_ERR_ARG, "device index out of range");
+  HA_HIP(hipSetDevice(device));
+
+  ha_engine* e = new ha_engine();
+  e->id = g_engine_ids.fetch_add(1);
+  e->cfg = *cfg;
+  e->kinds.assign(cfg->layer_kind, cfg->layer_kind + cfg->n_layers);
+  e->cfg.layer_kind = e->kinds.data();
+  e->device = device;
+  const ha_config& c = e->cfg;
+  const size_t B = c.batch;
+  auto bail = [&](int code) { free_engine(e); return code; };
+
+  if (hipStreamCreateWithFlags(&e->own, hipStreamNonBlocking) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipStreamCreate failed"));
+  e->stream = e->own;
+  if (hipEventCreate(&e->ev[0]) != hipSuccess || hipEventCreate(&e->ev[1]) != hipSuccess)
+    return bail(fail(HA_ERR_DEVICE, "hipEventCreate failed"));
+  e->lev.assign(c.n_layers + 1, nullptr);
+  for (auto& ev : e->lev)
+    if (hipEventCreate(&ev) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipEventCreate failed"));
+
+  e->layers.resize(c.n_layers);
+  for (int i = 0; i < c.n_layers; i++) {
+    Layer& l = e->layers[i];
+    l.kind = c.layer_kind[i];
+    if (l.kind == HA_LINEAR_ATTENTION) {
+      e->any_linear = true;
+      e->C = 2 * c.H * c.DK + c.H * c.DV;
+      const size_t esz = dtype_size(c.lin_dtype);
+      if ((rc = dalloc(&l.conv, sizeof(float) * e->C * kKC)) || (rc = dalloc(&l.negA, sizeof(float) * c.H)) ||
+          (rc = dalloc(&l.dtb, sizeof(float) * c.H)) || (rc = dalloc(&l.gnorm, sizeof(float) * c.DV)) ||
+          (rc = dalloc(&l.S, sizeof(float) * B * c.H * c.DK * c.DV)) ||
+          (rc = dalloc(&l.tail, esz * B * kTailCap * c.lin_stride)))
+        return bail(rc);
+      if (hipMemset(l.conv, 0, sizeof(float) * e->C * kKC) != hipSuccess || hipMemset(l.negA, 0, sizeof(float) * c.H) != hipSuccess ||
+          hipMemset(l.dtb, 0, sizeof(float) * c.H) != hipSuccess || hipMemset(l.tail, 0, esz * B * kTailCap * c.lin_stride) != hipSuccess)
+        return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
+      if ((rc = fill_f32(l.gnorm, c.DV, 1.0f))) return bail(rc);
+    } else {
+      e->any_full = true;
+      const size_t kv = B * c.HK * (size_t)c.max_ctx * c.HD;
+      if ((rc = dalloc(&l.qn, sizeof(float) * c.HD)) || (rc = dalloc(&l.kn, sizeof(float) * c.HD)) ||
+          (rc = dalloc(&l.K, sizeof(_Float16) * kv)) || (rc = dalloc(&l.V, sizeof(_Float16) * kv)))
+        return bail(rc);
+      if ((rc = fill_f32(l.qn, c.HD, 1.0f)) || (rc = fill_f32(l.kn, c.HD, 1.0f))) return bail(rc);
+      if (hipMemset(l.K, 0, sizeof(_Float16) * kv) != hipSuccess || hipMemset(l.V, 0, sizeof(_Float16) * kv) != hipSuccess)
+        return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
+    }
+  }
+  if (e->any_linear) {
+    const size_t bytes = dtype_size(c.lin_dtype) * B * (kKC - 1) * c.lin_stride;
+    if ((rc = dalloc(&e->zero_tail, bytes))) return bail(rc);
+    if (hipMemset(e->zero_tail, 0, bytes) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
+  }
+  if (e->any_full) {
+    // RoPE table as engine.js:105-106 builds it: angle t / theta^(2i/RD) in f64, stored as f32 (cos, sin)
+    const int RD = c.rot_dim;
+    std::vector<float> rope((size_t)c.max_ctx * RD);
+    for (int t = 0; t < c.max_ctx; t++)
+      for (int i = 0; i < RD / 2; i++) {
+        const double a = (double)t / std::pow((double)c.rope_theta, (2.0 * i) / RD);
+        rope[(size_t)t * RD + 2 * i] = (float)std::cos(a);
+        rope[(size_t)t * RD + 2 * i + 1] = (float)std::sin(a);
+      }
+    if ((rc = dalloc(&e->rope, rope.size() * sizeof(float)))) return bail(rc);
+    if (hipMemcpy(e->rope, rope.data(), rope.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+      return bail(fail(HA_ERR_DEVICE, "hipMemcpy rope failed"));
+    if ((rc = dalloc(&e->Q, sizeof(_Float16) * B * c.HQ * (size_t)c.max_ctx * c.HD))) return bail(rc);
+  }
+  *out = e;
+  return HA_OK;
+}
+
+int ha_destroy(ha_engine* e) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  free_engine(e);
+  return HA_OK;
+}
+
+int ha_set_stream(ha_engine* e, void* stream) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  e->stream = stream ? static_cast<hipStream_t>(stream) : e->own;
+  return HA_OK;
+}
+
+int ha_set_param(ha_engine* e, int layer, const char* name, const float* host, size_t count) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  if (!name || !host) return fail(HA_ERR_ARG, "name and data must be non-NULL");
+  if (layer < 0 || layer >= e->cfg.n_layers) return fail(HA_ERR_ARG, "layer index out of range");
+  const ha_config& c = e->cfg;
+  Layer& l = e->layers[layer];
+  float* dst = nullptr;
+  size_t want = 0;
+  const std::string n(name);
+  if (l.kind == HA_LINEAR_ATTENTION) {
+    if (n == "conv") { dst = l.conv; want = (size_t)e->C * kKC; }
+    else if (n == "neg_exp_A") { dst = l.negA; want = c.H; }
+    else if (n == "dt_bias") { dst = l.dtb; want = c.H; }
+    else if (n == "gnorm") { dst = l.gnorm; want = c.DV; }
+  } else {
+    if (n == "q_norm") { dst = l.qn; want = c.HD; }
+    else if (n == "k_norm") { dst = l.kn; want = c.HD; }
+  }
+  if (!dst) return fail(HA_ERR_PARAM, "no tensor layers." + std::to_string(layer) + "." + n + " for this layer kind");
+  if (count != want)
+    return fail(HA_ERR_PARAM, "layers." + std::to_string(layer) + "." + n + ": expected " + std::to_string(want) +
+                                  " floats, got " + std::to_string(count));
+  HA_HIP(hipSetDevice(e->device));
+  HA_HIP(hipMemcpy(dst, host, want * sizeof(float), hipMemcpyHostToDevice));
+  return HA_OK;
+}
+
+int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* layer_out, const ha_snapshot* resume,
+               ha_snapshot** keep, ha_forward_opts* opts) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  if (keep) *keep = nullptr;
+  const ha_config& c = e->cfg;
+  if (L <= 0) return fail(HA_ERR_ARG, "L must be > 0");
+  if (!layer_in || !layer_out) return fail(HA_ERR_ARG, "layer_in and layer_out must be non-NULL");
+  for (int i = 0; i < c.n_layers; i++)
+    if (!layer_in[i] || !layer_out[i]) return fail(HA_ERR_ARG, "layer " + std::to_string(i) + ": NULL input or output");
+  if (resume) {
+    if (resume->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+    if (resume->owner != e || resume->owner_id != e->id) return fail(HA_ERR_HANDLE, "snapshot belongs to another engine");
+    if (resume->released) return fail(HA_ERR_HANDLE, "snapshot was released");
+    if ((int)resume->layers.size() != c.n_layers) return fail(HA_ERR_HANDLE, "snapshot layer count mismatch");
+  }
+  const int P = resume ? resume->P : 0;
+  const int s0 = resume ? resume->s0 : 0;
+  if ((long)P + L > c.max_ctx)
+    return fail(HA_ERR_CONTEXT, "context " + std::to_string((long)P + L) + " exceeds " + std::to_string(c.max_ctx));
+  const int mode = opts ? opts->recurrence : HA_CHUNKED;
+  if (mode != HA_CHUNKED && mode != HA_SEQUENTIAL) return fail(HA_ERR_ARG, "unknown recurrence mode");
+  const bool timing = opts && (opts->timestamps || opts->layer_ms);
+  HA_HIP(hipSetDevice(e->device));
+  hipStream_t st = e->stream;
+  const size_t B = c.batch;
+
+  // resume: K/V rows [0, P) back into the working caches (engine.js:327); state and tail are read in place
+  if (resume && P > 0)
+    for (int i = 0; i < c.n_layers; i++)
+      if (e->layers[i].kind == HA_FULL_ATTENTION) {
+        const size_t w = (size_t)P * c.HD * sizeof(_Float16), dp = (size_t)c.max_ctx * c.HD * sizeof(_Float16);
+        HA_HIP(hipMemcpy2DAsync(e->layers[i].K, dp, resume->layers[i].K, w, w, B * c.HK, hipMemcpyDeviceToDevice, st));
+        HA_HIP(hipMemcpy2DAsync(e->layers[i].V, dp, resume->layers[i].V, w, w, B * c.HK, hipMemcpyDeviceToDevice, st));
+      }
+
+  const int end = P + L;
+  const int s1 = mode == HA_CHUNKED ? s0 + ha::kChunk * ((end - s0) / ha::kChunk) : end;  // new state position
+  if (timing) HA_HIP(hipEventRecord(e->ev[0], st));
+  for (int i = 0; i < c.n_layers; i++) {
+    Layer& l = e->layers[i];
+    if (opts && opts->layer_ms) HA_HIP(hipEventRecord(e->lev[i], st));
+    if (l.kind == HA_LINEAR_ATTENTION) {
+      ha::GdnArgs a{};
+      a.B = c.batch; a.H = c.H; a.DK = c.DK; a.DV = c.DV; a.KC = kKC; a.stride = c.lin_stride; a.C = e->C;
+      a.P = P; a.L = L; a.s0 = s0;
+      a.tail = resume ? resume->layers[i].tail : e->zero_tail;
+      a.tail_cap = resume ? resume->tail_rows : kKC - 1;
+      a.dtype = c.lin_dtype == HA_F16 ? 1 : 0;
+      a.in = layer_in[i]; a.out = layer_out[i];
+      a.S_in = resume ? resume->layers[i].S : nullptr; a.S_out = l.S;
+      a.conv_w = l.conv; a.negA = l.negA; a.dtb = l.dtb; a.gnorm = c.lin_gnorm ? l.gnorm : nullptr;
+      hipError_t he = mode == HA_CHUNKED ? ha::launch_gdn_chunked(a, st) : ha::launch_gdn_sequential(a, st);
+      if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " gated-delta launch: " + hipGetErrorString(he));
+      ha::TailArgs t{};
+      t.B = c.batch; t.stride = c.lin_stride; t.C = e->C; t.ab_off = e->C + c.H * c.DV; t.ab_n = 2 * c.H;
+      t.P = P; t.L = L; t.s0 = s0; t.KC = kKC; t.tail_cap_in = a.tail_cap; t.tail_cap_out = kTailCap;
+      t.dst_first = s1 - (kKC - 1); t.dtype = a.dtype; t.in = a.in; t.tail = a.tail; t.tail_out = l.tail;
+      he = ha::launch_tail_update(t, st);
+      if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " tail update: " + hipGetErrorString(he));
+    } else {
+      ha::GqaArgs a{};
+      a.B = c.batch; a.HQ = c.HQ; a.HK = c.HK; a.HD = c.HD; a.RD = c.rot_dim; a.stride = c.full_stride; a.LT = c.max_ctx;
+      a.P = P; a.L = L; a.dtype = c.full_dtype == HA_F16 ? 1 : 0;
+      a.in = layer_in[i]; a.out = layer_out[i]; a.qw = l.qn; a.kw = l.kn; a.rope = e->rope;
+      a.Q = e->Q; a.K = l.K; a.V = l.V;
+      hipError_t he = ha::launch_gqa(a, st);
+      if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " attention launch: " + hipGetErrorString(he));
+    }
+  }
+  if (opts && opts->layer_ms) HA_HIP(hipEventRecord(e->lev[c.n_layers], st));
+  if (timing) HA_HIP(hipEventRecord(e->ev[1], st));
+
+  if (keep) {
+    ha_snapshot* s = new ha_snapshot();
+    s->owner = e; s->owner_id = e->id; s->P = end; s->s0 = e->any_linear ? s1 : end;
+    s->tail_rows = s->P - (s->s0 - (kKC - 1));
+    s->layers.resize(c.n_layers);
+    auto bail = [&](int code) { (void)hipStreamSynchronize(st); free_snapshot_buffers(s); s->magic = kDeadMagic; delete s; return code; };
+    for (int i = 0; i < c.n_layers; i++) {
+      Layer& l = e->layers[i];
+      ha_snapshot::Part& p = s->layers[i];
+      int rc = HA_OK;
+      if (l.kind == HA_LINEAR_ATTENTION) {
+        const size_t sb = sizeof(float) * B * c.H * c.DK * c.DV, esz = dtype_size(c.lin_dtype);
+        const size_t rowb = esz * c.lin_stride;
+        if ((rc = dalloc(&p.S, sb)) || (rc = dalloc(&p.tail, rowb * B * s->tail_rows))) return bail(rc);
+        if (hipMemcpyAsync(p.S, l.S, sb, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipMemcpy2DAsync(p.tail, rowb * s->tail_rows, l.tail, rowb * kTailCap, rowb * s->tail_rows, B,
+                             hipMemcpyDeviceToDevice, st) != hipSuccess)
+          return bail(fail(HA_ERR_DEVICE, "snapshot copy failed"));
+      } else {
+        const size_t w = (size_t)end * c.HD * sizeof(_Float16), sp = (size_t)c.max_ctx * c.HD * sizeof(_Float16);
+        if ((rc = dalloc(&p.K, w * B * c.HK)) || (rc = dalloc(&p.V, w * B * c.HK))) return bail(rc);
+        if (hipMemcpy2DAsync(p.K, w, l.K, sp, w, B * c.HK, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipMemcpy2DAsync(p.V, w, l.V, sp, w, B * c.HK, hipMemcpyDeviceToDevice, st) != hipSuccess)
+          return bail(fail(HA_ERR_DEVICE, "snapshot copy failed"));
+      }
+    }
+    *keep = s;
+  }
+  if (timing || (opts && opts->sync)) {
+    HA_HIP(hipStreamSynchronize(st));
+    if (opts && opts->timestamps) HA_HIP(hipEventElapsedTime(&opts->gpu_ms, e->ev[0], e->ev[1]));
+    if (opts && opts->layer_ms)
+      for (int i = 0; i < c.n_layers; i++) HA_HIP(hipEventElapsedTime(&opts->layer_ms[i], e->lev[i], e->lev[i + 1]));
+  }
+  hipError_t le = hipGetLastError();
+  if (le != hipSuccess) return fail(HA_ERR_DEVICE, std::string("device error: ") + hipGetErrorString(le));
+  return HA_OK;
+}
+
+int ha_snapshot_tokens(const ha_snapshot* s, int* P) {
+  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (!P) return fail(HA_ERR_ARG, "P is NULL");
+  *P = s->P;
+  return HA_OK;
+}
+
+int ha_snapshot_layout(const ha_snapshot* s, int* state_pos, int* tail_rows) {
+  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (state_pos) *state_pos = s->s0;
+  if (tail_rows) *tail_rows = s->tail_rows;
+  return HA_OK;
+}
+
+int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* host, size_t bytes) {
+  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (s->released) return fail(HA_ERR_HANDLE, "snapshot was released");
+  if (!what || !host) return fail(HA_ERR_ARG, "what and host must be non-NULL");
+  const ha_engine* e = s->owner;
+  if (!engine_ok(e) || e->id != s->owner_id) return fail(HA_ERR_HANDLE, "the snapshot's engine was destroyed");
+  if (layer < 0 || layer >= (int)s->layers.size()) return fail(HA_ERR_ARG, "layer index out of range");
+  const ha_config& c = e->cfg;
+  const size_t B = c.batch;
+  const std::string w(what);
+  const void* src = nullptr;
+  size_t want = 0;
+  const bool lin = e->layers[layer].kind == HA_LINEAR_ATTENTION;
+  if (lin && w == "state") { src = s->layers[layer].S; want = sizeof(float) * B * c.H * c.DK * c.DV; }
+  else if (lin && w == "tail") { src = s->layers[layer].tail; want = dtype_size(c.lin_dtype) * B * s->tail_rows * c.lin_stride; }
+  else if (!lin && (w == "K" || w == "V")) {
+    src = w == "K" ? (const void*)s->layers[layer].K : (const void*)s->layers[layer].V;
+    want = sizeof(_Float16) * B * c.HK * (size_t)s->P * c.HD;
+  } else return fail(HA_ERR_PARAM, "no part '" + w + "' for this layer kind");
+  if (bytes != want) return fail(HA_ERR_ARG, "expected " + std::to_string(want) + " bytes, got " + std::to_string(bytes));
+  HA_HIP(hipSetDevice(e->device));
+  HA_HIP(hipMemcpyAsync(host, src, want, hipMemcpyDeviceToHost, e->stream));
+  HA_HIP(hipStreamSynchronize(e->stream));
+  return HA_OK;
+}
+
+int ha_snapshot_release(ha_snapshot* s) {
+  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (s->released) return HA_OK;
+  const ha_engine* e = s->owner;
+  if (engine_ok(e) && e->id == s->owner_id) {
+    (void)hipSetDevice(e->device);
+    (void)hipStreamSynchronize(e->stream);  // the snapshot's copies may still be in flight
+  }
+  free_snapshot_buffers(s);
+  s->released = true;
+  return HA_OK;
+}
+
+int ha_snapshot_destroy(ha_snapshot* s) {
+  int rc = ha_snapshot_release(s);
+  if (rc) return rc;
+  s->magic = kDeadMagic;
+  delete s;
+  return HA_OK;
+}
+
+int ha_device_alloc(ha_engine* e, size_t bytes, void** dptr) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  if (!dptr) return fail(HA_ERR_ARG, "dptr is NULL");
+  HA_HIP(hipSetDevice(e->device));
+  return dalloc(dptr, bytes);
+}
+
+int ha_device_free(ha_engine* e, void* dptr) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  HA_HIP(hipSetDevice(e->device));
+  HA_HIP(hipStreamSynchronize(e->stream));
+  if (dptr) HA_HIP(hipFree(dptr));
+  return HA_OK;
+}
+
+int ha_copy_to_device(ha_engine* e, void* dst, const void* host, size_t bytes) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  if (!dst || !host) return fail(HA_ERR_ARG, "NULL pointer");
+  HA_HIP(hipSetDevice(e->device));
+  HA_HIP(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, e->stream));
+  HA_HIP(hipStreamSynchronize(e->stream));
+  return HA_OK;
+}
+
+int ha_copy_to_host(ha_engine* e, void* host, const void* src, size_t bytes) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  if (!src || !host) return fail(HA_ERR_ARG, "NULL pointer");
+  HA_HIP(hipSetDevice(e->device));
+  HA_HIP(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, e->stream));
+  HA_HIP(hipStreamSynchronize(e->stream));
+  return HA_OK;
+}
+
+int ha_synchronize(ha_engine* e) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  HA_HIP(hipSetDevice(e->device));
+  HA_HIP(hipStreamSynchronize(e->stream));
+  return HA_OK;
+}
+
+}  // extern "C"

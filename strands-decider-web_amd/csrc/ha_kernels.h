@@ -1,0 +1,61 @@
+// Kernel argument blocks and launchers shared by the engine host code and the HIP kernels (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace ha {
+
+// One gated-delta layer over absolute rows [s0, P + L) of `B` sequences.
+// Rows r < P come from `tail` (raw rows kept by the previous call: [s0 - (KC-1), P)), rows >= P from `in`.
+// The conv of row r reads rows r-3..r, so rows s0-3..s0-1 must be present in `tail` (zeros at the start of a
+// sequence). Rows below P are replayed (state only, no output).
+struct GdnArgs {
+  int B, H, DK, DV, KC, stride, C;  // C = 2*H*DK + H*DV; a at C + H*DV, b at C + H*DV + H, z at C
+  int P, L, s0;                     // state position, cached rows, new rows
+  int tail_cap;                     // rows per sequence in `tail`
+  int dtype;                        // 0 f32 rows/out, 1 f16
+  const void* in;                   // [B][L][stride]
+  const void* tail;                 // [B][tail_cap][stride]
+  void* out;                        // [B][L][H*DV]
+  const float* S_in;                // [B][H][DK][DV] state at s0, or nullptr for a zero state
+  float* S_out;                     // [B][H][DK][DV] state at the returned position (may equal S_in)
+  const float* conv_w;              // [C][KC]
+  const float* negA;                // [H]
+  const float* dtb;                 // [H]
+  const float* gnorm;               // [DV], or nullptr to output the raw core output
+};
+
+// Full-attention prep (q/k RMSNorm, partial RoPE, K/V cache write) and attention for rows [P, P + L).
+struct GqaArgs {
+  int B, HQ, HK, HD, RD, stride, LT;
+  int P, L;
+  int dtype;                 // rows / out dtype: 0 f32, 1 f16
+  const void* in;            // [B][L][stride]
+  void* out;                 // [B][L][HQ*HD]
+  const float* qw;           // [HD] stored (1 + w)
+  const float* kw;           // [HD]
+  const float* rope;         // [LT][RD] cos/sin pairs
+  _Float16* Q;               // [B][HQ][L][HD] scratch: prepared q times HD^-1/2, f16
+  _Float16* K;               // [B][HK][LT][HD] cache
+  _Float16* V;               // [B][HK][LT][HD] cache
+};
+
+// Copy the raw rows [dst_first, P + L) (dst_first >= s0 - (KC-1)) of every sequence from (tail, in) into
+// `tail_out` ([B][tail_cap][stride]); only the conv channels [0, C) and the a/b columns are kept.
+struct TailArgs {
+  int B, stride, C, ab_off, ab_n;
+  int P, L, s0, KC, tail_cap_in, tail_cap_out, dst_first, dtype;
+  const void* in;
+  const void* tail;
+  void* tail_out;
+};
+
+hipError_t launch_gdn_sequential(const GdnArgs& a, hipStream_t s);
+hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t s);
+hipError_t launch_gqa(const GqaArgs& a, hipStream_t s);
+hipError_t launch_tail_update(const TailArgs& a, hipStream_t s);
+
+constexpr int kChunk = 64;  // gated-delta chunk length; chunk boundaries sit at s0 + 64k
+
+}  // namespace ha

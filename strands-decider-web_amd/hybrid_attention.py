@@ -1,0 +1,205 @@
+"""Python binding of the MI355X hybrid-attention engine (libha.so, C ABI in include/ha.h).
+
+This mirrors the reference engine's host API for the token-mixer path (web/public/engine/engine.js):
+``Engine(...)`` plays ``Engine.create`` / the constructor (engine.js:63-111), ``Engine.forward`` takes the
+reference's option names ``cache`` / ``keep_cache`` / ``timestamps`` (engine.js:313) and returns a dict with
+``cache`` (a :class:`Snapshot`, engine.js:349-362) and ``gpu_ms``; ``Snapshot.release()`` is engine.js:361.
+Errors raise :class:`HAError`, as the reference throws ``Error``.
+
+Tensors handed to :meth:`Engine.forward` are device buffers: any object with ``data_ptr()`` (a torch tensor on
+the GPU) or a raw device address as ``int``. There is no CPU path: loading fails loudly if libha.so is missing.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libha.so")
+
+HA_OK, HA_ERR_ARG, HA_ERR_CONTEXT, HA_ERR_HANDLE, HA_ERR_DEVICE, HA_ERR_NOMEM, HA_ERR_PARAM = 0, -1, -2, -3, -4, -5, -6
+LINEAR, FULL = 0, 1
+F32, F16 = 0, 1
+CHUNKED, SEQUENTIAL = 0, 1
+KIND_NAMES = {"linear_attention": LINEAR, "full_attention": FULL}
+
+
+class HAError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("%s (ha status %d)" % (msg, code))
+        self.code = code
+
+
+class HaConfig(ctypes.Structure):
+    _fields_ = [("n_layers", ctypes.c_int), ("layer_kind", ctypes.POINTER(ctypes.c_ubyte)),
+                ("batch", ctypes.c_int), ("max_ctx", ctypes.c_int),
+                ("H", ctypes.c_int), ("DK", ctypes.c_int), ("DV", ctypes.c_int), ("conv_k", ctypes.c_int),
+                ("lin_stride", ctypes.c_int), ("lin_dtype", ctypes.c_int), ("lin_gnorm", ctypes.c_int),
+                ("HQ", ctypes.c_int), ("HK", ctypes.c_int), ("HD", ctypes.c_int), ("rot_dim", ctypes.c_int),
+                ("full_stride", ctypes.c_int), ("full_dtype", ctypes.c_int),
+                ("rope_theta", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+class HaForwardOpts(ctypes.Structure):
+    _fields_ = [("recurrence", ctypes.c_int), ("timestamps", ctypes.c_int), ("sync", ctypes.c_int),
+                ("gpu_ms", ctypes.c_float), ("layer_ms", ctypes.POINTER(ctypes.c_float))]
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    """Load libha.so once; raise if it has not been built (there is no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError("libha.so is not built at %s; run __graft_entry__.build()" % path)
+    lib = ctypes.CDLL(path)
+    vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    sig = {
+        "ha_last_error": ([], ctypes.c_char_p),
+        "ha_abi_version": ([], i),
+        "ha_create": ([ctypes.POINTER(HaConfig), i, ctypes.POINTER(vp)], i),
+        "ha_destroy": ([vp], i),
+        "ha_set_stream": ([vp, vp], i),
+        "ha_set_param": ([vp, i, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), sz], i),
+        "ha_forward": ([vp, i, ctypes.POINTER(vp), ctypes.POINTER(vp), vp, ctypes.POINTER(vp),
+                        ctypes.POINTER(HaForwardOpts)], i),
+        "ha_snapshot_tokens": ([vp, ctypes.POINTER(i)], i),
+        "ha_snapshot_layout": ([vp, ctypes.POINTER(i), ctypes.POINTER(i)], i),
+        "ha_snapshot_read": ([vp, i, ctypes.c_char_p, vp, sz], i),
+        "ha_snapshot_release": ([vp], i),
+        "ha_snapshot_destroy": ([vp], i),
+        "ha_device_alloc": ([vp, sz, ctypes.POINTER(vp)], i),
+        "ha_device_free": ([vp, vp], i),
+        "ha_copy_to_device": ([vp, vp, vp, sz], i),
+        "ha_copy_to_host": ([vp, vp, vp, sz], i),
+        "ha_synchronize": ([vp], i),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = lib
+    return lib
+
+
+def _check(rc):
+    if rc != HA_OK:
+        raise HAError(rc, _lib.ha_last_error().decode())
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def model_config(layer_types, batch=1, max_ctx=4096, lin_dtype=F32, full_dtype=F16, lin_gnorm=True, **kw):
+    """Engine shape for the Qwen3.5-2B torso (the reference's manifest config, export_engine.py:83)."""
+    d = dict(H=16, DK=128, DV=128, conv_k=4, lin_stride=8256, HQ=8, HK=2, HD=256, rot_dim=64,
+             full_stride=5120, rope_theta=1e7, eps=1e-6)
+    d.update(kw)
+    kinds = [KIND_NAMES[k] if isinstance(k, str) else int(k) for k in layer_types]
+    return dict(kinds=kinds, batch=batch, max_ctx=max_ctx, lin_dtype=lin_dtype, full_dtype=full_dtype,
+                lin_gnorm=int(bool(lin_gnorm)), **d)
+
+
+class Snapshot:
+    """A prefix-cache snapshot (engine.js:352): ``P`` tokens of state, raw tail rows and K/V."""
+
+    def __init__(self, engine, handle):
+        self.engine = engine
+        self._h = ctypes.c_void_p(handle)
+        p = ctypes.c_int()
+        _check(_lib.ha_snapshot_tokens(self._h, ctypes.byref(p)))
+        self.P = p.value
+        sp, tr = ctypes.c_int(), ctypes.c_int()
+        _check(_lib.ha_snapshot_layout(self._h, ctypes.byref(sp), ctypes.byref(tr)))
+        self.state_pos, self.tail_rows = sp.value, tr.value
+
+    @property
+    def handle(self):
+        return self._h
+
+    def read(self, layer, what, out):
+        """Copy a part ("state", "tail", "K", "V") into the numpy array ``out`` (exact byte size)."""
+        _check(_lib.ha_snapshot_read(self._h, layer, what.encode(), out.ctypes.data, out.nbytes))
+        return out
+
+    def release(self):
+        _check(_lib.ha_snapshot_release(self._h))
+
+    def __del__(self):
+        try:
+            if self._h and _lib is not None:
+                _lib.ha_snapshot_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+class Engine:
+    """Hybrid-attention engine bound to one HIP device and stream (engine.js:61-111 facade)."""
+
+    def __init__(self, cfg, device=0, stream=None):
+        lib = load_library()
+        self.cfg = dict(cfg)
+        kinds = (ctypes.c_ubyte * len(cfg["kinds"]))(*cfg["kinds"])
+        self._kinds = kinds
+        c = HaConfig(n_layers=len(cfg["kinds"]), layer_kind=kinds, batch=cfg["batch"], max_ctx=cfg["max_ctx"],
+                     H=cfg["H"], DK=cfg["DK"], DV=cfg["DV"], conv_k=cfg["conv_k"], lin_stride=cfg["lin_stride"],
+                     lin_dtype=cfg["lin_dtype"], lin_gnorm=cfg["lin_gnorm"], HQ=cfg["HQ"], HK=cfg["HK"],
+                     HD=cfg["HD"], rot_dim=cfg["rot_dim"], full_stride=cfg["full_stride"],
+                     full_dtype=cfg["full_dtype"], rope_theta=cfg["rope_theta"], eps=cfg["eps"])
+        h = ctypes.c_void_p()
+        _check(lib.ha_create(ctypes.byref(c), device, ctypes.byref(h)))
+        self._h = h
+        self.n_layers = len(cfg["kinds"])
+        if stream is not None:
+            self.set_stream(stream)
+
+    def set_stream(self, stream):
+        _check(_lib.ha_set_stream(self._h, ctypes.c_void_p(stream) if stream else None))
+
+    def set_param(self, layer, name, values):
+        import numpy as np
+        a = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        _check(_lib.ha_set_param(self._h, layer, name.encode(), a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                 a.size))
+
+    def forward(self, L, layer_in, layer_out, cache=None, keep_cache=False, recurrence=CHUNKED, timestamps=False,
+                layer_ms=False, sync=False):
+        n = self.n_layers
+        ins = (ctypes.c_void_p * n)(*[_ptr(x) for x in layer_in])
+        outs = (ctypes.c_void_p * n)(*[_ptr(x) for x in layer_out])
+        lm = (ctypes.c_float * n)() if layer_ms else None
+        opts = HaForwardOpts(recurrence=recurrence, timestamps=int(timestamps), sync=int(sync), gpu_ms=0.0,
+                             layer_ms=lm)
+        keep = ctypes.c_void_p() if keep_cache else None
+        rc = _lib.ha_forward(self._h, L, ins, outs, cache.handle if cache is not None else None,
+                             ctypes.byref(keep) if keep_cache else None, ctypes.byref(opts))
+        _check(rc)
+        res = {"cache": Snapshot(self, keep.value) if keep_cache else None}
+        if timestamps:
+            res["gpu_ms"] = opts.gpu_ms
+        if layer_ms:
+            res["layer_ms"] = list(lm)
+        return res
+
+    def synchronize(self):
+        _check(_lib.ha_synchronize(self._h))
+
+    def close(self):
+        if self._h:
+            _check(_lib.ha_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            if self._h and _lib is not None:
+                _lib.ha_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass

@@ -1,0 +1,76 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol include/ha.h declares, and its host-side
+validation returns the documented status codes before touching a device (no compute without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import hybrid_attention as ha
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "ha.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(ha_[a-z_0-9]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ha.load_library()
+    names = _declared()
+    assert "ha_forward" in names and len(names) >= 17
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version_matches_header():
+    src = open(os.path.join(ROOT, "include", "ha.h")).read()
+    v = int(re.search(r"#define HA_ABI_VERSION (\d+)", src).group(1))
+    assert ha.load_library().ha_abi_version() == v
+
+
+def _cfg(**over):
+    c = ha.model_config(["linear_attention", "full_attention"])
+    c.update(over)
+    return c
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(kinds=[0, 7]), "unknown layer kind"),
+    (dict(batch=0), "batch"),
+    (dict(DK=64), "d_k = d_v = 128"),
+    (dict(conv_k=3), "conv kernel 4"),
+    (dict(lin_stride=8000), "lin_stride"),
+    (dict(HQ=6), "4 query heads per KV head"),
+    (dict(HD=128), "head_dim 256"),
+    (dict(rot_dim=48), "rotary_dim"),
+    (dict(full_stride=4096), "full_stride"),
+    (dict(eps=1e-5), "eps"),
+    (dict(lin_dtype=5), "lin_dtype"),
+])
+def test_create_rejects_bad_configs_before_touching_a_device(over, msg):
+    with pytest.raises(ha.HAError) as ei:
+        ha.Engine(_cfg(**over))
+    assert ei.value.code == ha.HA_ERR_ARG and msg in str(ei.value)
+
+
+def test_null_handles_are_rejected():
+    lib = ha.load_library()
+    assert lib.ha_destroy(None) == ha.HA_ERR_HANDLE
+    assert lib.ha_forward(None, 1, None, None, None, None, None) == ha.HA_ERR_HANDLE
+    p = ctypes.c_int()
+    assert lib.ha_snapshot_tokens(None, ctypes.byref(p)) == ha.HA_ERR_HANDLE
+    assert lib.ha_snapshot_release(None) == ha.HA_ERR_HANDLE
+    assert lib.ha_synchronize(None) == ha.HA_ERR_HANDLE
+    assert b"invalid" in lib.ha_last_error()
+
+
+def test_no_device_is_a_device_error_not_a_fallback():
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(ha.HAError) as ei:
+        ha.Engine(_cfg())
+    assert ei.value.code == ha.HA_ERR_DEVICE

@@ -1,0 +1,65 @@
+"""GPU parity of the gated GQA prep + MFMA attention kernels against the oracle (engine f16 storage points)."""
+import numpy as np
+import pytest
+
+import hybrid_attention as ha
+import synth
+from harness import Runner, oracle_gqa, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2  # north-star bar for fp16 MFMA attention
+
+
+def test_config1_T2048():
+    # T=2048, 8 q heads, 2 KV heads, head_dim 256, f16 rows ~N(0,1), RoPE 64 dims base 1e7,
+    # unit q/k norm gain, sigmoid gate
+    x = synth.gqa_rows(2048)
+    p = synth.gqa_params()
+    r = Runner(["full_attention"])
+    r.set_params(0, p)
+    (out,), _ = r.forward([x])
+    ref, _ = oracle_gqa(x, p, 4096)
+    e = rel_err(out, ref)
+    print("config1 T=2048 rel_err %.2e" % e)
+    assert e < TOL
+
+
+@pytest.mark.parametrize("T", [1, 31, 70, 257])
+def test_small_batches_with_norm_weights(T):
+    B = 2
+    x = synth.gqa_rows(T, B, seed=3)
+    p = synth.gqa_params(seed=3, noise=0.2)
+    r = Runner(["full_attention"], batch=B, max_ctx=512)
+    r.set_params(0, p)
+    (out,), snap = r.forward([x], keep=True)
+    ref, caches = oracle_gqa(x, p, 512)
+    e = rel_err(out, ref)
+    print("T=%d rel_err %.2e" % (T, e))
+    assert e < TOL
+    K = np.zeros((B, 2, T, 256), np.float16)
+    snap.read(0, "K", K)
+    for b in range(B):
+        assert rel_err(K[b].astype(np.float32), caches[b].K[:, :T]) < 2e-3
+
+
+def test_f32_rows():
+    x = synth.gqa_rows(100, 1, seed=4).astype(np.float32)
+    p = synth.gqa_params(seed=4, noise=0.1)
+    r = Runner(["full_attention"], full_dtype=ha.F32, max_ctx=256)
+    r.set_params(0, p)
+    (out,), _ = r.forward([x])
+    ref, _ = oracle_gqa(x, p, 256)
+    assert rel_err(out, ref) < TOL
+
+
+@pytest.mark.parametrize("P,L", [(100, 30), (64, 64), (1, 1), (33, 200)])
+def test_prefix_suffix_bit_exact(P, L):
+    x = synth.gqa_rows(P + L, 2, seed=5)
+    p = synth.gqa_params(seed=5, noise=0.1)
+    r = Runner(["full_attention"], batch=2, max_ctx=1024)
+    r.set_params(0, p)
+    (full,), _ = r.forward([x])
+    (pre,), snap = r.forward([x[:, :P]], keep=True)
+    (suf,), _ = r.forward([x[:, P:]], cache=snap)
+    np.testing.assert_array_equal(pre, full[:, :P])
+    np.testing.assert_array_equal(suf, full[:, P:])
