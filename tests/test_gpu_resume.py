@@ -1,0 +1,80 @@
+"""BASELINE config 3 on the GPU: a 1,536-token prefix through 3 gated-delta layers + 1 GQA layer, snapshot, then
+5 independent 64-token suffixes resumed from it; each must equal the last 64 rows of a full 1,600-token forward
+bit for bit (the reference claims the same for its engine, README.md:60-61). Also the failure paths of the
+snapshot boundary (engine.js:316 context guard, released / foreign handles)."""
+import numpy as np
+import pytest
+
+import hybrid_attention as ha
+import synth
+from harness import Runner, oracle_gdn, oracle_gqa, rel_err
+
+pytestmark = pytest.mark.gpu
+KINDS = ["linear_attention", "linear_attention", "linear_attention", "full_attention"]
+
+
+def _inputs(T, part, seed=3):
+    return [synth.gdn_rows(T, seed=seed, layer=i, part=part) if k == "linear_attention"
+            else synth.gqa_rows(T, seed=seed, layer=i, part=part) for i, k in enumerate(KINDS)]
+
+
+def _runner(recurrence_mode=None):
+    r = Runner(KINDS)
+    for i, k in enumerate(KINDS):
+        r.set_params(i, synth.gdn_params(seed=3, layer=i) if k == "linear_attention"
+                     else synth.gqa_params(seed=3, layer=i, noise=0.1))
+    return r
+
+
+def test_config3_prefix_cache_bit_exact():
+    r = _runner()
+    prefix = _inputs(1536, part=0)
+    _, snap = r.forward(prefix, keep=True)
+    assert snap.P == 1536 and snap.state_pos == 1536
+    for s in range(5):
+        suffix = _inputs(64, part=1 + s)
+        outs, _ = r.forward(suffix, cache=snap)
+        full_in = [np.concatenate([p, q], 1) for p, q in zip(prefix, suffix)]
+        full, _ = r.forward(full_in)
+        for i in range(len(KINDS)):
+            np.testing.assert_array_equal(outs[i], full[i][:, 1536:], err_msg="suffix %d layer %d" % (s, i))
+    snap.release()
+    snap.release()  # idempotent
+
+
+def test_config3_suffix_matches_oracle():
+    r = _runner()
+    prefix, suffix = _inputs(1536, 0), _inputs(64, 1)
+    _, snap = r.forward(prefix, keep=True)
+    outs, _ = r.forward(suffix, cache=snap)
+    for i, k in enumerate(KINDS):
+        if k == "linear_attention":
+            p = synth.gdn_params(seed=3, layer=i)
+            _, st = oracle_gdn(prefix[i], p)
+            ref, _ = oracle_gdn(suffix[i], p, states=st)
+            assert rel_err(outs[i], ref) < 2e-3, i
+        else:
+            p = synth.gqa_params(seed=3, layer=i, noise=0.1)
+            _, caches = oracle_gqa(prefix[i], p, 4096)
+            ref, _ = oracle_gqa(suffix[i], p, 4096, caches=caches)
+            assert rel_err(outs[i], ref) < 1e-2, i
+
+
+def test_snapshot_errors():
+    r = Runner(["linear_attention", "full_attention"], max_ctx=128)
+    x = [synth.gdn_rows(100), synth.gqa_rows(100)]
+    _, snap = r.forward(x, keep=True)
+    with pytest.raises(ha.HAError) as ei:  # 100 + 40 > 128
+        r.forward([synth.gdn_rows(40), synth.gqa_rows(40)], cache=snap)
+    assert ei.value.code == ha.HA_ERR_CONTEXT and "exceeds 128" in str(ei.value)
+    other = Runner(["linear_attention", "full_attention"], max_ctx=128)
+    with pytest.raises(ha.HAError) as ei:
+        other.forward([synth.gdn_rows(4), synth.gqa_rows(4)], cache=snap)
+    assert ei.value.code == ha.HA_ERR_HANDLE
+    snap.release()
+    with pytest.raises(ha.HAError) as ei:
+        r.forward([synth.gdn_rows(4), synth.gqa_rows(4)], cache=snap)
+    assert ei.value.code == ha.HA_ERR_HANDLE and "released" in str(ei.value)
+    with pytest.raises(ha.HAError) as ei:
+        r.eng.set_param(0, "q_norm", np.ones(256))
+    assert ei.value.code == ha.HA_ERR_PARAM
