@@ -116,6 +116,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the T / B sweep")
+    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa"],
+                    help="run only one layer kind (B=8, T=2048) --steps times, for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the hybrid-attention path is benchmarked on a single GPU in this build "
@@ -128,6 +130,22 @@ def main():
     ha.load_library()
     stream = torch.cuda.Stream()
     B, T = 8, 2048
+    if args.profile_kernel:
+        kind = "full_attention" if args.profile_kernel == "gqa" else "linear_attention"
+        rec = ha.SEQUENTIAL if args.profile_kernel == "gdn-seq" else ha.CHUNKED
+        with torch.cuda.stream(stream):
+            e = make_engine(ha, [kind], B, 4096, stream.cuda_stream)
+            i, o = make_buffers(torch, [kind], B, T)
+            for _ in range(args.warmup):
+                e.forward(T, i, o, recurrence=rec)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                e.forward(T, i, o, recurrence=rec)
+            torch.cuda.synchronize()
+        print(json.dumps({"profile_kernel": args.profile_kernel, "B": B, "T": T, "steps": args.steps,
+                          "ms_per_launch": (time.perf_counter() - t0) * 1e3 / args.steps}), flush=True)
+        return
     with torch.cuda.stream(stream):
         eng = make_engine(ha, KINDS, B, 4096, stream.cuda_stream)
         ins, outs = make_buffers(torch, KINDS, B, T)

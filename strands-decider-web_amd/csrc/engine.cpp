@@ -54,7 +54,7 @@ struct Layer {
   float* S = nullptr;     // [B][H][DK][DV] working state
   void* tail = nullptr;   // [B][kTailCap][lin_stride] working raw-row tail
   _Float16* K = nullptr;  // [B][HK][LT][HD]
-  _Float16* V = nullptr;
+  _Float16* V = nullptr;  // [B][HK][HD][LT] (transposed: positions contiguous)
 };
 
 size_t dtype_size(int dt) { return dt == HA_F16 ? 2 : 4; }
@@ -71,7 +71,6 @@ struct ha_engine {
   std::vector<Layer> layers;
   float* rope = nullptr;
   void* zero_tail = nullptr;  // [B][3][lin_stride] zeros: the history of an empty context
-  _Float16* Q = nullptr;      // [B][HQ][max_ctx][HD] prepared queries
   hipEvent_t ev[2] = {nullptr, nullptr};
   std::vector<hipEvent_t> lev;
   int C = 0;
@@ -119,8 +118,8 @@ int check_config(const ha_config* c) {
   if (full) {
     if (c->HD != 256 || c->HK <= 0 || c->HQ <= 0 || c->HQ % c->HK || c->HQ / c->HK != 4)
       return fail(HA_ERR_ARG, "full_attention layers need head_dim 256 and 4 query heads per KV head");
-    if (c->rot_dim <= 0 || c->rot_dim > 64 || (c->rot_dim & (c->rot_dim - 1)) || c->rot_dim < 2)
-      return fail(HA_ERR_ARG, "rotary_dim must be a power of two in [2, 64]");
+    if (c->rot_dim != 64) return fail(HA_ERR_ARG, "rotary_dim must be 64 (partial RoPE on 64 of 256 dims)");
+    if (c->max_ctx % 64) return fail(HA_ERR_ARG, "max_ctx must be a multiple of 64 for full_attention layers");
     if (c->full_stride < c->HQ * 2 * c->HD + 2 * c->HK * c->HD)
       return fail(HA_ERR_ARG, "full_stride smaller than the fused row [q|gate] x HQ | k | v");
     if (c->full_dtype != HA_F32 && c->full_dtype != HA_F16) return fail(HA_ERR_ARG, "full_dtype must be HA_F32 or HA_F16");
@@ -153,7 +152,6 @@ void free_engine(ha_engine* e) {
   }
   if (e->rope) (void)hipFree(e->rope);
   if (e->zero_tail) (void)hipFree(e->zero_tail);
-  if (e->Q) (void)hipFree(e->Q);
   for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
   for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
   if (e->own) (void)hipStreamDestroy(e->own);
@@ -250,7 +248,6 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
     if ((rc = dalloc(&e->rope, rope.size() * sizeof(float)))) return bail(rc);
     if (hipMemcpy(e->rope, rope.data(), rope.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
       return bail(fail(HA_ERR_DEVICE, "hipMemcpy rope failed"));
-    if ((rc = dalloc(&e->Q, sizeof(_Float16) * B * c.HQ * (size_t)c.max_ctx * c.HD))) return bail(rc);
   }
   *out = e;
   return HA_OK;
@@ -327,7 +324,9 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       if (e->layers[i].kind == HA_FULL_ATTENTION) {
         const size_t w = (size_t)P * c.HD * sizeof(_Float16), dp = (size_t)c.max_ctx * c.HD * sizeof(_Float16);
         HA_HIP(hipMemcpy2DAsync(e->layers[i].K, dp, resume->layers[i].K, w, w, B * c.HK, hipMemcpyDeviceToDevice, st));
-        HA_HIP(hipMemcpy2DAsync(e->layers[i].V, dp, resume->layers[i].V, w, w, B * c.HK, hipMemcpyDeviceToDevice, st));
+        // V^T: P positions of every (sequence, KV head, dim) row
+        const size_t vw = (size_t)P * sizeof(_Float16), vp = (size_t)c.max_ctx * sizeof(_Float16);
+        HA_HIP(hipMemcpy2DAsync(e->layers[i].V, vp, resume->layers[i].V, vw, vw, B * c.HK * c.HD, hipMemcpyDeviceToDevice, st));
       }
 
   const int end = P + L;
@@ -359,7 +358,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.B = c.batch; a.HQ = c.HQ; a.HK = c.HK; a.HD = c.HD; a.RD = c.rot_dim; a.stride = c.full_stride; a.LT = c.max_ctx;
       a.P = P; a.L = L; a.dtype = c.full_dtype == HA_F16 ? 1 : 0;
       a.in = layer_in[i]; a.out = layer_out[i]; a.qw = l.qn; a.kw = l.kn; a.rope = e->rope;
-      a.Q = e->Q; a.K = l.K; a.V = l.V;
+      a.K = l.K; a.V = l.V;
       hipError_t he = ha::launch_gqa(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " attention launch: " + hipGetErrorString(he));
     }
@@ -387,9 +386,10 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
           return bail(fail(HA_ERR_DEVICE, "snapshot copy failed"));
       } else {
         const size_t w = (size_t)end * c.HD * sizeof(_Float16), sp = (size_t)c.max_ctx * c.HD * sizeof(_Float16);
+        const size_t vw = (size_t)end * sizeof(_Float16), vp = (size_t)c.max_ctx * sizeof(_Float16);
         if ((rc = dalloc(&p.K, w * B * c.HK)) || (rc = dalloc(&p.V, w * B * c.HK))) return bail(rc);
         if (hipMemcpy2DAsync(p.K, w, l.K, sp, w, B * c.HK, hipMemcpyDeviceToDevice, st) != hipSuccess ||
-            hipMemcpy2DAsync(p.V, w, l.V, sp, w, B * c.HK, hipMemcpyDeviceToDevice, st) != hipSuccess)
+            hipMemcpy2DAsync(p.V, vw, l.V, vp, vw, B * c.HK * c.HD, hipMemcpyDeviceToDevice, st) != hipSuccess)
           return bail(fail(HA_ERR_DEVICE, "snapshot copy failed"));
       }
     }
@@ -441,6 +441,17 @@ int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* ho
   } else return fail(HA_ERR_PARAM, "no part '" + w + "' for this layer kind");
   if (bytes != want) return fail(HA_ERR_ARG, "expected " + std::to_string(want) + " bytes, got " + std::to_string(bytes));
   HA_HIP(hipSetDevice(e->device));
+  if (w == "V") {  // stored [B][HK][HD][P]; returned as [B][HK][P][HD]
+    std::vector<uint16_t> tmp(want / 2);
+    HA_HIP(hipMemcpyAsync(tmp.data(), src, want, hipMemcpyDeviceToHost, e->stream));
+    HA_HIP(hipStreamSynchronize(e->stream));
+    uint16_t* dst = static_cast<uint16_t*>(host);
+    const size_t P = s->P, HD = c.HD;
+    for (size_t bh = 0; bh < B * c.HK; bh++)
+      for (size_t d = 0; d < HD; d++)
+        for (size_t t = 0; t < P; t++) dst[(bh * P + t) * HD + d] = tmp[(bh * HD + d) * P + t];
+    return HA_OK;
+  }
   HA_HIP(hipMemcpyAsync(host, src, want, hipMemcpyDeviceToHost, e->stream));
   HA_HIP(hipStreamSynchronize(e->stream));
   return HA_OK;

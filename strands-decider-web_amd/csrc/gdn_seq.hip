@@ -25,7 +25,7 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 template <typename T>
 __device__ __forceinline__ const T* row_of(const GdnArgs& a, int b, int r) {
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void gdn_seq_kernel(GdnArgs a) {
     qk[wave][1][lane] = u[2] * rk;
     qk[wave][1][lane + 64] = u[3] * rk;
     wave_sync();
-    const float beta = 1.0f / (1.0f + __expf(-bv));
+    const float beta = __builtin_amdgcn_rcpf(1.0f + __expf(-bv));
     const float xs = av + db;
     const float sp = xs > 20.0f ? xs : log1pf(__expf(xs));
     const float alpha = __expf(na * sp);

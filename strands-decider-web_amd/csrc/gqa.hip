@@ -4,16 +4,23 @@
 // transformers qwen3_5 Qwen3_5RMSNorm, apply_rotary_pos_emb, eager_attention_forward, sigmoid(gate)):
 //   q~ = q rsqrt(mean(q^2) + 1e-6) * qw,  k~ likewise with kw   (qw, kw are the stored 1 + w)
 //   rotate-half RoPE on dims [0, RD) at absolute position P + t (engine.js:105-106 table)
-//   K[kh][P+t] = f16(k~'), V[kh][P+t] = f16(v), Q = f16(f16(q~') / sqrt(HD))
-//   out = softmax_j<=P+t(Q . K_j) V * sigmoid(gate)
+//   K[P+t] = f16(k~'), V[P+t] = f16(v), q = f16(f16(q~') / sqrt(HD))
+//   out = softmax_{j <= P+t}(q . K_j) V * sigmoid(gate)
 //
-// gqa_prep_kernel: one wave per (sequence, row, head slot); RMS via a wave reduction, the RoPE partner dim via a
-//   lane swap (d <-> d +- RD/2), f16 stores into the Q scratch and the K/V cache.
-// gqa_attn_kernel: one workgroup per (sequence, KV head, block of 32 query rows) with one wave per query head of
-//   the KV group, so each 64-key K/V tile is staged once in LDS and consumed by all G heads. S^T = K Q^T and
-//   O += P V run on v_mfma_f32_16x16x32_f16 with fp32 accumulation; Q stays in VGPRs; the online softmax
-//   (max / exp2 / sum in fp32) works on the S^T accumulators directly, which already have the A-operand shape P
-//   needs for P V. The next tile is fetched into registers while the current one is consumed.
+// Cache layout in HBM (per sequence, per KV head): K row-major [LT][HD]; V transposed [HD][LT] (positions
+// contiguous), so that the attention kernel stages both tiles with 16-byte copies and reads the P V operand
+// without an LDS transpose.
+//
+// gqa_kv_kernel: one workgroup per (sequence, KV head, 64 rows): k RMSNorm + RoPE -> K rows; v through an LDS
+//   transpose -> V^T columns.
+// gqa_attn_kernel: one workgroup per (sequence, KV head, 64 query rows), one wave per (query head of the group,
+//   32-row half), so each 64-key K/V tile is staged once in LDS and consumed by 8 waves. q's RMSNorm, RoPE (both halves
+//   of a rotated pair sit in the same lane) and 1/sqrt(HD) scaling happen in registers as Q is loaded.
+//   S^T = K Q^T and O += P V run on v_mfma_f32_32x32x16_f16 with fp32 accumulation; the S^T accumulators are
+//   already the A operand P V needs. K/V tiles are double-buffered in LDS and arrive by global_load_lds_dwordx4
+//   one tile ahead, so no registers hold the prefetch. Online softmax in fp32 with a per-row reference max that is raised only when
+//   a score exceeds it by 2^8, so the 128 O accumulators are rarely rescaled; the decision is per row, which keeps
+//   every row's arithmetic independent of the other rows in its block (prefix + suffix stays bit-identical).
 #include "ha_kernels.h"
 
 namespace ha {
@@ -22,244 +29,289 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
-
-constexpr int kHD = 256, kBQ = 32, kBK = 64, kKPad = 8, kVPad = 8;
-constexpr int kKRow = kHD + kKPad;  // halves per K row in LDS
-constexpr int kVRow = kBK + kVPad;  // halves per transposed-V row in LDS
-constexpr size_t kAttnLds = sizeof(_Float16) * (size_t)(kBK * kKRow + kHD * kVRow);
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
-  return v;
-}
+typedef float f16v __attribute__((ext_vector_type(16)));
 
 template <typename T>
-__global__ __launch_bounds__(256) void gqa_prep_kernel(GqaArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int NS = a.HQ + a.HK;
-  const long item = (long)blockIdx.x * 4 + wave;
-  if (item >= (long)a.B * a.L * NS) return;
-  const int s = (int)(item % NS);
-  const long bt = item / NS;
-  const int t = (int)(bt % a.L), b = (int)(bt / a.L);
-  const int HD = a.HD, RD = a.RD, pos = a.P + t;
-  const T* row = static_cast<const T*>(a.in) + ((size_t)b * a.L + t) * a.stride;
-  const bool isq = s < a.HQ;
-  const T* src = isq ? row + (size_t)s * 2 * HD : row + (size_t)a.HQ * 2 * HD + (size_t)(s - a.HQ) * HD;
-  const int nper = HD / 64;  // dims lane + 64 i
-  float v[8], ss = 0.0f;
+using gptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ gptr<T> gp(const void* p) { return (gptr<T>)(p); }
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gpw(void* p) { return (__attribute__((address_space(1))) T*)(p); }
+
+constexpr int kHD = 256, kBQ = 32, kBK = 64;
+constexpr size_t kAttnLds = sizeof(_Float16) * (size_t)(4 * kBK * kHD);  // two K + V^T tile buffers
+constexpr float kRescale = 8.0f;    // log2 headroom before the reference max is raised
+
+__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+template <typename T>
+__device__ __forceinline__ void load8f(gptr<T> p, float* o);
+template <>
+__device__ __forceinline__ void load8f<float>(gptr<float> p, float* o) {
+  const f4 x = *(gptr<f4>)(p), y = *(gptr<f4>)(p + 4);
+  o[0] = x[0]; o[1] = x[1]; o[2] = x[2]; o[3] = x[3]; o[4] = y[0]; o[5] = y[1]; o[6] = y[2]; o[7] = y[3];
+}
+template <>
+__device__ __forceinline__ void load8f<_Float16>(gptr<_Float16> p, float* o) {
+  const h8 x = *(gptr<h8>)(p);
 #pragma unroll
-  for (int i = 0; i < 8; i++)
-    if (i < nper) { v[i] = (float)src[lane + 64 * i]; ss += v[i] * v[i]; }
-  ss = wave_sum(ss);
-  const float inv = rsqrtf(ss / HD + 1e-6f);
-  const float* w = isq ? a.qw : a.kw;
-#pragma unroll
-  for (int i = 0; i < 8; i++)
-    if (i < nper) v[i] = v[i] * inv * w[lane + 64 * i];
-  // rotate-half on dims [0, RD): dim d pairs with d + RD/2 (d < RD/2) or d - RD/2; all of them are in v[0]
-  const float partner = __shfl_xor(v[0], RD / 2);
-  if (lane < RD) {
-    const int i = lane % (RD / 2);
-    const float cs = a.rope[(size_t)pos * RD + 2 * i], sn = a.rope[(size_t)pos * RD + 2 * i + 1];
-    v[0] = lane < RD / 2 ? v[0] * cs - partner * sn : v[0] * cs + partner * sn;
-  }
-  if (isq) {
-    const float scale = rsqrtf((float)HD);
-    _Float16* dst = a.Q + (((size_t)b * a.HQ + s) * a.L + t) * HD;
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      if (i < nper) dst[lane + 64 * i] = (_Float16)((float)(_Float16)v[i] * scale);
-  } else {
-    const int kh = s - a.HQ;
-    const size_t cb = (((size_t)b * a.HK + kh) * a.LT + pos) * HD;
-    const T* vs = row + (size_t)a.HQ * 2 * HD + (size_t)a.HK * HD + (size_t)kh * HD;
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      if (i < nper) {
-        a.K[cb + lane + 64 * i] = (_Float16)v[i];
-        a.V[cb + lane + 64 * i] = (_Float16)(float)vs[lane + 64 * i];
-      }
-  }
+  for (int i = 0; i < 8; i++) o[i] = (float)x[i];
 }
 
-template <int G, typename T>
-__global__ __launch_bounds__(64 * G) void gqa_attn_kernel(GqaArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
-  _Float16* Ks = reinterpret_cast<_Float16*>(lds_raw);  // [kBK][kKRow]
-  _Float16* Vt = Ks + kBK * kKRow;                      // [kHD][kVRow], transposed V tile
-
-  const int nqb = (a.L + kBQ - 1) / kBQ;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int kh = blockIdx.y, b = blockIdx.z;
+// K rows and V^T columns for rows [t0, t0 + 64) of one (sequence, KV head).
+template <typename T>
+__global__ __launch_bounds__(256) void gqa_kv_kernel(GqaArgs a) {
+  __shared__ _Float16 vs[64][kHD + 8];
+  const int t0 = blockIdx.x * 64, kh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = kh * G + wave;
-  const int g = lane >> 4, c16 = lane & 15;
-  const int q0 = qb * kBQ;
-  constexpr int NT = 64 * G;
+  const int RD = a.RD;
+  const size_t kvb = ((size_t)b * a.HK + kh) * a.LT * kHD;
+  // K: wave handles rows wave, wave + 4, ...; lane holds dims lane + 64 i
+  for (int rr = wave; rr < 64; rr += 4) {
+    const int t = t0 + rr;
+    if (t >= a.L) break;
+    const int pos = a.P + t;
+    gptr<T> row = gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride;
+    gptr<T> src = row + (size_t)a.HQ * 2 * kHD + (size_t)kh * kHD;
+    float v[4], ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) { v[i] = (float)src[lane + 64 * i]; ss += v[i] * v[i]; }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m);
+    const float inv = rsqrtf(ss / kHD + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = v[i] * inv * gp<float>(a.kw)[lane + 64 * i];
+    const float partner = __shfl_xor(v[0], RD / 2);
+    if (lane < RD) {
+      const int i = lane % (RD / 2);
+      const float cs = gp<float>(a.rope)[(size_t)pos * RD + 2 * i], sn = gp<float>(a.rope)[(size_t)pos * RD + 2 * i + 1];
+      v[0] = lane < RD / 2 ? v[0] * cs - partner * sn : v[0] * cs + partner * sn;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) gpw<_Float16>(a.K)[kvb + (size_t)pos * kHD + lane + 64 * i] = (_Float16)v[i];
+    // raw v row into LDS for the transpose
+    gptr<T> vsrc = row + (size_t)a.HQ * 2 * kHD + (size_t)a.HK * kHD + (size_t)kh * kHD;
+#pragma unroll
+    for (int i = 0; i < 4; i++) vs[rr][lane + 64 * i] = (_Float16)(float)vsrc[lane + 64 * i];
+  }
+  __syncthreads();
+  // V^T: thread d writes the positions of this block for dim d
+  const int d = tid;
+  const int n = min(64, a.L - t0);
+  __attribute__((address_space(1))) _Float16* vt = gpw<_Float16>(a.V) + kvb + (size_t)d * a.LT + a.P + t0;
+  for (int r = 0; r < n; r++) vt[r] = vs[r][d];
+}
 
-  // Q rows as the B operand of S^T = K Q^T: qreg[rt][ks] = Q[q0 + 16 rt + c16][32 ks + 8 g .. +7]
-  h8 qreg[2][8];
-  const _Float16* Qh = a.Q + ((size_t)b * a.HQ + h) * a.L * kHD;
+// Workgroup = 8 waves: wave w serves query head kh*4 + (w & 3) on rows q0 + 32 (w >> 2) .. +31 (a block of 64
+// query rows for all 4 heads of the KV group), so each staged 64-key K/V tile feeds 8 waves, and two waves share
+// every SIMD to hide each other's latency.
+constexpr int kRows = 64;     // query rows per workgroup
+constexpr int kWaves = 8;
+
+template <typename T>
+__global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
+  // Two LDS buffers of one 64-key tile each. K tile: key r at [r][32 chunks of 8 dims], chunk j stored in slot
+  // j ^ (r & 31); V^T tile: dim d at [d][8 chunks of 8 positions], chunk c stored in slot c ^ (d & 7). A wave's
+  // global_load_lds_dwordx4 covers whole 512 B K rows or 128 B V^T rows (coalesced), and the XOR swizzle spreads
+  // the 32 rows an MFMA operand read touches over the LDS banks.
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  constexpr int kTileHalves = kBK * kHD;
+  _Float16* lds = reinterpret_cast<_Float16*>(lds_raw);
+
+  // heavy-first order over all workgroups; the 16 (sequence, KV head) pairs cycle fastest, so every workgroup of a
+  // pair lands on the same XCD (round-robin dispatch over 8 XCDs) and its K/V stays in that XCD's L2
+  const int npair = a.B * a.HK;
+  const int nqb = (a.L + kRows - 1) / kRows;
+  const int id = blockIdx.x;
+  const int pair = id % npair, qb = nqb - 1 - id / npair;
+  const int b = pair / a.HK, kh = pair % a.HK;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = kh * 4 + (wave & 3);
+  const int half = lane >> 5, c32 = lane & 31;
+  const int q0 = qb * kRows + 32 * (wave >> 2);
+  const int RD = a.RD;
+
+  const int nvalid = a.P + a.L;
+  const int last_key = min(a.P + qb * kRows + kRows - 1, nvalid - 1);
+  const int ntiles = last_key / kBK + 1;
+  const size_t kvb = ((size_t)b * a.HK + kh) * a.LT * kHD;
+  gptr<_Float16> Kg = gp<_Float16>(a.K) + kvb;
+  gptr<_Float16> Vg = gp<_Float16>(a.V) + kvb;
+
+  // a tile = 32 K instructions (2 keys each) + 32 V^T instructions (8 dims each); each wave issues 4 + 4
+  auto issue = [&](int kt, int buf) {
+    _Float16* kb = lds + (size_t)buf * 2 * kTileHalves;
+    _Float16* vb = kb + kTileHalves;
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    const int t = q0 + 16 * rt + c16;
+    for (int i = 0; i < 4; i++) {
+      const int ins = wave + kWaves * i;             // 0..31
+      const int r = 2 * ins + (lane >> 5), js = lane & 31;
+      const int j = js ^ (r & 31);                   // global chunk that belongs in slot js
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(Kg + (size_t)(kt * kBK + r) * kHD + 8 * j),
+                                       (__attribute__((address_space(3))) void*)(kb + (size_t)ins * 512), 16, 0, 0);
+      const int d = 8 * ins + (lane >> 3), cs = lane & 7;
+      const int c = cs ^ (d & 7);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(Vg + (size_t)d * a.LT + kt * kBK + 8 * c),
+                                       (__attribute__((address_space(3))) void*)(vb + (size_t)ins * 512), 16, 0, 0);
+    }
+  };
+  issue(0, 0);
+
+  // Q as the B operand of S^T = K Q^T (32x32x16): qreg[ks] = q[q0 + c32][16 ks + 8 half .. +7], prepared here:
+  // RMSNorm (the two halves of a row sit in lanes l and l + 32), RoPE (dim i < 32 in ks 0/1 pairs with i + 32 in
+  // ks 2/3 of the same lane and element), then f16(f16(.) / sqrt(HD)).
+  h8 qreg[16];
+  {
+    const int t = q0 + c32;
+    const int tc = min(t, a.L - 1);
+    gptr<T> src = gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD;
+    float ss = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) {
-      h8 z = {};
-      qreg[rt][ks] = t < a.L ? *reinterpret_cast<const h8*>(Qh + (size_t)t * kHD + 32 * ks + 8 * g) : z;
+    for (int ks = 0; ks < 16; ks++) {
+      float qv[8];
+      load8f<T>(src + 16 * ks + 8 * half, qv);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        ss += qv[e] * qv[e];
+        qreg[ks][e] = (_Float16)0.0f;
+      }
+    }
+    ss += __shfl_xor(ss, 32);
+    const float inv = rsqrtf(ss / kHD + 1e-6f);
+    const int pos = a.P + tc;
+    const float scale = rsqrtf((float)kHD);
+    // dims 0..63 (slots ks 0..3): normalise, rotate pairs (ks, ks + 2), scale
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      float x1[8], x2[8];
+      load8f<T>(src + 16 * ks + 8 * half, x1);
+      load8f<T>(src + 16 * (ks + 2) + 8 * half, x2);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int i = 16 * ks + 8 * half + e;
+        const float n1 = x1[e] * inv * gp<float>(a.qw)[i], n2 = x2[e] * inv * gp<float>(a.qw)[i + 32];
+        const float cs = gp<float>(a.rope)[(size_t)pos * RD + 2 * i], sn = gp<float>(a.rope)[(size_t)pos * RD + 2 * i + 1];
+        qreg[ks][e] = t < a.L ? (_Float16)((float)(_Float16)(n1 * cs - n2 * sn) * scale) : (_Float16)0.0f;
+        qreg[ks + 2][e] = t < a.L ? (_Float16)((float)(_Float16)(n2 * cs + n1 * sn) * scale) : (_Float16)0.0f;
+      }
+    }
+#pragma unroll
+    for (int ks = 4; ks < 16; ks++) {
+      float qv[8];
+      load8f<T>(src + 16 * ks + 8 * half, qv);
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        qreg[ks][e] = t < a.L ? (_Float16)((float)(_Float16)(qv[e] * inv * gp<float>(a.qw)[16 * ks + 8 * half + e]) * scale)
+                              : (_Float16)0.0f;
     }
   }
 
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-  f4 O[2][16];
+  // row state: this lane's S^T columns are query row c32 (both halves hold it after the xor-32 reductions)
+  float mref = -INFINITY, lsum = 0.0f;
+  f16v O[8];  // O[dt][v] = out row 8 (v/4) + 4 half + v%4, dim 32 dt + c32
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-    for (int dt = 0; dt < 16; dt++) O[rt][dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  const int nvalid = a.P + a.L;
-  const int last_key = min(a.P + q0 + kBQ - 1, nvalid - 1);
-  const int ntiles = last_key / kBK + 1;
-  const _Float16* Kg = a.K + ((size_t)b * a.HK + kh) * a.LT * kHD;
-  const _Float16* Vg = a.V + ((size_t)b * a.HK + kh) * a.LT * kHD;
-  constexpr int kChunks = kBK * kHD / 8;  // 16-byte chunks per tile
-  constexpr int kPer = kChunks / NT;
+  for (int dt = 0; dt < 8; dt++) O[dt] = f16v{};
+  const int rowpos = a.P + q0 + c32;
   const float log2e = 1.4426950408889634f;
 
-  h8 kbuf[kPer], vbuf[kPer];
-  auto fetch = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-      const int c = tid + i * NT, kr = c / (kHD / 8), d8 = c % (kHD / 8), key = kt * kBK + kr;
-      h8 z = {};
-      kbuf[i] = key < nvalid ? *reinterpret_cast<const h8*>(Kg + (size_t)key * kHD + d8 * 8) : z;
-      vbuf[i] = key < nvalid ? *reinterpret_cast<const h8*>(Vg + (size_t)key * kHD + d8 * 8) : z;
-    }
-  };
-  auto stash = [&]() {
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-      const int c = tid + i * NT, kr = c / (kHD / 8), d8 = c % (kHD / 8);
-      *reinterpret_cast<h8*>(Ks + kr * kKRow + d8 * 8) = kbuf[i];
-#pragma unroll
-      for (int e = 0; e < 8; e++) Vt[(d8 * 8 + e) * kVRow + kr] = vbuf[i][e];
-    }
-  };
-
-  fetch(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
   for (int kt = 0; kt < ntiles; kt++) {
-    __syncthreads();
-    stash();
-    __syncthreads();
-    if (kt + 1 < ntiles) fetch(kt + 1);
+    const int cur = kt & 1;
+    if (kt + 1 < ntiles) issue(kt + 1, cur ^ 1);
+    const _Float16* ks_l = lds + (size_t)cur * 2 * kTileHalves;
+    const _Float16* vs_l = ks_l + kTileHalves;
 
-    // S^T[key 16kk + 4g + e][row 16rt + c16]
-    f4 st[4][2];
+    // the 64-key tile in two 32-key halves kk; S^T[key 32 kk + 8 (v/4) + 4 half + v%4][row c32]
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++)
+    for (int kk = 0; kk < 2; kk++) {
+      f16v st = f16v{};
 #pragma unroll
-      for (int rt = 0; rt < 2; rt++) {
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-          const h8 ka = *reinterpret_cast<const h8*>(Ks + (16 * kk + c16) * kKRow + 32 * ks + 8 * g);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qreg[rt][ks], acc, 0, 0, 0);
-        }
-        st[kk][rt] = acc;
+      for (int ks = 0; ks < 16; ks++) {
+        const int r = 32 * kk + c32, j = 2 * ks + half;
+        const h8 ka = *reinterpret_cast<const h8*>(ks_l + (size_t)r * kHD + 8 * (j ^ (r & 31)));
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[ks], st, 0, 0, 0);
       }
-
-    h8 pa[2][2];
-#pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
-      const int rowpos = a.P + q0 + 16 * rt + c16;
       float mx = -INFINITY;
 #pragma unroll
-      for (int kk = 0; kk < 4; kk++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int key = kt * kBK + 16 * kk + 4 * g + e;
-          const float s = key <= rowpos ? st[kk][rt][e] * log2e : -INFINITY;
-          st[kk][rt][e] = s;
-          mx = fmaxf(mx, s);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      for (int v = 0; v < 16; v++) {
+        const int key = kt * kBK + 32 * kk + 8 * (v >> 2) + 4 * half + (v & 3);
+        const float sv = key <= rowpos ? st[v] * log2e : -INFINITY;
+        st[v] = sv;
+        mx = fmaxf(mx, sv);
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(m[rt], mx);
-      const float alpha = exp2f(m[rt] - mnew);
+      // raise the reference max only when a score would exceed it by 2^kRescale (decided per row)
+      const float mnew = mx > mref + kRescale ? mx : mref;
+      const float alpha = __builtin_amdgcn_exp2f(mref - mnew);  // exactly 1 when unchanged, 0 on a row's first keys
+      const bool need = mnew != mref && mref != -INFINITY;
+      mref = mnew;
       float sum = 0.0f;
 #pragma unroll
-      for (int kk = 0; kk < 4; kk++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const float p = exp2f(st[kk][rt][e] - mnew);
-          st[kk][rt][e] = p;
-          sum += p;
-        }
-      sum += __shfl_xor(sum, 16);
+      for (int v = 0; v < 16; v++) {
+        const float pv = __builtin_amdgcn_exp2f(st[v] - mnew);
+        st[v] = pv;
+        sum += pv;
+      }
       sum += __shfl_xor(sum, 32);
-      l[rt] = l[rt] * alpha + sum;
-      m[rt] = mnew;
-      // O rows of this lane are 16 rt + 4 g + e; their alpha lives in lane 4 g + e
-      float al[4];
+      lsum = lsum * alpha + sum;
+      if (__any(need)) {
+        // O rows 8 (v/4) + 4 half + v%4 take alpha from lane (row) in the low half
 #pragma unroll
-      for (int e = 0; e < 4; e++) al[e] = __shfl(alpha, 4 * g + e);
+        for (int v = 0; v < 16; v++) {
+          const float al = __shfl(alpha, 8 * (v >> 2) + 4 * half + (v & 3));
 #pragma unroll
-      for (int dt = 0; dt < 16; dt++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) O[rt][dt][e] *= al[e];
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          pa[rt][kb][e] = (_Float16)st[2 * kb][rt][e];
-          pa[rt][kb][4 + e] = (_Float16)st[2 * kb + 1][rt][e];
+          for (int dt = 0; dt < 8; dt++) O[dt][v] *= al;
         }
-    }
-
-#pragma unroll
-    for (int dt = 0; dt < 16; dt++)
+      }
+      // P V: k-step kb covers keys 32 kk + 16 kb + {4 half + r, 8 + 4 half + r} (the S^T accumulator order)
 #pragma unroll
       for (int kb = 0; kb < 2; kb++) {
-        const _Float16* vr = Vt + (16 * dt + c16) * kVRow + 32 * kb + 4 * g;
-        const h4 lo = *reinterpret_cast<const h4*>(vr);
-        const h4 hi = *reinterpret_cast<const h4*>(vr + 16);
-        const h8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        h8 pa;
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++) O[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt][kb], vb, O[rt][dt], 0, 0, 0);
+        for (int r = 0; r < 4; r++) {
+          pa[r] = (_Float16)st[8 * kb + r];
+          pa[4 + r] = (_Float16)st[8 * kb + 4 + r];
+        }
+        const int c0 = 2 * (2 * kk + kb);  // V^T chunks c0, c0 + 1 hold these 16 positions
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+          const int d = 32 * dt + c32;
+          const _Float16* vr = vs_l + (size_t)d * kBK;
+          const h4 lo = *reinterpret_cast<const h4*>(vr + 8 * (c0 ^ (d & 7)) + 4 * half);
+          const h4 hi = *reinterpret_cast<const h4*>(vr + 8 * ((c0 + 1) ^ (d & 7)) + 4 * half);
+          const h8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, vb, O[dt], 0, 0, 0);
+        }
       }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next tile has landed
+    __syncthreads();                // ... and every wave's; nobody reads the current buffer any more
   }
 
   // epilogue: out[t][h][d] = O / l * sigmoid(gate)
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
-    float linv[4];
+  for (int v = 0; v < 16; v++) {
+    const float linv = 1.0f / __shfl(lsum, 8 * (v >> 2) + 4 * half + (v & 3));
+    const int t = q0 + 8 * (v >> 2) + 4 * half + (v & 3);
+    if (t >= a.L) continue;
+    gptr<T> grow = gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)h * 2 * kHD + kHD;
+    __attribute__((address_space(1))) T* orow = gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD;
 #pragma unroll
-    for (int e = 0; e < 4; e++) linv[e] = 1.0f / __shfl(l[rt], 4 * g + e);
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int t = q0 + 16 * rt + 4 * g + e;
-      if (t >= a.L) continue;
-      const T* grow = static_cast<const T*>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)h * 2 * kHD + kHD;
-      T* orow = static_cast<T*>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD;
-#pragma unroll
-      for (int dt = 0; dt < 16; dt++) {
-        const int d = 16 * dt + c16;
-        const float gt = (float)grow[d];
-        orow[d] = (T)(O[rt][dt][e] * linv[e] / (1.0f + __expf(-gt)));
-      }
+    for (int dt = 0; dt < 8; dt++) {
+      const int d = 32 * dt + c32;
+      orow[d] = (T)(O[dt][v] * linv * sigmoid((float)grow[d]));
     }
   }
 }
 
-template <int G, typename T>
+template <typename T>
 hipError_t launch_attn(const GqaArgs& a, hipStream_t s) {
-  auto k = gqa_attn_kernel<G, T>;
+  auto k = gqa_attn_kernel<T>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)kAttnLds);
   if (e != hipSuccess) return e;
-  dim3 grid((a.L + kBQ - 1) / kBQ, a.HK, a.B), block(64 * G);
+  dim3 grid(((a.L + kRows - 1) / kRows) * a.HK * a.B), block(64 * kWaves);
   hipLaunchKernelGGL(k, grid, block, kAttnLds, s, a);
   return hipGetLastError();
 }
@@ -267,20 +319,17 @@ hipError_t launch_attn(const GqaArgs& a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_gqa(const GqaArgs& a, hipStream_t s) {
-  if (a.HD != kHD || a.RD <= 0 || a.RD > 64 || (a.RD & (a.RD - 1)) || a.HQ % a.HK) return hipErrorInvalidValue;
-  const int G = a.HQ / a.HK;
-  const long items = (long)a.B * a.L * (a.HQ + a.HK);
-  dim3 pgrid((unsigned)((items + 3) / 4)), pblock(256);
+  // RD = 64 puts both halves of every rotated q pair in one lane of the fused q preparation
+  if (a.HD != kHD || a.RD != 64 || a.HQ % a.HK || a.HQ / a.HK != 4) return hipErrorInvalidValue;
+  if (a.LT % kBK) return hipErrorInvalidValue;  // V^T tiles are read 64 positions at a time, inside [0, LT)
+  dim3 kgrid((a.L + 63) / 64, a.HK, a.B), kblock(256);
   if (a.dtype == 0)
-    hipLaunchKernelGGL(gqa_prep_kernel<float>, pgrid, pblock, 0, s, a);
+    hipLaunchKernelGGL(gqa_kv_kernel<float>, kgrid, kblock, 0, s, a);
   else
-    hipLaunchKernelGGL(gqa_prep_kernel<_Float16>, pgrid, pblock, 0, s, a);
+    hipLaunchKernelGGL(gqa_kv_kernel<_Float16>, kgrid, kblock, 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  switch (G) {
-    case 4: return a.dtype == 0 ? launch_attn<4, float>(a, s) : launch_attn<4, _Float16>(a, s);
-    default: return hipErrorInvalidValue;
-  }
+  return a.dtype == 0 ? launch_attn<float>(a, s) : launch_attn<_Float16>(a, s);
 }
 
 }  // namespace ha

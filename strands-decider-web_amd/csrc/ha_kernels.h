@@ -36,9 +36,8 @@ struct GqaArgs {
   const float* qw;           // [HD] stored (1 + w)
   const float* kw;           // [HD]
   const float* rope;         // [LT][RD] cos/sin pairs
-  _Float16* Q;               // [B][HQ][L][HD] scratch: prepared q times HD^-1/2, f16
-  _Float16* K;               // [B][HK][LT][HD] cache
-  _Float16* V;               // [B][HK][LT][HD] cache
+  _Float16* K;               // [B][HK][LT][HD] cache, row-major
+  _Float16* V;               // [B][HK][HD][LT] cache, transposed (positions contiguous)
 };
 
 // Copy the raw rows [dst_first, P + L) (dst_first >= s0 - (KC-1)) of every sequence from (tail, in) into
