@@ -6,20 +6,20 @@
 // Sequence Length"; Yang, Kautz & Hatamizadeh, "Gated Delta Networks"). For a chunk of 64 rows with cumulative
 // log-decay gc (gc_t = sum_{s<=t} g_s inside the chunk) and the state S at the chunk start:
 //   A   = strictly_lower(beta_t (k^_t . k^_t') exp(gc_t - gc_t'))      T = (I + A)^-1
-//   U   = T (beta v)      W = T (beta exp(gc) k^)      V_new = U - W S
+//   U   = T diag(beta) v      V_new = U - T diag(beta e^gc) (k^ S)     (that is U - W S, W never formed)
 //   o_t = exp(gc_t) q^_t S + sum_{t'<=t} (q^_t . k^_t') exp(gc_t - gc_t') V_new_t'
-//   S  <- exp(gc_63) S + sum_t exp(gc_63 - gc_t) k^_t V_new_t^T          (complete chunks only)
+//   S  <- exp(gc_63) S + k^T diag(exp(gc_63 - gc)) V_new                 (complete chunks only)
 //
 // One workgroup of 8 waves per (sequence, head) walks the chunks in order; the fp32 state stays in MFMA
 // accumulator registers for the whole call (wave w owns value columns 16w..16w+15). Per chunk:
-//   1. conv (4 taps) + SiLU straight from the fused rows in HBM, l2 norms by 16-lane reductions, gates by a
-//      64-lane scan; f16 tiles of q^, k^ and the pre-scaled transposes (beta e^gc k^)^T, (e^(gl-gc) k^)^T and
-//      (beta v)^T land in LDS;
+//   1. conv (4 taps) + SiLU of raw rows fetched one chunk ahead (their loads overlap the previous chunk's state
+//      update), l2 norms by 16-lane reductions, gates by a 64-lane scan; f16 tiles of q^, k^, k^T and v^T in LDS
+//      (the per-row gate factors are applied to T's columns and V_new's rows instead of to copies of k);
 //   2. K K^T and Q K^T on v_mfma_f32_16x16x32_f16 -> A (fp32) and the decay-masked scores (f16);
-//   3. T by fp32 forward substitution on the four 16x16 diagonal blocks and fp32 MFMA (16x16x4) for the
-//      off-diagonal blocks, while the other waves compute q^ S;
-//   4. U and W on f16 MFMA; 5. V_new, o and the state update on f16 MFMA with fp32 accumulation, with S as f16
-//      B operands built in registers; 6. gated RMSNorm epilogue (GNORM) and the store.
+//   3. T: right-looking fp32 substitution on the four 16x16 diagonal blocks (one wave) and fp32 MFMA (16x16x4) for
+//      the off-diagonal blocks, while the other waves compute q^ S; T diag(beta), T diag(beta e^gc) stored f16;
+//   4-5. U, k^ S, V_new, o and the state update on f16 MFMA with fp32 accumulation, S as f16 B operands built in
+//      registers; 6. gated RMSNorm epilogue (GNORM) and the store.
 // Chunk boundaries sit at s0 + 64k, so a row is processed identically however a sequence is split into calls;
 // only complete chunks advance the stored state.
 //
@@ -45,11 +45,10 @@ constexpr int kAP = kCH + 4;  // row pitch (floats) of the fp32 A / T tile
 struct Lds {
   _Float16 Qs[kCH * kQP];   // q^ / sqrt(DK), [t][i]
   _Float16 Ks[kCH * kQP];   // k^, [t][i]
-  _Float16 Ws[kCH * kQP];   // -W, [t][i]
-  _Float16 KbT[kDK * kTP];  // (beta e^gc k^)^T, [i][t]
-  _Float16 KdT[kDK * kTP];  // (e^(gl - gc) k^)^T, [i][t]
-  _Float16 VbT[kDV * kTP];  // (beta v)^T, [j][t]
-  _Float16 Tf[kCH * kTP];   // T in f16, [t][t']
+  _Float16 KT[kDK * kTP];   // k^ transposed, [i][t]
+  _Float16 VT[kDV * kTP];   // v transposed, [j][t]
+  _Float16 Tb[kCH * kTP];   // T diag(beta), f16, [t][t']
+  _Float16 Tw[kCH * kTP];   // T diag(beta e^gc), f16
   _Float16 Att[kCH * kTP];  // decay-masked causal q^ k^T, [t][t']
   float Tm[kCH * kAP];      // A, then T, fp32
   float Xs[3 * 256];        // off-diagonal solve scratch
@@ -58,29 +57,39 @@ struct Lds {
   float inv[kCH];
 };
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// SiLU / sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE division sequence
+__device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// Global (address space 1) pointers: loads through them are global_load_*, not flat_load_*, so they are not
+// counted by the LDS wait counter and outstanding global loads do not stall LDS traffic.
+template <typename T>
+using gptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ gptr<T> gp(const void* p) { return (gptr<T>)(p); }
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gpw(void* p) { return (__attribute__((address_space(1))) T*)(p); }
 
 template <typename T>
-__device__ __forceinline__ const T* row_of(const GdnArgs& a, int b, int r) {
-  if (r < a.P) return static_cast<const T*>(a.tail) + ((size_t)b * a.tail_cap + (r - (a.s0 - (kKC - 1)))) * a.stride;
-  return static_cast<const T*>(a.in) + ((size_t)b * a.L + (r - a.P)) * a.stride;
+__device__ __forceinline__ gptr<T> row_of(const GdnArgs& a, int b, int r) {
+  if (r < a.P) return gp<T>(a.tail) + ((size_t)b * a.tail_cap + (r - (a.s0 - (kKC - 1)))) * a.stride;
+  return gp<T>(a.in) + ((size_t)b * a.L + (r - a.P)) * a.stride;
 }
 
-__device__ __forceinline__ void load8(const float* p, float* o) {
-  const f4 x = *reinterpret_cast<const f4*>(p), y = *reinterpret_cast<const f4*>(p + 4);
+__device__ __forceinline__ void load8(gptr<float> p, float* o) {
+  const f4 x = *(gptr<f4>)(p), y = *(gptr<f4>)(p + 4);
   o[0] = x[0]; o[1] = x[1]; o[2] = x[2]; o[3] = x[3]; o[4] = y[0]; o[5] = y[1]; o[6] = y[2]; o[7] = y[3];
 }
-__device__ __forceinline__ void load8(const _Float16* p, float* o) {
-  const h8 x = *reinterpret_cast<const h8*>(p);
+__device__ __forceinline__ void load8(gptr<_Float16> p, float* o) {
+  const h8 x = *(gptr<h8>)(p);
 #pragma unroll
   for (int i = 0; i < 8; i++) o[i] = (float)x[i];
 }
-__device__ __forceinline__ void load4(const float* p, float* o) {
-  const f4 x = *reinterpret_cast<const f4*>(p);
+__device__ __forceinline__ void load4(gptr<float> p, float* o) {
+  const f4 x = *(gptr<f4>)(p);
   o[0] = x[0]; o[1] = x[1]; o[2] = x[2]; o[3] = x[3];
 }
-__device__ __forceinline__ void load4(const _Float16* p, float* o) {
-  const h4 x = *reinterpret_cast<const h4*>(p);
+__device__ __forceinline__ void load4(gptr<_Float16> p, float* o) {
+  const h4 x = *(gptr<h4>)(p);
   o[0] = (float)x[0]; o[1] = (float)x[1]; o[2] = (float)x[2]; o[3] = (float)x[3];
 }
 
@@ -102,12 +111,17 @@ __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 template <typename T>
 __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   Lds& sm = *reinterpret_cast<Lds*>(lds_raw);
   const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
+  const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
   const int end = a.P + a.L;
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
 
@@ -118,34 +132,77 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   for (int it = 0; it < 8; it++)
 #pragma unroll
     for (int e = 0; e < 4; e++)
-      S[it][e] = a.S_in ? a.S_in[sbase + (size_t)(16 * it + 4 * grp + e) * kDV + 16 * w + c16] : 0.0f;
+      S[it][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * it + 4 * ((tid0 & 63) >> 4) + e) * kDV + 16 * w + (tid0 & 15)] : 0.0f;
 
   // this head's conv taps: local channel q 0..127, k 128..255, v 256..383
-  for (int i = tid; i < 3 * 128 * kKC; i += kNT) {
+  for (int i = tid0; i < 3 * 128 * kKC; i += kNT) {
     const int lc = i / kKC, j = i % kKC;
     const int ch = lc < 128 ? h * kDK + lc : lc < 256 ? a.H * kDK + h * kDK + (lc - 128) : 2 * a.H * kDK + h * kDV + (lc - 256);
-    sm.cw[lc][j] = a.conv_w[(size_t)ch * kKC + j];
+    sm.cw[lc][j] = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
   }
-  __syncthreads();
 
-  // conv tasks: rows 4 rg .. 4 rg + 3 of the chunk; 8 q-or-k channels and 4 v channels
-  const int rg = tid >> 5, cgi = tid & 31, qk = cgi >> 4, cg = cgi & 15;
-  const int chq = (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, lq = qk * 128 + 8 * cg;
-  const int chv = 2 * a.H * kDK + h * kDV + 4 * cgi, lv = 256 + 4 * cgi;
-  const float na = a.negA[h], db = a.dtb[h];
+  const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
   const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
+
+  // raw rows of a chunk (and its a/b gate inputs), fetched one chunk ahead; rows past the end read as 0, so the
+  // fetch is unconditional and the previous chunk's rows are dead once it is issued
+  float x[7][8], xv[7][4], ga, gb;
+  __syncthreads();  // conv taps visible
 
   for (int c0 = a.s0; c0 < end; c0 += kCH) {
     const int m = min(kCH, end - c0);
     const bool full = m == kCH;
+    // per-lane indices re-derived every chunk through an opaque copy: address arithmetic built on them stays in
+    // the loop instead of being hoisted out of it and spilled
+    const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
+    // conv tasks: rows 4 rg .. 4 rg + 3 of the chunk; 8 q-or-k channels and 4 v channels
+    const int rg = tid >> 5, cgi = tid & 31, qk = cgi >> 4, cg = cgi & 15;
+    const int chq = (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, lq = qk * 128 + 8 * cg;
+    const int chv = 2 * a.H * kDK + h * kDV + 4 * cgi, lv = 256 + 4 * cgi;
 
-    // ---- 1. gates: every wave computes all 64 rows (lane = row), kept in registers and read by lane shuffles
+    // raw rows of a chunk (and its a/b gate inputs), fetched one chunk ahead; rows past the end read as 0, so the
+    // fetch is unconditional and the previous chunk's rows are dead once it is issued
+    auto fetch = [&](int cs) {
+      const bool fresh = cs - (kKC - 1) >= a.P;  // no row of this chunk (incl. its conv history) is a replay row
+      const gptr<T> base = gp<T>(a.in) + ((ptrdiff_t)b * a.L + (cs - a.P)) * a.stride;
+  #pragma unroll
+      for (int i = 0; i < 7; i++) {
+        const int r = cs + 4 * rg - 3 + i, rc = min(r, end - 1);
+        const gptr<T> row = fresh ? base + (ptrdiff_t)(rc - cs) * a.stride : row_of<T>(a, b, rc);
+        load8(row + chq, x[i]);
+        load4(row + chv, xv[i]);
+        if (r >= end) {
+  #pragma unroll
+          for (int c = 0; c < 8; c++) x[i][c] = 0.0f;
+  #pragma unroll
+          for (int c = 0; c < 4; c++) xv[i][c] = 0.0f;
+        }
+      }
+      const gptr<T> grow = row_of<T>(a, b, min(cs + lane, end - 1));
+      ga = cs + lane < end ? (float)grow[aoff] : 0.0f;
+      gb = cs + lane < end ? (float)grow[boff] : 0.0f;
+    };
+    if (c0 == a.s0) fetch(c0);
+
+    // z of this chunk for the gated-norm epilogue, in flight during the whole chunk
+    float zr[4][4];
+    {
+      const gptr<T> zb = gp<T>(a.in) + (size_t)b * a.L * a.stride + a.C + h * kDV + 16 * w + c16;
+#pragma unroll
+      for (int ti = 0; ti < 4; ti++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int t = 16 * ti + 4 * grp + e, r = c0 + t;
+          const int rr = min(max(r - a.P, 0), a.L - 1);
+          zr[ti][e] = (float)zb[(size_t)rr * a.stride];
+        }
+    }
+
+    // ---- 1. gates: every wave holds all 64 rows (lane = row) in registers, read by lane shuffles ----
     float gcr = 0.0f, btr = 0.0f;
     if (lane < m) {
-      const T* row = row_of<T>(a, b, c0 + lane);
-      const float av = (float)row[aoff], bv = (float)row[boff];
-      btr = 1.0f / (1.0f + __expf(-bv));
-      const float xs = av + db;
+      btr = __builtin_amdgcn_rcpf(1.0f + __expf(-gb));
+      const float xs = ga + db;
       gcr = na * (xs > 20.0f ? xs : log1pf(__expf(xs)));
     }
 #pragma unroll
@@ -155,19 +212,8 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
     }
     const float gl = __shfl(gcr, 63);
 
-    // conv + SiLU + l2 norm of 8 q-or-k channels over 4 rows; f16 tiles (and k's scaled transposes) to LDS
+    // conv + SiLU + l2 norm of 8 q-or-k channels over 4 rows -> q^ / k^ rows, k^ transposed
     {
-      float x[7][8];
-#pragma unroll
-      for (int i = 0; i < 7; i++) {
-        const int r = c0 + 4 * rg - 3 + i;
-        if (r < end) {
-          load8(row_of<T>(a, b, r) + chq, x[i]);
-        } else {
-#pragma unroll
-          for (int c = 0; c < 8; c++) x[i][c] = 0.0f;
-        }
-      }
       float u[4][8], rs[4];
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) {
@@ -176,11 +222,11 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
 #pragma unroll
         for (int c = 0; c < 8; c++) {
           const float* wc = sm.cw[lq + c];
-          float s = wc[0] * x[rr][c];
-          s = fmaf(wc[1], x[rr + 1][c], s);
-          s = fmaf(wc[2], x[rr + 2][c], s);
-          s = fmaf(wc[3], x[rr + 3][c], s);
-          u[rr][c] = valid ? silu(s) : 0.0f;
+          float sv = wc[0] * x[rr][c];
+          sv = fmaf(wc[1], x[rr + 1][c], sv);
+          sv = fmaf(wc[2], x[rr + 2][c], sv);
+          sv = fmaf(wc[3], x[rr + 3][c], sv);
+          u[rr][c] = valid ? silu(sv) : 0.0f;
           ss = fmaf(u[rr][c], u[rr][c], ss);
         }
 #pragma unroll
@@ -194,64 +240,37 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         for (int c = 0; c < 8; c++) hv[c] = (_Float16)(u[rr][c] * rs[rr]);
         *reinterpret_cast<h8*>((qk ? sm.Ks : sm.Qs) + (4 * rg + rr) * kQP + 8 * cg) = hv;
       }
-      float fb[4], fd[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        const int t = 4 * rg + rr;
-        const float gt = __shfl(gcr, t), bt = __shfl(btr, t);
-        fb[rr] = bt * __expf(gt) * rs[rr];
-        fd[rr] = __expf(gl - gt) * rs[rr];
-      }
       if (qk) {
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-          h4 kb, kd;
+          h4 kt;
 #pragma unroll
-          for (int rr = 0; rr < 4; rr++) {
-            kb[rr] = (_Float16)(u[rr][c] * fb[rr]);
-            kd[rr] = (_Float16)(u[rr][c] * fd[rr]);
-          }
-          *reinterpret_cast<h4*>(sm.KbT + (8 * cg + c) * kTP + 4 * rg) = kb;
-          *reinterpret_cast<h4*>(sm.KdT + (8 * cg + c) * kTP + 4 * rg) = kd;
+          for (int rr = 0; rr < 4; rr++) kt[rr] = (_Float16)(u[rr][c] * rs[rr]);
+          *reinterpret_cast<h4*>(sm.KT + (8 * cg + c) * kTP + 4 * rg) = kt;
         }
       }
     }
-    // conv + SiLU of 4 v channels over 4 rows -> (beta v)^T
-    {
-      float xv[7][4];
+    // conv + SiLU of 4 v channels over 4 rows -> v^T
 #pragma unroll
-      for (int i = 0; i < 7; i++) {
-        const int r = c0 + 4 * rg - 3 + i;
-        if (r < end) {
-          load4(row_of<T>(a, b, r) + chv, xv[i]);
-        } else {
+    for (int c = 0; c < 4; c++) {
+      const float* wc = sm.cw[lv + c];
+      h4 vt;
 #pragma unroll
-          for (int c = 0; c < 4; c++) xv[i][c] = 0.0f;
-        }
+      for (int rr = 0; rr < 4; rr++) {
+        float sv = wc[0] * xv[rr][c];
+        sv = fmaf(wc[1], xv[rr + 1][c], sv);
+        sv = fmaf(wc[2], xv[rr + 2][c], sv);
+        sv = fmaf(wc[3], xv[rr + 3][c], sv);
+        vt[rr] = (_Float16)(4 * rg + rr < m ? silu(sv) : 0.0f);
       }
-      float bt[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; rr++) bt[rr] = __shfl(btr, 4 * rg + rr);
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const float* wc = sm.cw[lv + c];
-        h4 vb;
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-          float s = wc[0] * xv[rr][c];
-          s = fmaf(wc[1], xv[rr + 1][c], s);
-          s = fmaf(wc[2], xv[rr + 2][c], s);
-          s = fmaf(wc[3], xv[rr + 3][c], s);
-          vb[rr] = (_Float16)(4 * rg + rr < m ? bt[rr] * silu(s) : 0.0f);
-        }
-        *reinterpret_cast<h4*>(sm.VbT + (4 * cgi + c) * kTP + 4 * rg) = vb;
-      }
+      *reinterpret_cast<h4*>(sm.VT + (4 * cgi + c) * kTP + 4 * rg) = vt;
     }
     // upper blocks of the f16 T and score tiles are read by full 32-wide K blocks: keep them zero
     for (int idx = tid; idx < kCH * kCH; idx += kNT) {
       const int t = idx >> 6, tp = idx & 63;
       if ((tp >> 4) > (t >> 4)) {
-        sm.Tf[t * kTP + tp] = (_Float16)0.0f;
+        sm.Tb[t * kTP + tp] = (_Float16)0.0f;
+        sm.Tw[t * kTP + tp] = (_Float16)0.0f;
         sm.Att[t * kTP + tp] = (_Float16)0.0f;
       }
     }
@@ -270,12 +289,12 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       for (int ks = 0; ks < 4; ks++)
         acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
       const int tp = 16 * tj + c16;
-      const float gp = __shfl(gcr, tp);
+      const float gp_ = __shfl(gcr, tp);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int t = 16 * ti + 4 * grp + e;
         // lane shuffles stay outside the masks: a shuffle in divergent code reads inactive lanes
-        const float dec = __expf(fminf(__shfl(gcr, t) - gp, 0.0f)), bt = __shfl(btr, t);
+        const float dec = __expf(fminf(__shfl(gcr, t) - gp_, 0.0f)), bt = __shfl(btr, t);
         if (!isq)
           sm.Tm[t * kAP + tp] = tp < t ? bt * acc[e] * dec : 0.0f;
         else
@@ -284,12 +303,16 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
     }
     __syncthreads();
 
-    // ---- 3a. diagonal 16x16 blocks of T (wave 0, fp32 forward substitution); q^ S on the other waves ----
+    // column factors of T diag(beta) and T diag(beta e^gc) for column c16 of block grp
+    const int colc = 16 * grp + c16;
+    const float cb = __shfl(btr, colc), cbw = cb * __expf(__shfl(gcr, colc));
+
+    // ---- 3a. diagonal 16x16 blocks of T (wave 0); q^ S on the other waves ----
     h8 S16[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++) S16[kb] = pack_b(S[2 * kb], S[2 * kb + 1]);
     f4 O[4];
     auto q_times_s = [&]() {
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) S16[kb] = pack_b(S[2 * kb], S[2 * kb + 1]);
 #pragma unroll
       for (int ti = 0; ti < 4; ti++) {
         f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -299,27 +322,28 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       }
     };
     if (w == 0) {
-      // lane (grp, c16) solves column c16 of diagonal block grp: x_r = [r == c] - sum_{j<r} A_rj x_j
+      // lane (grp, c16) computes column c16 of diagonal block grp, right-looking: after x_j is final, every
+      // later row r subtracts A_rj x_j (A's column j read from LDS as it is needed)
       const int base = 16 * grp;
-      float xc[16];
+      float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        float s = r == c16 ? 1.0f : 0.0f;
-        const float* arow = sm.Tm + (base + r) * kAP + base;
+      for (int r = 0; r < 16; r++) p[r] = r == c16 ? 1.0f : 0.0f;
 #pragma unroll
-        for (int j = 0; j < r; j++) s = fmaf(-arow[j], xc[j], s);
-        xc[r] = s;
+      for (int j = 0; j < 15; j++) {
+#pragma unroll
+        for (int r = j + 1; r < 16; r++) p[r] = fmaf(-sm.Tm[(base + r) * kAP + base + j], p[j], p[r]);
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        sm.Tm[(base + r) * kAP + base + c16] = xc[r];
-        sm.Tf[(base + r) * kTP + base + c16] = (_Float16)xc[r];
+        sm.Tm[(base + r) * kAP + base + c16] = p[r];
+        sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(p[r] * cb);
+        sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(p[r] * cbw);
       }
     } else {
       q_times_s();
     }
     __syncthreads();
-    if (w == 0) q_times_s();
 
     // ---- 3b. off-diagonal blocks: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, block rows in order ----
     for (int bi = 1; bi < 4; bi++) {
@@ -339,6 +363,8 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       __syncthreads();
       if (w < bi) {
         const int j = w;
+        const int col = 16 * j + c16;
+        const float fb = __shfl(btr, col), fw = fb * __expf(__shfl(gcr, col));
         f4 Y = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -348,45 +374,51 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         }
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const int t = 16 * bi + 4 * grp + e, tp = 16 * j + c16;
-          sm.Tm[t * kAP + tp] = -Y[e];
-          sm.Tf[t * kTP + tp] = (_Float16)(-Y[e]);
+          const int t = 16 * bi + 4 * grp + e;
+          sm.Tm[t * kAP + col] = -Y[e];
+          sm.Tb[t * kTP + col] = (_Float16)(-Y[e] * fb);
+          sm.Tw[t * kTP + col] = (_Float16)(-Y[e] * fw);
         }
       }
       __syncthreads();
     }
+    if (w == 0) q_times_s();
 
-    // ---- 4. U = T (beta v) for this wave's columns (registers); W = T (beta e^gc k^) -> -W in LDS ----
-    f4 U[4];
+    // ---- 4-5. U = T diag(beta) v; V_new = U - T diag(beta e^gc) (k^ S); o += scores V_new; S update ----
+    // the next chunk's raw rows and gates load from here on, behind the state update and the epilogue
+    fetch(c0 + kCH);
+    f4 Vn[4];
+    {
+      // k^ S for this wave's columns (S16 still holds S), as a B operand over t
+      h8 KSb[2];
+      f4 ksd[4];
 #pragma unroll
-    for (int ti = 0; ti < 4; ti++) {
-      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, wacc = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int ti = 0; ti < 4; ti++) {
+        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int kb = 0; kb <= (ti >> 1); kb++) {
-        const h8 ta = *reinterpret_cast<const h8*>(sm.Tf + (16 * ti + c16) * kTP + 32 * kb + 8 * grp);
-        acc = mfma16(ta, *reinterpret_cast<const h8*>(sm.VbT + (16 * w + c16) * kTP + 32 * kb + 8 * grp), acc);
-        wacc = mfma16(ta, *reinterpret_cast<const h8*>(sm.KbT + (16 * w + c16) * kTP + 32 * kb + 8 * grp), wacc);
+        for (int kb = 0; kb < 4; kb++) acc = mfma16(perm_a(sm.Ks, kQP, 16 * ti + c16, kb, grp), S16[kb], acc);
+        ksd[ti] = acc;
       }
-      U[ti] = acc;
+      KSb[0] = pack_b(ksd[0], ksd[1]);
+      KSb[1] = pack_b(ksd[2], ksd[3]);
+      const int col = 16 * w + c16;
 #pragma unroll
-      for (int e = 0; e < 4; e++) sm.Ws[(16 * ti + 4 * grp + e) * kQP + 16 * w + c16] = (_Float16)(-wacc[e]);
+      for (int ti = 0; ti < 4; ti++) {
+        f4 u = {0.0f, 0.0f, 0.0f, 0.0f}, ws = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb <= (ti >> 1); kb++) {
+          u = mfma16(*reinterpret_cast<const h8*>(sm.Tb + (16 * ti + c16) * kTP + 32 * kb + 8 * grp),
+                     *reinterpret_cast<const h8*>(sm.VT + col * kTP + 32 * kb + 8 * grp), u);
+          ws = mfma16(perm_a(sm.Tw, kTP, 16 * ti + c16, kb, grp), KSb[kb], ws);
+        }
+        Vn[ti] = u - ws;
+      }
     }
-    // row decay of the inter-chunk output term: o_t += e^gc_t (q^ S)_t
+    // o_t = e^gc_t (q^ S)_t + scores V_new
 #pragma unroll
     for (int ti = 0; ti < 4; ti++)
 #pragma unroll
       for (int e = 0; e < 4; e++) O[ti][e] *= __expf(__shfl(gcr, 16 * ti + 4 * grp + e));
-    __syncthreads();
-
-    // ---- 5. V_new = U - W S; o += scores V_new; S <- e^gl S + (e^(gl-gc) k^)^T V_new ----
-    f4 Vn[4];
-#pragma unroll
-    for (int ti = 0; ti < 4; ti++) {
-      f4 acc = U[ti];
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++) acc = mfma16(perm_a(sm.Ws, kQP, 16 * ti + c16, kb, grp), S16[kb], acc);
-      Vn[ti] = acc;
-    }
     const h8 Vb0 = pack_b(Vn[0], Vn[1]), Vb1 = pack_b(Vn[2], Vn[3]);
 #pragma unroll
     for (int ti = 0; ti < 4; ti++) {
@@ -394,12 +426,19 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       if (ti >= 2) O[ti] = mfma16(perm_a(sm.Att, kTP, 16 * ti + c16, 1, grp), Vb1, O[ti]);
     }
     if (full) {
+      // rows of V_new scaled by e^(gl - gc_t), then S <- e^gl S + k^T (scaled V_new)
+      f4 Vd[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ti++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) Vd[ti][e] = Vn[ti][e] * __expf(gl - __shfl(gcr, 16 * ti + 4 * grp + e));
+      const h8 Vd0 = pack_b(Vd[0], Vd[1]), Vd1 = pack_b(Vd[2], Vd[3]);
       const float el = __expf(gl);
 #pragma unroll
       for (int it = 0; it < 8; it++) {
         f4 acc = S[it] * el;
-        acc = mfma16(perm_a(sm.KdT, kTP, 16 * it + c16, 0, grp), Vb0, acc);
-        acc = mfma16(perm_a(sm.KdT, kTP, 16 * it + c16, 1, grp), Vb1, acc);
+        acc = mfma16(perm_a(sm.KT, kTP, 16 * it + c16, 0, grp), Vd0, acc);
+        acc = mfma16(perm_a(sm.KT, kTP, 16 * it + c16, 1, grp), Vd1, acc);
         S[it] = acc;
       }
     }
@@ -410,32 +449,32 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       for (int ti = 0; ti < 4; ti++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          float s = O[ti][e] * O[ti][e];
+          float sq = O[ti][e] * O[ti][e];
 #pragma unroll
-          for (int d = 1; d < 16; d <<= 1) s += __shfl_xor(s, d);
-          if (c16 == 0) sm.red[(16 * ti + 4 * grp + e) * kNW + w] = s;
+          for (int d = 1; d < 16; d <<= 1) sq += __shfl_xor(sq, d);
+          if (c16 == 0) sm.red[(16 * ti + 4 * grp + e) * kNW + w] = sq;
         }
       __syncthreads();
       if (tid < kCH) {
-        float s = 0.0f;
+        float sq = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kNW; k++) s += sm.red[tid * kNW + k];
-        sm.inv[tid] = rsqrtf(s / kDV + 1e-6f);
+        for (int k = 0; k < kNW; k++) sq += sm.red[tid * kNW + k];
+        sm.inv[tid] = rsqrtf(sq / kDV + 1e-6f);
       }
       __syncthreads();
     }
     const int j = 16 * w + c16;
-    const float gw = a.gnorm ? a.gnorm[j] : 1.0f;
+    const float gw = a.gnorm ? gp<float>(a.gnorm)[j] : 1.0f;
+    __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + j;
 #pragma unroll
     for (int ti = 0; ti < 4; ti++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int t = 16 * ti + 4 * grp + e, r = c0 + t;
         if (t < m && r >= a.P) {
-          const T* row = static_cast<const T*>(a.in) + ((size_t)b * a.L + (r - a.P)) * a.stride;
           float y = O[ti][e];
-          if (a.gnorm) y = gw * y * sm.inv[t] * silu((float)row[a.C + h * kDV + j]);
-          static_cast<T*>(a.out)[((size_t)b * a.L + (r - a.P)) * (size_t)(a.H * kDV) + (size_t)h * kDV + j] = (T)y;
+          if (a.gnorm) y = gw * y * sm.inv[t] * silu(zr[ti][e]);
+          ob[(size_t)(r - a.P) * (a.H * kDV)] = (T)y;
         }
       }
     __syncthreads();  // every wave is done with this chunk's LDS tiles before the next chunk writes them
@@ -444,7 +483,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   for (int it = 0; it < 8; it++)
 #pragma unroll
     for (int e = 0; e < 4; e++)
-      a.S_out[sbase + (size_t)(16 * it + 4 * grp + e) * kDV + 16 * w + c16] = S[it][e];
+      gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * ((tid0 & 63) >> 4) + e) * kDV + 16 * w + (tid0 & 15)] = S[it][e];
 }
 
 template <typename T>
