@@ -11,15 +11,21 @@
 //   S  <- exp(gc_63) S + k^T diag(exp(gc_63 - gc)) V_new                 (complete chunks only)
 //
 // One workgroup of 8 waves per (sequence, head) walks the chunks in order; the fp32 state stays in MFMA
-// accumulator registers for the whole call (wave w owns value columns 16w..16w+15). Per chunk:
-//   1. conv (4 taps) + SiLU of raw rows fetched one chunk ahead (their loads overlap the previous chunk's state
-//      update), l2 norms by 16-lane reductions, gates by a 64-lane scan; f16 tiles of q^, k^, k^T and v^T in LDS
-//      (the per-row gate factors are applied to T's columns and V_new's rows instead of to copies of k);
+// accumulator registers for the whole call (wave w owns value columns 16w..16w+15). Five workgroup barriers per
+// chunk separate:
+//   1. conv (4 taps) + SiLU of raw rows fetched one chunk ahead (their loads overlap the previous chunk's solve and
+//      state update), l2 norms by 16-lane DPP reductions -> f16 tiles of q^, k^, k^T and v^T in LDS; one wave turns
+//      the a/b columns into the chunk's gate vectors (cumulative log decay, e^gc, beta, e^(gc_63 - gc)) in LDS. The
+//      per-row gate factors go onto T's columns and V_new's rows instead of onto copies of k;
 //   2. K K^T and Q K^T on v_mfma_f32_16x16x32_f16 -> A (fp32) and the decay-masked scores (f16);
-//   3. T: right-looking fp32 substitution on the four 16x16 diagonal blocks (one wave) and fp32 MFMA (16x16x4) for
-//      the off-diagonal blocks, while the other waves compute q^ S; T diag(beta), T diag(beta e^gc) stored f16;
-//   4-5. U, k^ S, V_new, o and the state update on f16 MFMA with fp32 accumulation, S as f16 B operands built in
-//      registers; 6. gated RMSNorm epilogue (GNORM) and the store.
+//   3. T = (I + A)^-1: one wave solves the four 16x16 diagonal blocks (left-looking, A rows read as LDS
+//      broadcasts) while the others compute q^ S and k^ S; then waves 0..2 each own one block column of the
+//      off-diagonal blocks (fp32 MFMA 16x16x4, the column kept in registers), with no barrier between block rows;
+//      T diag(beta) and T diag(beta e^gc) are stored f16;
+//   4. V_new = T diag(beta) v - T diag(beta e^gc) (k^ S), o and the state update on f16 MFMA with fp32
+//      accumulation, S as f16 B operands built in registers; 5. gated RMSNorm epilogue (GNORM) and the store.
+// Memory is addressed from wave-uniform (SGPR) row bases plus 32-bit lane offsets on the common path (chunks with
+// no replay rows and no rows past the end); the first and last chunk of a call take a general path.
 // Chunk boundaries sit at s0 + 64k, so a row is processed identically however a sequence is split into calls;
 // only complete chunks advance the stored state.
 //
@@ -41,24 +47,54 @@ constexpr int kDK = 128, kDV = 128, kCH = 64, kKC = 4, kNW = 8, kNT = 64 * kNW;
 constexpr int kQP = kDK + 8;  // row pitch (halves) of [64][128] f16 tiles
 constexpr int kTP = kCH + 8;  // row pitch (halves) of [*][64] f16 tiles
 constexpr int kAP = kCH + 4;  // row pitch (floats) of the fp32 A / T tile
+constexpr int kGW = kNW - 1;  // the wave that computes the gate vectors and the diagonal blocks of T
 
 struct Lds {
   _Float16 Qs[kCH * kQP];   // q^ / sqrt(DK), [t][i]
   _Float16 Ks[kCH * kQP];   // k^, [t][i]
-  _Float16 KT[kDK * kTP];   // k^ transposed, [i][t]
-  _Float16 VT[kDV * kTP];   // v transposed, [j][t]
+  _Float16 KT[kDK * kTP];   // k^ transposed, [i][t], 4-column groups swizzled by kt_at
+  _Float16 VT[kDV * kTP];   // v transposed, [j][t], 4-column groups swizzled by vt_at
   _Float16 Tb[kCH * kTP];   // T diag(beta), f16, [t][t']
   _Float16 Tw[kCH * kTP];   // T diag(beta e^gc), f16
   _Float16 Att[kCH * kTP];  // decay-masked causal q^ k^T, [t][t']
   float Tm[kCH * kAP];      // A, then T, fp32
-  float Xs[3 * 256];        // off-diagonal solve scratch
-  float cw[3 * 128][kKC];   // this head's conv taps (q, k, v channels)
-  float red[kCH * kNW];     // gated-norm partial sums
-  float inv[kCH];
+  // this head's conv taps, laid out so that the 32 conv lanes of a half wave read consecutive 16-byte entries:
+  // q/k channel 8 g + c (g < 32: q then k) at cwq[c][g], v channel 4 g + c at cwv[c][g]
+  float cwq[8][32][kKC];
+  float cwv[4][32][kKC];
+  float gc[kCH];            // cumulative log decay inside the chunk
+  float eg[kCH];            // e^gc
+  float bt[kCH];            // beta
+  float ed[kCH];            // e^(gc_63 - gc)
+  float red[kCH * kNW];     // gated-norm partial sums, [t][wave]
+  float inv[kNW][kCH];      // per-wave copy of the row inverse norms
 };
 
 // SiLU / sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE division sequence
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15) with row rotations; every lane gets the sum.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
+  return v;
+}
+
+// Orders a wave's LDS writes before its later reads of other lanes' entries (no workgroup barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// An identity the compiler cannot see through: per-lane indices re-derived from it every chunk keep the address
+// arithmetic built on them inside the chunk loop instead of being hoisted out of it and spilled.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 // Global (address space 1) pointers: loads through them are global_load_*, not flat_load_*, so they are not
 // counted by the LDS wait counter and outstanding global loads do not stall LDS traffic.
@@ -101,6 +137,20 @@ __device__ __forceinline__ h8 perm_a(const _Float16* base, int pitch, int r, int
   return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// Transposed tiles are written one 4-row strip per lane (8 bytes) down the rows of the transpose, which would put
+// the lanes of a write 8 (k^T) or 4 (v^T) rows apart and in the same banks; the 4-column group index is XORed
+// with a function of the row so those writes spread over the banks. Element (row, col) lives at
+// row * kTP + 4 * (col / 4 ^ f(row)) + col % 4. For v^T, f is even, so 8-column (16-byte) reads stay contiguous.
+__device__ __forceinline__ int kt_at(int i, int g4) { return i * kTP + 4 * (g4 ^ ((i >> 3) & 15)); }
+__device__ __forceinline__ int vt_at(int j, int g4) { return j * kTP + 4 * (g4 ^ (2 * ((j >> 4) & 7))); }
+
+// perm_a for the swizzled k^T tile
+__device__ __forceinline__ h8 perm_a_kt(const _Float16* kt, int r, int kb, int grp) {
+  const h4 lo = *reinterpret_cast<const h4*>(kt + kt_at(r, 8 * kb + grp));
+  const h4 hi = *reinterpret_cast<const h4*>(kt + kt_at(r, 8 * kb + 4 + grp));
+  return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // Two D tiles (rows 32kb..32kb+15 and 32kb+16..+31 of a column) as one f16 B operand.
 __device__ __forceinline__ h8 pack_b(const f4& x, const f4& y) {
   return h8{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3],
@@ -111,9 +161,42 @@ __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
+__device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+
+// Block column J of T below the diagonal: T_iJ = -T_ii sum_{k=J}^{i-1} A_ik T_kJ for block rows i = J+1..3, in
+// order. The column's blocks stay in registers (D layout: rows 4 grp + e, column c16), so A is never overwritten
+// and the three column waves need no barrier between block rows; only the f16 copies T diag(beta) and
+// T diag(beta e^gc) are stored. The D layout is used directly as the B operand of v_mfma_f32_16x16x4f32 by giving
+// step e the K index 4 grp + e, and the A operand is read in the same order.
+template <int J>
+__device__ __forceinline__ void t_column(Lds& sm, int grp, int c16) {
+  const int cj = 16 * J + c16;
+  const float fb = sm.bt[cj], fw = fb * sm.eg[cj];
+  f4 Tc[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) Tc[J][e] = sm.Tm[(16 * J + 4 * grp + e) * kAP + cj];
+#pragma unroll
+  for (int bi = J + 1; bi < 4; bi++) {
+    const float* arow = &sm.Tm[(16 * bi + c16) * kAP];
+    f4 X = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = J; k < bi; k++) {
+      const f4 av = lds4(arow + 16 * k + 4 * grp);
+#pragma unroll
+      for (int e = 0; e < 4; e++) X = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[k][e], X, 0, 0, 0);
+    }
+    const f4 tv = lds4(arow + 16 * bi + 4 * grp);
+    f4 Y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 4; e++) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(tv[e], X[e], Y, 0, 0, 0);
+    Tc[bi] = -Y;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int t = 16 * bi + 4 * grp + e;
+      sm.Tb[t * kTP + cj] = (_Float16)(Tc[bi][e] * fb);
+      sm.Tw[t * kTP + cj] = (_Float16)(Tc[bi][e] * fw);
+    }
+  }
 }
 
 template <typename T>
@@ -124,6 +207,8 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
   const int end = a.P + a.L;
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
+  const unsigned rowb = (unsigned)a.stride * sizeof(T);         // bytes per input row
+  const unsigned orowb = (unsigned)(a.H * kDV) * sizeof(T);     // bytes per output row
 
   // state: S[it][e] = S[16 it + 4 grp + e][16 w + c16]
   f4 S[8];
@@ -138,106 +223,141 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   for (int i = tid0; i < 3 * 128 * kKC; i += kNT) {
     const int lc = i / kKC, j = i % kKC;
     const int ch = lc < 128 ? h * kDK + lc : lc < 256 ? a.H * kDK + h * kDK + (lc - 128) : 2 * a.H * kDK + h * kDV + (lc - 256);
-    sm.cw[lc][j] = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
+    const float v = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
+    if (lc < 256)
+      sm.cwq[lc & 7][lc >> 3][j] = v;
+    else
+      sm.cwv[(lc - 256) & 3][(lc - 256) >> 2][j] = v;
   }
-
+  // blocks above the diagonal of the f16 T and score tiles are read by full 32-wide K blocks and never written
+  for (int idx = tid0; idx < kCH * kCH; idx += kNT) {
+    const int t = idx >> 6, tp = idx & 63;
+    if ((tp >> 4) > (t >> 4)) {
+      sm.Tb[t * kTP + tp] = (_Float16)0.0f;
+      sm.Tw[t * kTP + tp] = (_Float16)0.0f;
+      sm.Att[t * kTP + tp] = (_Float16)0.0f;
+    }
+  }
   const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
   const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
+  const float gw = a.gnorm ? gp<float>(a.gnorm)[16 * w + (tid0 & 15)] : 1.0f;
 
-  // raw rows of a chunk (and its a/b gate inputs), fetched one chunk ahead; rows past the end read as 0, so the
-  // fetch is unconditional and the previous chunk's rows are dead once it is issued
-  float x[7][8], xv[7][4], ga, gb;
-  __syncthreads();  // conv taps visible
+  // raw rows of a chunk (and, on the gate wave, its a/b inputs), fetched one chunk ahead
+  float x[7][8], xv[7][4], ga = 0.0f, gb = 0.0f;
+  __syncthreads();  // conv taps and zero blocks visible
 
   for (int c0 = a.s0; c0 < end; c0 += kCH) {
     const int m = min(kCH, end - c0);
     const bool full = m == kCH;
-    // per-lane indices re-derived every chunk through an opaque copy: address arithmetic built on them stays in
-    // the loop instead of being hoisted out of it and spilled
     const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
     // conv tasks: rows 4 rg .. 4 rg + 3 of the chunk; 8 q-or-k channels and 4 v channels
     const int rg = tid >> 5, cgi = tid & 31, qk = cgi >> 4, cg = cgi & 15;
-    const int chq = (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, lq = qk * 128 + 8 * cg;
-    const int chv = 2 * a.H * kDK + h * kDV + 4 * cgi, lv = 256 + 4 * cgi;
+    const int chq = (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, chv = 2 * a.H * kDK + h * kDV + 4 * cgi;
 
-    // raw rows of a chunk (and its a/b gate inputs), fetched one chunk ahead; rows past the end read as 0, so the
-    // fetch is unconditional and the previous chunk's rows are dead once it is issued
+    // rows cs-3 .. cs+63 of every sequence; rows past the end read as 0
     auto fetch = [&](int cs) {
-      const bool fresh = cs - (kKC - 1) >= a.P;  // no row of this chunk (incl. its conv history) is a replay row
-      const gptr<T> base = gp<T>(a.in) + ((ptrdiff_t)b * a.L + (cs - a.P)) * a.stride;
-  #pragma unroll
-      for (int i = 0; i < 7; i++) {
-        const int r = cs + 4 * rg - 3 + i, rc = min(r, end - 1);
-        const gptr<T> row = fresh ? base + (ptrdiff_t)(rc - cs) * a.stride : row_of<T>(a, b, rc);
-        load8(row + chq, x[i]);
-        load4(row + chv, xv[i]);
-        if (r >= end) {
-  #pragma unroll
-          for (int c = 0; c < 8; c++) x[i][c] = 0.0f;
-  #pragma unroll
-          for (int c = 0; c < 4; c++) xv[i][c] = 0.0f;
+      if (cs - (kKC - 1) >= a.P && cs + kCH <= end) {
+        // common path: all 67 rows come from `in`; uniform row bases, 32-bit lane offsets
+        const char* base = (const char*)a.in + ((size_t)b * a.L + (cs - (kKC - 1) - a.P)) * (size_t)rowb;
+        const unsigned oq = 4u * rg * rowb + chq * (unsigned)sizeof(T), ov = 4u * rg * rowb + chv * (unsigned)sizeof(T);
+#pragma unroll
+        for (int i = 0; i < 7; i++) {
+          const char* rb = base + (size_t)i * rowb;
+          load8(gp<T>(rb + oq), x[i]);
+          load4(gp<T>(rb + ov), xv[i]);
+        }
+        if (w == kGW) {
+          const char* gb0 = base + (size_t)(kKC - 1) * rowb;
+          const unsigned og = (unsigned)lane * rowb;
+          ga = (float)*gp<T>(gb0 + og + aoff * sizeof(T));
+          gb = (float)*gp<T>(gb0 + og + boff * sizeof(T));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 7; i++) {
+          const int r = cs + 4 * rg - 3 + i, rc = min(r, end - 1);
+          const gptr<T> row = row_of<T>(a, b, rc);
+          load8(row + chq, x[i]);
+          load4(row + chv, xv[i]);
+          if (r >= end) {
+#pragma unroll
+            for (int c = 0; c < 8; c++) x[i][c] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) xv[i][c] = 0.0f;
+          }
+        }
+        if (w == kGW) {
+          const gptr<T> grow = row_of<T>(a, b, min(cs + lane, end - 1));
+          ga = cs + lane < end ? (float)grow[aoff] : 0.0f;
+          gb = cs + lane < end ? (float)grow[boff] : 0.0f;
         }
       }
-      const gptr<T> grow = row_of<T>(a, b, min(cs + lane, end - 1));
-      ga = cs + lane < end ? (float)grow[aoff] : 0.0f;
-      gb = cs + lane < end ? (float)grow[boff] : 0.0f;
     };
     if (c0 == a.s0) fetch(c0);
 
     // z of this chunk for the gated-norm epilogue, in flight during the whole chunk
+    const bool plain = c0 >= a.P && full;  // no replay rows, no rows past the end
     float zr[4][4];
-    {
+    if (plain) {
+      const char* zb = (const char*)a.in + ((size_t)b * a.L + (c0 - a.P)) * (size_t)rowb + (a.C + h * kDV) * sizeof(T);
+      const unsigned oz = 4u * grp * rowb + (16 * w + c16) * (unsigned)sizeof(T);
+#pragma unroll
+      for (int ti = 0; ti < 4; ti++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) zr[ti][e] = (float)*gp<T>(zb + (size_t)(16 * ti + e) * rowb + oz);
+    } else {
       const gptr<T> zb = gp<T>(a.in) + (size_t)b * a.L * a.stride + a.C + h * kDV + 16 * w + c16;
 #pragma unroll
       for (int ti = 0; ti < 4; ti++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const int t = 16 * ti + 4 * grp + e, r = c0 + t;
-          const int rr = min(max(r - a.P, 0), a.L - 1);
+          const int rr = min(max(c0 + 16 * ti + 4 * grp + e - a.P, 0), a.L - 1);
           zr[ti][e] = (float)zb[(size_t)rr * a.stride];
         }
     }
 
-    // ---- 1. gates: every wave holds all 64 rows (lane = row) in registers, read by lane shuffles ----
-    float gcr = 0.0f, btr = 0.0f;
-    if (lane < m) {
-      btr = __builtin_amdgcn_rcpf(1.0f + __expf(-gb));
-      const float xs = ga + db;
-      gcr = na * (xs > 20.0f ? xs : log1pf(__expf(xs)));
-    }
+    // ---- 1. gate vectors (one wave, lane = row), conv + SiLU + norms (all waves) ----
+    if (w == kGW) {
+      float gcr = 0.0f, btr = 0.0f;
+      if (lane < m) {
+        btr = __builtin_amdgcn_rcpf(1.0f + __expf(-gb));
+        const float xs = ga + db;
+        gcr = na * (xs > 20.0f ? xs : log1pf(__expf(xs)));
+      }
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float o = __shfl_up(gcr, d);
-      if (lane >= d) gcr += o;
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(gcr, d);
+        if (lane >= d) gcr += o;
+      }
+      const float gl = __shfl(gcr, 63);
+      sm.gc[lane] = gcr;
+      sm.eg[lane] = __expf(gcr);
+      sm.bt[lane] = btr;
+      sm.ed[lane] = __expf(gl - gcr);
     }
-    const float gl = __shfl(gcr, 63);
-
-    // conv + SiLU + l2 norm of 8 q-or-k channels over 4 rows -> q^ / k^ rows, k^ transposed
     {
-      float u[4][8], rs[4];
+      float u[4][8], ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        const bool valid = 4 * rg + rr < m;
-        float ss = 0.0f;
+      for (int c = 0; c < 8; c++) {
+        const f4 wc = lds4(sm.cwq[c][cgi]);
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-          const float* wc = sm.cw[lq + c];
+        for (int rr = 0; rr < 4; rr++) {
           float sv = wc[0] * x[rr][c];
           sv = fmaf(wc[1], x[rr + 1][c], sv);
           sv = fmaf(wc[2], x[rr + 2][c], sv);
           sv = fmaf(wc[3], x[rr + 3][c], sv);
-          u[rr][c] = valid ? silu(sv) : 0.0f;
-          ss = fmaf(u[rr][c], u[rr][c], ss);
+          u[rr][c] = 4 * rg + rr < m ? silu(sv) : 0.0f;
+          ss[rr] = fmaf(u[rr][c], u[rr][c], ss[rr]);
         }
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) ss += __shfl_xor(ss, d);
-        rs[rr] = rsqrtf(ss + 1e-6f) * (qk ? 1.0f : qscale);
       }
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) {
+        const float rs = rsqrtf(row_sum16(ss[rr]) + 1e-6f) * (qk ? 1.0f : qscale);
+#pragma unroll
+        for (int c = 0; c < 8; c++) u[rr][c] *= rs;
         h8 hv;
 #pragma unroll
-        for (int c = 0; c < 8; c++) hv[c] = (_Float16)(u[rr][c] * rs[rr]);
+        for (int c = 0; c < 8; c++) hv[c] = (_Float16)u[rr][c];
         *reinterpret_cast<h8*>((qk ? sm.Ks : sm.Qs) + (4 * rg + rr) * kQP + 8 * cg) = hv;
       }
       if (qk) {
@@ -245,15 +365,14 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         for (int c = 0; c < 8; c++) {
           h4 kt;
 #pragma unroll
-          for (int rr = 0; rr < 4; rr++) kt[rr] = (_Float16)(u[rr][c] * rs[rr]);
-          *reinterpret_cast<h4*>(sm.KT + (8 * cg + c) * kTP + 4 * rg) = kt;
+          for (int rr = 0; rr < 4; rr++) kt[rr] = (_Float16)u[rr][c];
+          *reinterpret_cast<h4*>(sm.KT + kt_at(8 * cg + c, rg)) = kt;
         }
       }
     }
-    // conv + SiLU of 4 v channels over 4 rows -> v^T
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float* wc = sm.cw[lv + c];
+      const f4 wc = lds4(sm.cwv[c][cgi]);
       h4 vt;
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) {
@@ -263,18 +382,9 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         sv = fmaf(wc[3], xv[rr + 3][c], sv);
         vt[rr] = (_Float16)(4 * rg + rr < m ? silu(sv) : 0.0f);
       }
-      *reinterpret_cast<h4*>(sm.VT + (4 * cgi + c) * kTP + 4 * rg) = vt;
+      *reinterpret_cast<h4*>(sm.VT + vt_at(4 * cgi + c, rg)) = vt;
     }
-    // upper blocks of the f16 T and score tiles are read by full 32-wide K blocks: keep them zero
-    for (int idx = tid; idx < kCH * kCH; idx += kNT) {
-      const int t = idx >> 6, tp = idx & 63;
-      if ((tp >> 4) > (t >> 4)) {
-        sm.Tb[t * kTP + tp] = (_Float16)0.0f;
-        sm.Tw[t * kTP + tp] = (_Float16)0.0f;
-        sm.Att[t * kTP + tp] = (_Float16)0.0f;
-      }
-    }
-    __syncthreads();
+    __syncthreads();  // B1
 
     // ---- 2. K K^T -> A (fp32), Q K^T -> decay-masked scores (f16); the 10 lower 16x16 tiles of each ----
     for (int job = w; job < 20; job += kNW) {
@@ -288,52 +398,56 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
 #pragma unroll
       for (int ks = 0; ks < 4; ks++)
         acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
-      const int tp = 16 * tj + c16;
-      const float gp_ = __shfl(gcr, tp);
+      const int tp = 16 * tj + c16, t0 = 16 * ti + 4 * grp;
+      const float gp_ = sm.gc[tp];
+      const f4 gt = lds4(&sm.gc[t0]), bt = lds4(&sm.bt[t0]);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const int t = 16 * ti + 4 * grp + e;
-        // lane shuffles stay outside the masks: a shuffle in divergent code reads inactive lanes
-        const float dec = __expf(fminf(__shfl(gcr, t) - gp_, 0.0f)), bt = __shfl(btr, t);
+        const int t = t0 + e;
+        const float dec = __expf(fminf(gt[e] - gp_, 0.0f));
         if (!isq)
-          sm.Tm[t * kAP + tp] = tp < t ? bt * acc[e] * dec : 0.0f;
+          sm.Tm[t * kAP + tp] = tp < t ? bt[e] * acc[e] * dec : 0.0f;
         else
           sm.Att[t * kTP + tp] = (_Float16)(tp <= t ? acc[e] * dec : 0.0f);
       }
     }
-    __syncthreads();
+    __syncthreads();  // B2
 
-    // column factors of T diag(beta) and T diag(beta e^gc) for column c16 of block grp
-    const int colc = 16 * grp + c16;
-    const float cb = __shfl(btr, colc), cbw = cb * __expf(__shfl(gcr, colc));
-
-    // ---- 3a. diagonal 16x16 blocks of T (wave 0); q^ S on the other waves ----
-    h8 S16[4];
+    // ---- 3. T = (I + A)^-1; q^ S and k^ S ----
+    h8 S16[4], KSb[2];
     f4 O[4];
-    auto q_times_s = [&]() {
+    auto qk_times_s = [&]() {
 #pragma unroll
       for (int kb = 0; kb < 4; kb++) S16[kb] = pack_b(S[2 * kb], S[2 * kb + 1]);
+      f4 ksd[4];
 #pragma unroll
       for (int ti = 0; ti < 4; ti++) {
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acck = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++) acc = mfma16(perm_a(sm.Qs, kQP, 16 * ti + c16, kb, grp), S16[kb], acc);
+        for (int kb = 0; kb < 4; kb++) {
+          acc = mfma16(perm_a(sm.Qs, kQP, 16 * ti + c16, kb, grp), S16[kb], acc);
+          acck = mfma16(perm_a(sm.Ks, kQP, 16 * ti + c16, kb, grp), S16[kb], acck);
+        }
         O[ti] = acc;
+        ksd[ti] = acck;
       }
+      KSb[0] = pack_b(ksd[0], ksd[1]);
+      KSb[1] = pack_b(ksd[2], ksd[3]);
     };
-    if (w == 0) {
-      // lane (grp, c16) computes column c16 of diagonal block grp, right-looking: after x_j is final, every
-      // later row r subtracts A_rj x_j (A's column j read from LDS as it is needed)
+    if (w == kGW) {
+      // lane (grp, c16): column c16 of diagonal block grp, rows in order (left-looking); row r of A is read as a
+      // broadcast shared by the 16 lanes of the block
       const int base = 16 * grp;
       float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; r++) p[r] = r == c16 ? 1.0f : 0.0f;
+      for (int r = 0; r < 16; r++) {
+        const float* ar = &sm.Tm[(base + r) * kAP + base];
+        float acc = r == c16 ? 1.0f : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 15; j++) {
-#pragma unroll
-        for (int r = j + 1; r < 16; r++) p[r] = fmaf(-sm.Tm[(base + r) * kAP + base + j], p[j], p[r]);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < r; j++) acc = fmaf(-ar[j], p[j], acc);
+        p[r] = acc;
       }
+      const float cb = sm.bt[base + c16], cbw = cb * sm.eg[base + c16];
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         sm.Tm[(base + r) * kAP + base + c16] = p[r];
@@ -341,84 +455,37 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(p[r] * cbw);
       }
     } else {
-      q_times_s();
+      qk_times_s();
     }
-    __syncthreads();
-
-    // ---- 3b. off-diagonal blocks: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj, block rows in order ----
-    for (int bi = 1; bi < 4; bi++) {
-      if (w < bi) {
-        const int j = w;
-        f4 X = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int k = j; k < bi; k++)
-#pragma unroll
-          for (int ks = 0; ks < 4; ks++) {
-            const float av = sm.Tm[(16 * bi + c16) * kAP + 16 * k + 4 * ks + grp];
-            const float bv = sm.Tm[(16 * k + 4 * ks + grp) * kAP + 16 * j + c16];
-            X = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, X, 0, 0, 0);
-          }
-#pragma unroll
-        for (int e = 0; e < 4; e++) sm.Xs[j * 256 + (4 * grp + e) * 16 + c16] = X[e];
-      }
-      __syncthreads();
-      if (w < bi) {
-        const int j = w;
-        const int col = 16 * j + c16;
-        const float fb = __shfl(btr, col), fw = fb * __expf(__shfl(gcr, col));
-        f4 Y = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-          const float av = sm.Tm[(16 * bi + c16) * kAP + 16 * bi + 4 * ks + grp];
-          const float bv = sm.Xs[j * 256 + (4 * ks + grp) * 16 + c16];
-          Y = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, Y, 0, 0, 0);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int t = 16 * bi + 4 * grp + e;
-          sm.Tm[t * kAP + col] = -Y[e];
-          sm.Tb[t * kTP + col] = (_Float16)(-Y[e] * fb);
-          sm.Tw[t * kTP + col] = (_Float16)(-Y[e] * fw);
-        }
-      }
-      __syncthreads();
-    }
-    if (w == 0) q_times_s();
-
-    // ---- 4-5. U = T diag(beta) v; V_new = U - T diag(beta e^gc) (k^ S); o += scores V_new; S update ----
-    // the next chunk's raw rows and gates load from here on, behind the state update and the epilogue
+    __syncthreads();  // B3
+    // the next chunk's raw rows load from here on, behind the solve, the state update and the epilogue
     fetch(c0 + kCH);
+    if (w == 0)
+      t_column<0>(sm, grp, c16);
+    else if (w == 1)
+      t_column<1>(sm, grp, c16);
+    else if (w == 2)
+      t_column<2>(sm, grp, c16);
+    else if (w == kGW)
+      qk_times_s();
+    __syncthreads();  // B4
+
+    // ---- 4. V_new = T diag(beta) v - T diag(beta e^gc) (k^ S); o = e^gc (q^ S) + scores V_new; state ----
     f4 Vn[4];
-    {
-      // k^ S for this wave's columns (S16 still holds S), as a B operand over t
-      h8 KSb[2];
-      f4 ksd[4];
+    const int col = 16 * w + c16;
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++) {
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ti = 0; ti < 4; ti++) {
+      f4 u = {0.0f, 0.0f, 0.0f, 0.0f}, ws = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++) acc = mfma16(perm_a(sm.Ks, kQP, 16 * ti + c16, kb, grp), S16[kb], acc);
-        ksd[ti] = acc;
+      for (int kb = 0; kb <= (ti >> 1); kb++) {
+        u = mfma16(*reinterpret_cast<const h8*>(sm.Tb + (16 * ti + c16) * kTP + 32 * kb + 8 * grp),
+                   *reinterpret_cast<const h8*>(sm.VT + vt_at(col, 8 * kb + 2 * grp)), u);
+        ws = mfma16(perm_a(sm.Tw, kTP, 16 * ti + c16, kb, grp), KSb[kb], ws);
       }
-      KSb[0] = pack_b(ksd[0], ksd[1]);
-      KSb[1] = pack_b(ksd[2], ksd[3]);
-      const int col = 16 * w + c16;
-#pragma unroll
-      for (int ti = 0; ti < 4; ti++) {
-        f4 u = {0.0f, 0.0f, 0.0f, 0.0f}, ws = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int kb = 0; kb <= (ti >> 1); kb++) {
-          u = mfma16(*reinterpret_cast<const h8*>(sm.Tb + (16 * ti + c16) * kTP + 32 * kb + 8 * grp),
-                     *reinterpret_cast<const h8*>(sm.VT + col * kTP + 32 * kb + 8 * grp), u);
-          ws = mfma16(perm_a(sm.Tw, kTP, 16 * ti + c16, kb, grp), KSb[kb], ws);
-        }
-        Vn[ti] = u - ws;
-      }
+      Vn[ti] = u - ws;
     }
-    // o_t = e^gc_t (q^ S)_t + scores V_new
 #pragma unroll
-    for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) O[ti][e] *= __expf(__shfl(gcr, 16 * ti + 4 * grp + e));
+    for (int ti = 0; ti < 4; ti++) O[ti] *= lds4(&sm.eg[16 * ti + 4 * grp]);
     const h8 Vb0 = pack_b(Vn[0], Vn[1]), Vb1 = pack_b(Vn[2], Vn[3]);
 #pragma unroll
     for (int ti = 0; ti < 4; ti++) {
@@ -427,57 +494,64 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
     }
     if (full) {
       // rows of V_new scaled by e^(gl - gc_t), then S <- e^gl S + k^T (scaled V_new)
-      f4 Vd[4];
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) Vd[ti][e] = Vn[ti][e] * __expf(gl - __shfl(gcr, 16 * ti + 4 * grp + e));
-      const h8 Vd0 = pack_b(Vd[0], Vd[1]), Vd1 = pack_b(Vd[2], Vd[3]);
-      const float el = __expf(gl);
+      for (int ti = 0; ti < 4; ti++) Vn[ti] *= lds4(&sm.ed[16 * ti + 4 * grp]);
+      const h8 Vd0 = pack_b(Vn[0], Vn[1]), Vd1 = pack_b(Vn[2], Vn[3]);
+      const float el = sm.eg[kCH - 1];
 #pragma unroll
       for (int it = 0; it < 8; it++) {
         f4 acc = S[it] * el;
-        acc = mfma16(perm_a(sm.KT, kTP, 16 * it + c16, 0, grp), Vd0, acc);
-        acc = mfma16(perm_a(sm.KT, kTP, 16 * it + c16, 1, grp), Vd1, acc);
+        acc = mfma16(perm_a_kt(sm.KT, 16 * it + c16, 0, grp), Vd0, acc);
+        acc = mfma16(perm_a_kt(sm.KT, 16 * it + c16, 1, grp), Vd1, acc);
         S[it] = acc;
       }
     }
-
-    // ---- 6. gated RMSNorm over the head's 128 columns and the store ----
     if (a.gnorm) {
 #pragma unroll
       for (int ti = 0; ti < 4; ti++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          float sq = O[ti][e] * O[ti][e];
-#pragma unroll
-          for (int d = 1; d < 16; d <<= 1) sq += __shfl_xor(sq, d);
-          if (c16 == 0) sm.red[(16 * ti + 4 * grp + e) * kNW + w] = sq;
+          const float sq = row_sum16(O[ti][e] * O[ti][e]);
+          if (c16 == 4 * ti + e) sm.red[(16 * ti + 4 * grp + e) * kNW + w] = sq;
         }
-      __syncthreads();
-      if (tid < kCH) {
-        float sq = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kNW; k++) sq += sm.red[tid * kNW + k];
-        sm.inv[tid] = rsqrtf(sq / kDV + 1e-6f);
-      }
-      __syncthreads();
     }
-    const int j = 16 * w + c16;
-    const float gw = a.gnorm ? gp<float>(a.gnorm)[j] : 1.0f;
-    __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + j;
+    __syncthreads();  // B5: every wave is done with this chunk's tiles; the next chunk may overwrite them
+
+    // ---- 5. gated RMSNorm over the head's 128 columns and the store ----
+    f4 iv[4];
+    if (a.gnorm) {
+      const f4 r0 = lds4(&sm.red[lane * kNW]), r1 = lds4(&sm.red[lane * kNW + 4]);
+      const float sq = ((r0[0] + r0[1]) + (r0[2] + r0[3])) + ((r1[0] + r1[1]) + (r1[2] + r1[3]));
+      sm.inv[w][lane] = rsqrtf(sq / kDV + 1e-6f);
+      wave_sync();
 #pragma unroll
-    for (int ti = 0; ti < 4; ti++)
+      for (int ti = 0; ti < 4; ti++) iv[ti] = lds4(&sm.inv[w][16 * ti + 4 * grp]);
+    }
+    if (plain) {
+      char* ob = (char*)a.out + ((size_t)b * a.L + (c0 - a.P)) * (size_t)orowb + (size_t)h * kDV * sizeof(T);
+      const unsigned oo = 4u * grp * orowb + col * (unsigned)sizeof(T);
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int t = 16 * ti + 4 * grp + e, r = c0 + t;
-        if (t < m && r >= a.P) {
+      for (int ti = 0; ti < 4; ti++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
           float y = O[ti][e];
-          if (a.gnorm) y = gw * y * sm.inv[t] * silu(zr[ti][e]);
-          ob[(size_t)(r - a.P) * (a.H * kDV)] = (T)y;
+          if (a.gnorm) y = gw * y * iv[ti][e] * silu(zr[ti][e]);
+          *gpw<T>(ob + (size_t)(16 * ti + e) * orowb + oo) = (T)y;
         }
-      }
-    __syncthreads();  // every wave is done with this chunk's LDS tiles before the next chunk writes them
+    } else {
+      __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + col;
+#pragma unroll
+      for (int ti = 0; ti < 4; ti++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int t = 16 * ti + 4 * grp + e, r = c0 + t;
+          if (t < m && r >= a.P) {
+            float y = O[ti][e];
+            if (a.gnorm) y = gw * y * iv[ti][e] * silu(zr[ti][e]);
+            ob[(size_t)(r - a.P) * (a.H * kDV)] = (T)y;
+          }
+        }
+    }
   }
 #pragma unroll
   for (int it = 0; it < 8; it++)
