@@ -66,9 +66,24 @@ struct Lds {
   float eg[kCH];            // e^gc
   float bt[kCH];            // beta
   float ed[kCH];            // e^(gc_63 - gc)
+  float rowf[kCH];          // e^(gc_t - gc_16(t/16)), in (0, 1]
+  float brow[kCH];          // beta_t rowf_t
+  float colf[3][kCH];       // colf[i-1][t'] = e^(gc_16i - gc_t') for t' < 16 i, in (0, 1]
   float red[kCH * kNW];     // gated-norm partial sums, [t][wave]
   float inv[kNW][kCH];      // per-wave copy of the row inverse norms
 };
+// After the solve, Tm is free until the next chunk's K K^T: each wave stages 32 x 16 floats of its output there.
+static_assert(sizeof(float) * kCH * kAP >= kNW * 32 * 16 * sizeof(float), "staging area");
+
+// Row permutation of the staging area: rows 4 g + e (fixed e) of a D tile land in different quarters of the banks.
+__device__ __forceinline__ int stage_row(int r) { return (r & ~3) | ((r + (r >> 2)) & 3); }
+
+// Quad sums (lanes 4q..4q+3) with DPP quad permutations.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
+  return v;
+}
 
 // SiLU / sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE division sequence
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
@@ -127,6 +142,18 @@ __device__ __forceinline__ void load4(gptr<float> p, float* o) {
 __device__ __forceinline__ void load4(gptr<_Float16> p, float* o) {
   const h4 x = *(gptr<h4>)(p);
   o[0] = (float)x[0]; o[1] = (float)x[1]; o[2] = (float)x[2]; o[3] = (float)x[3];
+}
+
+__device__ __forceinline__ f4 ld4(gptr<float> p) { return *(gptr<f4>)(p); }
+__device__ __forceinline__ f4 ld4(gptr<_Float16> p) {
+  const h4 x = *(gptr<h4>)(p);
+  return f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+}
+__device__ __forceinline__ void store4(__attribute__((address_space(1))) float* p, const f4& v) {
+  *(__attribute__((address_space(1))) f4*)(p) = v;
+}
+__device__ __forceinline__ void store4(__attribute__((address_space(1))) _Float16* p, const f4& v) {
+  *(__attribute__((address_space(1))) h4*)(p) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
 }
 
 // A operand read in the permuted K order matching a D tile pair used as B: row r of a [*][pitch] f16 tile,
@@ -240,7 +267,9 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   }
   const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
   const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
-  const float gw = a.gnorm ? gp<float>(a.gnorm)[16 * w + (tid0 & 15)] : 1.0f;
+  // epilogue layout: lane l holds rows 16 q + l / 4 (q < 4) of columns 16 w + 4 (l % 4) .. +3
+  f4 gw = {1.0f, 1.0f, 1.0f, 1.0f};
+  if (a.gnorm) gw = ld4(gp<float>(a.gnorm) + 16 * w + 4 * (tid0 & 3));
 
   // raw rows of a chunk (and, on the gate wave, its a/b inputs), fetched one chunk ahead
   float x[7][8], xv[7][4], ga = 0.0f, gb = 0.0f;
@@ -295,25 +324,22 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
     };
     if (c0 == a.s0) fetch(c0);
 
-    // z of this chunk for the gated-norm epilogue, in flight during the whole chunk
+    // z of this chunk for the gated-norm epilogue (epilogue layout), in flight during the whole chunk
     const bool plain = c0 >= a.P && full;  // no replay rows, no rows past the end
-    float zr[4][4];
+    const int er = lane >> 2, ec = 16 * w + 4 * (lane & 3);  // epilogue row within a 16-row block, column
+    f4 zq[4];
     if (plain) {
       const char* zb = (const char*)a.in + ((size_t)b * a.L + (c0 - a.P)) * (size_t)rowb + (a.C + h * kDV) * sizeof(T);
-      const unsigned oz = 4u * grp * rowb + (16 * w + c16) * (unsigned)sizeof(T);
+      const unsigned oz = (unsigned)er * rowb + ec * (unsigned)sizeof(T);
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) zr[ti][e] = (float)*gp<T>(zb + (size_t)(16 * ti + e) * rowb + oz);
+      for (int q = 0; q < 4; q++) zq[q] = ld4(gp<T>(zb + (size_t)(16 * q) * rowb + oz));
     } else {
-      const gptr<T> zb = gp<T>(a.in) + (size_t)b * a.L * a.stride + a.C + h * kDV + 16 * w + c16;
+      const gptr<T> zb = gp<T>(a.in) + (size_t)b * a.L * a.stride + a.C + h * kDV + ec;
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int rr = min(max(c0 + 16 * ti + 4 * grp + e - a.P, 0), a.L - 1);
-          zr[ti][e] = (float)zb[(size_t)rr * a.stride];
-        }
+      for (int q = 0; q < 4; q++) {
+        const int rr = min(max(c0 + 16 * q + er - a.P, 0), a.L - 1);
+        zq[q] = ld4(zb + (size_t)rr * a.stride);
+      }
     }
 
     // ---- 1. gate vectors (one wave, lane = row), conv + SiLU + norms (all waves) ----
@@ -334,6 +360,14 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       sm.eg[lane] = __expf(gcr);
       sm.bt[lane] = btr;
       sm.ed[lane] = __expf(gl - gcr);
+      const float rf = __expf(gcr - __shfl(gcr, lane & ~15));
+      sm.rowf[lane] = rf;
+      sm.brow[lane] = btr * rf;
+#pragma unroll
+      for (int i = 1; i < 4; i++) {
+        const float gi = __shfl(gcr, 16 * i);
+        sm.colf[i - 1][lane] = lane < 16 * i ? __expf(gi - gcr) : 0.0f;
+      }
     }
     {
       float u[4][8], ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -399,16 +433,30 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       for (int ks = 0; ks < 4; ks++)
         acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
       const int tp = 16 * tj + c16, t0 = 16 * ti + 4 * grp;
-      const float gp_ = sm.gc[tp];
-      const f4 gt = lds4(&sm.gc[t0]), bt = lds4(&sm.bt[t0]);
+      if (ti != tj) {
+        // below the diagonal blocks gc_t <= gc_16ti <= gc_t', so e^(gc_t - gc_t') factors into two terms <= 1
+        const float cf = sm.colf[ti - 1][tp];
+        if (!isq) {
+          const f4 bf = lds4(&sm.brow[t0]);
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int t = t0 + e;
-        const float dec = __expf(fminf(gt[e] - gp_, 0.0f));
-        if (!isq)
-          sm.Tm[t * kAP + tp] = tp < t ? bt[e] * acc[e] * dec : 0.0f;
-        else
-          sm.Att[t * kTP + tp] = (_Float16)(tp <= t ? acc[e] * dec : 0.0f);
+          for (int e = 0; e < 4; e++) sm.Tm[(t0 + e) * kAP + tp] = acc[e] * bf[e] * cf;
+        } else {
+          const f4 rf = lds4(&sm.rowf[t0]);
+#pragma unroll
+          for (int e = 0; e < 4; e++) sm.Att[(t0 + e) * kTP + tp] = (_Float16)(acc[e] * rf[e] * cf);
+        }
+      } else {
+        const float gp_ = sm.gc[tp];
+        const f4 gt = lds4(&sm.gc[t0]), bt = lds4(&sm.bt[t0]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int t = t0 + e;
+          const float dec = __expf(fminf(gt[e] - gp_, 0.0f));
+          if (!isq)
+            sm.Tm[t * kAP + tp] = tp < t ? bt[e] * acc[e] * dec : 0.0f;
+          else
+            sm.Att[t * kTP + tp] = (_Float16)(tp <= t ? acc[e] * dec : 0.0f);
+        }
       }
     }
     __syncthreads();  // B2
@@ -458,8 +506,6 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       qk_times_s();
     }
     __syncthreads();  // B3
-    // the next chunk's raw rows load from here on, behind the solve, the state update and the epilogue
-    fetch(c0 + kCH);
     if (w == 0)
       t_column<0>(sm, grp, c16);
     else if (w == 1)
@@ -468,6 +514,9 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       t_column<2>(sm, grp, c16);
     else if (w == kGW)
       qk_times_s();
+    // the next chunk's raw rows load from here on, behind the state update and the epilogue (issued after the
+    // solve on the waves that do it, so address-unit back-pressure from the other waves' loads does not delay it)
+    fetch(c0 + kCH);
     __syncthreads();  // B4
 
     // ---- 4. V_new = T diag(beta) v - T diag(beta e^gc) (k^ S); o = e^gc (q^ S) + scores V_new; state ----
@@ -506,51 +555,57 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         S[it] = acc;
       }
     }
+    // O (D layout) -> epilogue layout (4 consecutive columns of a row per lane) through this wave's slice of Tm,
+    // 32 rows at a time, so that the z loads and the output stores are 16-byte accesses
+    f4 Y[4];
+    {
+      float* stg = sm.Tm + w * (32 * 16);
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) stg[stage_row(16 * ti + 4 * grp + e) * 16 + c16] = O[2 * hf + ti][e];
+        wave_sync();
+#pragma unroll
+        for (int s = 0; s < 2; s++) Y[2 * hf + s] = lds4(stg + stage_row(16 * s + er) * 16 + 4 * (lane & 3));
+        wave_sync();
+      }
+    }
     if (a.gnorm) {
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const float sq = row_sum16(O[ti][e] * O[ti][e]);
-          if (c16 == 4 * ti + e) sm.red[(16 * ti + 4 * grp + e) * kNW + w] = sq;
-        }
+      for (int q = 0; q < 4; q++) {
+        const float sq = quad_sum((Y[q][0] * Y[q][0] + Y[q][1] * Y[q][1]) + (Y[q][2] * Y[q][2] + Y[q][3] * Y[q][3]));
+        if ((lane & 3) == 0) sm.red[(16 * q + er) * kNW + w] = sq;
+      }
     }
     __syncthreads();  // B5: every wave is done with this chunk's tiles; the next chunk may overwrite them
 
     // ---- 5. gated RMSNorm over the head's 128 columns and the store ----
-    f4 iv[4];
     if (a.gnorm) {
       const f4 r0 = lds4(&sm.red[lane * kNW]), r1 = lds4(&sm.red[lane * kNW + 4]);
       const float sq = ((r0[0] + r0[1]) + (r0[2] + r0[3])) + ((r1[0] + r1[1]) + (r1[2] + r1[3]));
       sm.inv[w][lane] = rsqrtf(sq / kDV + 1e-6f);
       wave_sync();
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++) iv[ti] = lds4(&sm.inv[w][16 * ti + 4 * grp]);
+      for (int q = 0; q < 4; q++) {
+        const float iv = sm.inv[w][16 * q + er];
+#pragma unroll
+        for (int c = 0; c < 4; c++) Y[q][c] = gw[c] * Y[q][c] * iv * silu(zq[q][c]);
+      }
     }
     if (plain) {
       char* ob = (char*)a.out + ((size_t)b * a.L + (c0 - a.P)) * (size_t)orowb + (size_t)h * kDV * sizeof(T);
-      const unsigned oo = 4u * grp * orowb + col * (unsigned)sizeof(T);
+      const unsigned oo = (unsigned)er * orowb + ec * (unsigned)sizeof(T);
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          float y = O[ti][e];
-          if (a.gnorm) y = gw * y * iv[ti][e] * silu(zr[ti][e]);
-          *gpw<T>(ob + (size_t)(16 * ti + e) * orowb + oo) = (T)y;
-        }
+      for (int q = 0; q < 4; q++) store4(gpw<T>(ob + (size_t)(16 * q) * orowb + oo), Y[q]);
     } else {
-      __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + col;
+      __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + ec;
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int t = 16 * ti + 4 * grp + e, r = c0 + t;
-          if (t < m && r >= a.P) {
-            float y = O[ti][e];
-            if (a.gnorm) y = gw * y * iv[ti][e] * silu(zr[ti][e]);
-            ob[(size_t)(r - a.P) * (a.H * kDV)] = (T)y;
-          }
-        }
+      for (int q = 0; q < 4; q++) {
+        const int t = 16 * q + er, r = c0 + t;
+        if (t < m && r >= a.P) store4(ob + (size_t)(r - a.P) * (a.H * kDV), Y[q]);
+      }
     }
   }
 #pragma unroll
