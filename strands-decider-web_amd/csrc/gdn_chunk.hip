@@ -283,19 +283,21 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
     const int rg = tid >> 5, cgi = tid & 31, qk = cgi >> 4, cg = cgi & 15;
     const int chq = (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, chv = 2 * a.H * kDK + h * kDV + 4 * cgi;
 
-    // rows cs-3 .. cs+63 of every sequence; rows past the end read as 0
-    auto fetch = [&](int cs) {
+    // rows i0..i1-1 of the 7 conv input rows of this lane (chunk rows cs-3 .. cs+63; rows past the end read as 0),
+    // and with the first group the gate wave's a/b inputs. The groups are issued at different points of the
+    // previous chunk so that the whole workgroup's loads do not reach the memory system in one burst.
+    auto fetch = [&](int cs, int i0, int i1) {
       if (cs - (kKC - 1) >= a.P && cs + kCH <= end) {
         // common path: all 67 rows come from `in`; uniform row bases, 32-bit lane offsets
         const char* base = (const char*)a.in + ((size_t)b * a.L + (cs - (kKC - 1) - a.P)) * (size_t)rowb;
         const unsigned oq = 4u * rg * rowb + chq * (unsigned)sizeof(T), ov = 4u * rg * rowb + chv * (unsigned)sizeof(T);
 #pragma unroll
-        for (int i = 0; i < 7; i++) {
+        for (int i = i0; i < i1; i++) {
           const char* rb = base + (size_t)i * rowb;
           load8(gp<T>(rb + oq), x[i]);
           load4(gp<T>(rb + ov), xv[i]);
         }
-        if (w == kGW) {
+        if (w == kGW && i0 == 0) {
           const char* gb0 = base + (size_t)(kKC - 1) * rowb;
           const unsigned og = (unsigned)lane * rowb;
           ga = (float)*gp<T>(gb0 + og + aoff * sizeof(T));
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 7; i++) {
+        for (int i = i0; i < i1; i++) {
           const int r = cs + 4 * rg - 3 + i, rc = min(r, end - 1);
           const gptr<T> row = row_of<T>(a, b, rc);
           load8(row + chq, x[i]);
@@ -315,32 +317,14 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
             for (int c = 0; c < 4; c++) xv[i][c] = 0.0f;
           }
         }
-        if (w == kGW) {
+        if (w == kGW && i0 == 0) {
           const gptr<T> grow = row_of<T>(a, b, min(cs + lane, end - 1));
           ga = cs + lane < end ? (float)grow[aoff] : 0.0f;
           gb = cs + lane < end ? (float)grow[boff] : 0.0f;
         }
       }
     };
-    if (c0 == a.s0) fetch(c0);
-
-    // z of this chunk for the gated-norm epilogue (epilogue layout), in flight during the whole chunk
-    const bool plain = c0 >= a.P && full;  // no replay rows, no rows past the end
-    const int er = lane >> 2, ec = 16 * w + 4 * (lane & 3);  // epilogue row within a 16-row block, column
-    f4 zq[4];
-    if (plain) {
-      const char* zb = (const char*)a.in + ((size_t)b * a.L + (c0 - a.P)) * (size_t)rowb + (a.C + h * kDV) * sizeof(T);
-      const unsigned oz = (unsigned)er * rowb + ec * (unsigned)sizeof(T);
-#pragma unroll
-      for (int q = 0; q < 4; q++) zq[q] = ld4(gp<T>(zb + (size_t)(16 * q) * rowb + oz));
-    } else {
-      const gptr<T> zb = gp<T>(a.in) + (size_t)b * a.L * a.stride + a.C + h * kDV + ec;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int rr = min(max(c0 + 16 * q + er - a.P, 0), a.L - 1);
-        zq[q] = ld4(zb + (size_t)rr * a.stride);
-      }
-    }
+    if (c0 == a.s0) fetch(c0, 0, 7);
 
     // ---- 1. gate vectors (one wave, lane = row), conv + SiLU + norms (all waves) ----
     if (w == kGW) {
@@ -419,6 +403,25 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       *reinterpret_cast<h4*>(sm.VT + vt_at(4 * cgi + c, rg)) = vt;
     }
     __syncthreads();  // B1
+    fetch(c0 + kCH, 0, 3);
+    // z of this chunk for the gated-norm epilogue (epilogue layout), in flight from here to the epilogue
+    const bool plain = c0 >= a.P && full;  // no replay rows, no rows past the end
+    const int er = lane >> 2, ec = 16 * w + 4 * (lane & 3);  // epilogue row within a 16-row block, column
+    f4 zq[4];
+    if (plain) {
+      const char* zb = (const char*)a.in + ((size_t)b * a.L + (c0 - a.P)) * (size_t)rowb + (a.C + h * kDV) * sizeof(T);
+      const unsigned oz = (unsigned)er * rowb + ec * (unsigned)sizeof(T);
+#pragma unroll
+      for (int q = 0; q < 4; q++) zq[q] = ld4(gp<T>(zb + (size_t)(16 * q) * rowb + oz));
+    } else {
+      const gptr<T> zb = gp<T>(a.in) + (size_t)b * a.L * a.stride + a.C + h * kDV + ec;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int rr = min(max(c0 + 16 * q + er - a.P, 0), a.L - 1);
+        zq[q] = ld4(zb + (size_t)rr * a.stride);
+      }
+    }
+
 
     // ---- 2. K K^T -> A (fp32), Q K^T -> decay-masked scores (f16); the 10 lower 16x16 tiles of each ----
     for (int job = w; job < 20; job += kNW) {
@@ -502,7 +505,9 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(p[r] * cb);
         sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(p[r] * cbw);
       }
+      fetch(c0 + kCH, 3, 5);
     } else {
+      fetch(c0 + kCH, 3, 5);
       qk_times_s();
     }
     __syncthreads();  // B3
@@ -516,7 +521,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       qk_times_s();
     // the next chunk's raw rows load from here on, behind the state update and the epilogue (issued after the
     // solve on the waves that do it, so address-unit back-pressure from the other waves' loads does not delay it)
-    fetch(c0 + kCH);
+    fetch(c0 + kCH, 5, 7);
     __syncthreads();  // B4
 
     // ---- 4. V_new = T diag(beta) v - T diag(beta e^gc) (k^ S); o = e^gc (q^ S) + scores V_new; state ----
