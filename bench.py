@@ -37,6 +37,37 @@ def gqa_flops(T, P=0):
     return 4 * HQ * HD * (T * (T + 1) // 2 + P * T)
 
 
+COPY_BYTES = 512 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gdn_chunk_B8_T2048_hbm_traffic.md")
+GDN_SOURCE = os.path.join(ROOT, "strands-decider-web_amd", "csrc", "gdn_chunk.hip")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gated-delta kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by the same counter's reading for a copy kernel of known size), used only
+    if that summary was taken on the kernel source that is built now; otherwise None."""
+    import hashlib
+    try:
+        with open(TRAFFIC_FILE) as f:
+            text = f.read()
+        with open(GDN_SOURCE, "rb") as f:
+            sha = hashlib.sha256(f.read()).hexdigest()
+    except OSError:
+        return None
+    vals = {}
+    for line in text.splitlines():
+        line = line.strip().lstrip("-* ")
+        if ":" in line and line.startswith(("traffic_bytes_per_launch", "kernel_source_sha256")):
+            k, v = line.split(":", 1)
+            vals[k.strip()] = v.strip().strip("` ")
+    if vals.get("kernel_source_sha256") != sha:
+        return None
+    try:
+        return int(vals["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
 def make_engine(ha, kinds, B, max_ctx, stream):
     import synth
     eng = ha.Engine(ha.model_config(kinds, batch=B, max_ctx=max_ctx, lin_dtype=ha.F32, full_dtype=ha.F16),
@@ -116,8 +147,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the T / B sweep")
-    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa"],
-                    help="run only one layer kind (B=8, T=2048) --steps times, for rocprofv3")
+    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy"],
+                    help="run only one layer kind (B=8, T=2048) --steps times, for rocprofv3; 'copy' runs a plain "
+                         "512 MiB device-to-device copy kernel, the reference point that scales FETCH_SIZE / "
+                         "WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the hybrid-attention path is benchmarked on a single GPU in this build "
@@ -130,6 +163,20 @@ def main():
     ha.load_library()
     stream = torch.cuda.Stream()
     B, T = 8, 2048
+    if args.profile_kernel == "copy":
+        with torch.cuda.stream(stream):
+            src = torch.ones(COPY_BYTES // 4, device="cuda:0", dtype=torch.float32)
+            dst = torch.empty_like(src)
+            for _ in range(args.warmup):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+        print(json.dumps({"profile_kernel": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
+                          "ms_per_launch": (time.perf_counter() - t0) * 1e3 / args.steps}), flush=True)
+        return
     if args.profile_kernel:
         kind = "full_attention" if args.profile_kernel == "gqa" else "linear_attention"
         rec = ha.SEQUENTIAL if args.profile_kernel == "gdn-seq" else ha.CHUNKED
@@ -204,7 +251,7 @@ def main():
         "per_kind_ms": {"gated_delta_18": round(gdn_ms, 4), "gqa_6": round(gqa_ms, 4)},
         "roofline": {"bound": "hbm", "kernel": "gdn_chunk_kernel (+ its 3-row tail copy)",
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(achieved / 8000.0, 4), "traffic": None,
+                     "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": gdn_bytes, "launch_ms": round(gdn_launch_ms, 5)},
         "roofline_gqa": {"bound": "mfma", "kernel": "gqa_prep_kernel + gqa_attn_kernel",
                          "achieved": round(gqa_tf, 1), "peak": 2500.0, "unit": "TFLOP/s",

@@ -17,7 +17,9 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "ha.h"
@@ -42,6 +44,10 @@ constexpr uint32_t kEngineMagic = 0x4841454eu, kSnapMagic = 0x48415350u, kDeadMa
 constexpr int kKC = 4;                          // conv kernel the kernels are built for
 constexpr int kTailCap = ha::kChunk - 1 + kKC;  // at most 63 open rows + 3 history rows (+1 spare)
 std::atomic<uint64_t> g_engine_ids{1};
+// Engines that exist right now. Handle checks look a pointer up here before reading through it, so a snapshot
+// outliving its engine (any order of release is allowed, e.g. under a garbage collector) never touches freed memory.
+std::mutex g_live_mu;
+std::unordered_set<const ha_engine*> g_live;
 
 struct Layer {
   int kind = 0;
@@ -94,7 +100,17 @@ struct ha_snapshot {
 
 namespace {
 
-bool engine_ok(const ha_engine* e) { return e && e->magic == kEngineMagic; }
+bool engine_ok(const ha_engine* e) {
+  std::lock_guard<std::mutex> lock(g_live_mu);
+  return e && g_live.count(e) && e->magic == kEngineMagic;
+}
+
+// The live engine that made a snapshot, or nullptr once that engine is gone.
+const ha_engine* snapshot_owner(const ha_snapshot* s) {
+  std::lock_guard<std::mutex> lock(g_live_mu);
+  const ha_engine* e = s->owner;
+  return (e && g_live.count(e) && e->id == s->owner_id) ? e : nullptr;
+}
 
 int check_config(const ha_config* c) {
   if (!c) return fail(HA_ERR_ARG, "config is NULL");
@@ -155,6 +171,10 @@ void free_engine(ha_engine* e) {
   for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
   for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
   if (e->own) (void)hipStreamDestroy(e->own);
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    g_live.erase(e);
+  }
   e->magic = kDeadMagic;
   delete e;
 }
@@ -186,6 +206,10 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
 
   ha_engine* e = new ha_engine();
   e->id = g_engine_ids.fetch_add(1);
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    g_live.insert(e);
+  }
   e->cfg = *cfg;
   e->kinds.assign(cfg->layer_kind, cfg->layer_kind + cfg->n_layers);
   e->cfg.layer_kind = e->kinds.data();
@@ -424,8 +448,8 @@ int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* ho
   if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
   if (s->released) return fail(HA_ERR_HANDLE, "snapshot was released");
   if (!what || !host) return fail(HA_ERR_ARG, "what and host must be non-NULL");
-  const ha_engine* e = s->owner;
-  if (!engine_ok(e) || e->id != s->owner_id) return fail(HA_ERR_HANDLE, "the snapshot's engine was destroyed");
+  const ha_engine* e = snapshot_owner(s);
+  if (!e) return fail(HA_ERR_HANDLE, "the snapshot's engine was destroyed");
   if (layer < 0 || layer >= (int)s->layers.size()) return fail(HA_ERR_ARG, "layer index out of range");
   const ha_config& c = e->cfg;
   const size_t B = c.batch;
@@ -460,8 +484,7 @@ int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* ho
 int ha_snapshot_release(ha_snapshot* s) {
   if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
   if (s->released) return HA_OK;
-  const ha_engine* e = s->owner;
-  if (engine_ok(e) && e->id == s->owner_id) {
+  if (const ha_engine* e = snapshot_owner(s)) {
     (void)hipSetDevice(e->device);
     (void)hipStreamSynchronize(e->stream);  // the snapshot's copies may still be in flight
   }

@@ -1,0 +1,194 @@
+'use strict';
+/*
+ * engine.js: the Node host side of the MI355X hybrid-attention path, shaped like the reference engine's API
+ * (web/public/engine/engine.js): Engine.create(...) (engine.js:63), engine.forward(..., {cache, keepCache,
+ * timestamps}) returning {cache, gpu_ms, layers} (engine.js:313-375), and snapshots with P and release()
+ * (engine.js:349-362). It drives the HIP kernels through the N-API addon ha_napi.node over the C ABI in
+ * include/ha.h; there is no fallback: if the addon or the library cannot load, require() throws.
+ *
+ * What is passed per layer is the token-mixer input that the reference's projections produce on the GPU: rows of
+ * the fused in_proj output (linear layers, [batch][L][linStride]) or of the fused qkv projection (full layers,
+ * [batch][L][fullStride]) in device memory, and an output buffer ([batch][L][H*DV] or [batch][L][HQ*HD]).
+ * DeviceBuffer wraps device memory for callers without a HIP allocator of their own.
+ *
+ * Written for Node >= 12 (no optional chaining, no nullish coalescing).
+ */
+const path = require('path');
+
+const native = require(path.join(__dirname, 'ha_napi.node'));
+
+const F32 = 0;
+const F16 = 1;
+const CHUNKED = 0;
+const SEQUENTIAL = 1;
+const LAYER_KIND = { linear_attention: 0, full_attention: 1 };
+
+function pick(obj, key, def) {
+  return obj !== undefined && obj !== null && obj[key] !== undefined && obj[key] !== null ? obj[key] : def;
+}
+
+function dtypeCode(d, def) {
+  if (d === undefined || d === null) return def;
+  if (d === F32 || d === 'f32' || d === 'float32') return F32;
+  if (d === F16 || d === 'f16' || d === 'float16') return F16;
+  throw new TypeError('unsupported dtype ' + d);
+}
+
+/*
+ * Engine config from the manifest's config object (convert/export_engine.py:83 writes the Hugging Face config keys:
+ * layer_types, linear_num_key_heads, linear_key_head_dim, linear_value_head_dim, linear_conv_kernel_dim,
+ * num_attention_heads, num_key_value_heads, head_dim, partial_rotary_factor, rope_theta, rms_norm_eps) plus
+ * runtime options {batch, maxCtx, linDtype, fullDtype, linGnorm}.
+ */
+function configFromManifest(manifest, opts) {
+  const m = manifest || {};
+  const o = opts || {};
+  const types = pick(m, 'layer_types', null);
+  if (!Array.isArray(types)) throw new TypeError('manifest config needs layer_types');
+  const layerKinds = types.map(function (t) {
+    if (!(t in LAYER_KIND)) throw new TypeError('unsupported layer type ' + t + ' (this engine runs the token mixers)');
+    return LAYER_KIND[t];
+  });
+  const H = pick(m, 'linear_num_key_heads', 16);
+  const DK = pick(m, 'linear_key_head_dim', 128);
+  const DV = pick(m, 'linear_value_head_dim', 128);
+  const HQ = pick(m, 'num_attention_heads', 8);
+  const HK = pick(m, 'num_key_value_heads', 2);
+  const HD = pick(m, 'head_dim', 256);
+  const rp = pick(m, 'rope_parameters', null);
+  const prf = pick(rp, 'partial_rotary_factor', pick(m, 'partial_rotary_factor', 0.25));
+  return {
+    layerKinds: layerKinds,
+    batch: pick(o, 'batch', 1),
+    maxCtx: pick(o, 'maxCtx', 4096),
+    H: H, DK: DK, DV: DV,
+    convK: pick(m, 'linear_conv_kernel_dim', 4),
+    // fused in_proj row: q | k | v | z | a | b (export_engine.py:52), padded to a multiple of 64 columns
+    linStride: pick(o, 'linStride', Math.ceil((2 * H * DK + 2 * H * DV + 2 * H) / 64) * 64),
+    linDtype: dtypeCode(pick(o, 'linDtype', null), F32),
+    linGnorm: pick(o, 'linGnorm', true) ? 1 : 0,
+    HQ: HQ, HK: HK, HD: HD,
+    rotDim: Math.round(HD * prf),
+    fullStride: pick(o, 'fullStride', 2 * HQ * HD + 2 * HK * HD),
+    fullDtype: dtypeCode(pick(o, 'fullDtype', null), F16),
+    ropeTheta: pick(rp, 'rope_theta', pick(m, 'rope_theta', 1e7)),
+    eps: pick(m, 'rms_norm_eps', 1e-6),
+  };
+}
+
+class DeviceBuffer {
+  constructor(engine, bytes) {
+    this._engine = engine;
+    this.bytes = bytes;
+    this.ptr = native.deviceAlloc(engine._h, bytes);
+  }
+  upload(typedArray) {
+    if (typedArray.byteLength > this.bytes) throw new RangeError('upload larger than the buffer');
+    native.copyToDevice(this._engine._h, this.ptr, typedArray);
+    return this;
+  }
+  download(typedArray) {
+    if (typedArray.byteLength > this.bytes) throw new RangeError('download larger than the buffer');
+    native.copyToHost(this._engine._h, typedArray, this.ptr);
+    return typedArray;
+  }
+  free() {
+    if (this.ptr !== null) {
+      native.deviceFree(this._engine._h, this.ptr);
+      this.ptr = null;
+    }
+  }
+}
+
+class Snapshot {
+  constructor(handle) {
+    this._h = handle;
+    this.P = native.snapshotTokens(handle);
+  }
+  layout() {
+    return native.snapshotLayout(this._h);
+  }
+  // what: 'state' | 'tail' (linear layers), 'K' | 'V' (full layers); into a TypedArray of the right size
+  read(layer, what, typedArray) {
+    native.snapshotRead(this._h, layer, what, typedArray);
+    return typedArray;
+  }
+  // frees the snapshot's device memory; idempotent, like the reference's release() (engine.js:361)
+  release() {
+    native.snapshotRelease(this._h);
+  }
+}
+
+function ptrOf(x) {
+  if (typeof x === 'bigint') return x;
+  if (x instanceof DeviceBuffer) {
+    if (x.ptr === null) throw new Error('device buffer was freed');
+    return x.ptr;
+  }
+  throw new TypeError('layer buffers must be DeviceBuffer or BigInt device pointers');
+}
+
+class Engine {
+  // The reference's Engine.create is async (engine.js:63); so is this one. opts: {device}
+  static create(config, opts) {
+    return new Promise(function (resolve) {
+      resolve(new Engine(config, opts));
+    });
+  }
+  static createSync(config, opts) {
+    return new Engine(config, opts);
+  }
+  constructor(config, opts) {
+    this.config = Array.isArray(config.layerKinds) ? config : configFromManifest(config, opts);
+    this._h = native.create(this.config, pick(opts, 'device', 0));
+  }
+  // per-layer tensor under its manifest name (conv, neg_exp_A, dt_bias, gnorm, q_norm, k_norm), Float32Array
+  setParam(layer, name, data) {
+    native.setParam(this._h, layer, name, data);
+  }
+  alloc(bytes) {
+    return new DeviceBuffer(this, bytes);
+  }
+  /*
+   * One forward over L new rows of every sequence (engine.js:313). inputs / outputs: one device buffer per layer.
+   * options: {cache: Snapshot to resume from, keepCache: return a snapshot of the context after this call,
+   *           timestamps: report gpu_ms, layerMs: per-layer GPU ms, recurrence: CHUNKED | SEQUENTIAL}
+   * Throws (as the reference does at engine.js:316) when the cached plus new rows exceed maxCtx.
+   */
+  forward(L, inputs, outputs, options) {
+    const o = options || {};
+    const cache = pick(o, 'cache', null);
+    const r = native.forward(this._h, L, inputs.map(ptrOf), outputs.map(ptrOf), cache ? cache._h : null,
+      !!pick(o, 'keepCache', false), {
+        recurrence: pick(o, 'recurrence', CHUNKED),
+        timestamps: pick(o, 'timestamps', false) ? 1 : 0,
+        layerMs: pick(o, 'layerMs', false) ? 1 : 0,
+        sync: 0,
+      });
+    const out = { cache: r.snapshot ? new Snapshot(r.snapshot) : null };
+    if (r.gpuMs !== undefined) out.gpu_ms = r.gpuMs;
+    if (r.layerMs !== undefined) out.layers = r.layerMs;
+    return out;
+  }
+  synchronize() {
+    native.synchronize(this._h);
+  }
+  destroy() {
+    if (this._h) {
+      native.destroy(this._h);
+      this._h = null;
+    }
+  }
+}
+
+module.exports = {
+  Engine: Engine,
+  Snapshot: Snapshot,
+  DeviceBuffer: DeviceBuffer,
+  configFromManifest: configFromManifest,
+  F32: F32,
+  F16: F16,
+  CHUNKED: CHUNKED,
+  SEQUENTIAL: SEQUENTIAL,
+  abiVersion: native.abiVersion,
+};

@@ -1,0 +1,524 @@
+/*
+ * ha_napi.c: Node N-API binding of the hybrid-attention C ABI (include/ha.h). Thin by design: every export maps to
+ * one ha_* call, a non-zero status becomes a thrown Error carrying ha_last_error() (the reference engine throws
+ * Errors from Engine.forward, web/public/engine/engine.js:316,373), and handles are JS externals whose finalizers
+ * free what the script leaked (a snapshot not release()d, an engine not destroy()ed).
+ *
+ * Device pointers cross into JS as BigInt (N-API 6+, Node >= 10.20). Host data crosses as TypedArrays.
+ */
+#define NAPI_VERSION 6
+#include <node_api.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ha.h"
+
+typedef struct {
+  ha_engine* e;
+} engine_box;
+
+typedef struct {
+  ha_snapshot* s;
+} snap_box;
+
+static napi_value throw_status(napi_env env, int rc) {
+  char code[16];
+  snprintf(code, sizeof(code), "HA_%d", -rc);
+  const char* msg = ha_last_error();
+  napi_throw_error(env, code, (msg && *msg) ? msg : "hybrid-attention call failed");
+  return NULL;
+}
+
+#define CHECK_NAPI(call)                                                    \
+  do {                                                                      \
+    if ((call) != napi_ok) {                                                \
+      const napi_extended_error_info* info = NULL;                          \
+      napi_get_last_error_info(env, &info);                                 \
+      bool pending = false;                                                 \
+      napi_is_exception_pending(env, &pending);                             \
+      if (!pending)                                                         \
+        napi_throw_error(env, NULL, info && info->error_message ? info->error_message : "N-API call failed"); \
+      return NULL;                                                          \
+    }                                                                       \
+  } while (0)
+
+#define CHECK_HA(call)                   \
+  do {                                   \
+    int rc_ = (call);                    \
+    if (rc_ != HA_OK) return throw_status(env, rc_); \
+  } while (0)
+
+static napi_value type_error(napi_env env, const char* msg) {
+  napi_throw_type_error(env, NULL, msg);
+  return NULL;
+}
+
+/* ---- argument helpers ---- */
+
+static int get_args(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, NULL, NULL) != napi_ok) return 0;
+  for (size_t i = argc; i < want; i++) napi_get_undefined(env, &argv[i]);
+  return 1;
+}
+
+static int is_nullish(napi_env env, napi_value v) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok) return 1;
+  return t == napi_undefined || t == napi_null;
+}
+
+static int get_int(napi_env env, napi_value obj, const char* key, int def, int* out) {
+  napi_value v;
+  bool has = false;
+  if (napi_has_named_property(env, obj, key, &has) != napi_ok) return 0;
+  if (!has) { *out = def; return 1; }
+  if (napi_get_named_property(env, obj, key, &v) != napi_ok) return 0;
+  if (is_nullish(env, v)) { *out = def; return 1; }
+  int32_t x;
+  if (napi_get_value_int32(env, v, &x) != napi_ok) return 0;
+  *out = x;
+  return 1;
+}
+
+static int get_float(napi_env env, napi_value obj, const char* key, float def, float* out) {
+  napi_value v;
+  bool has = false;
+  if (napi_has_named_property(env, obj, key, &has) != napi_ok) return 0;
+  if (!has) { *out = def; return 1; }
+  if (napi_get_named_property(env, obj, key, &v) != napi_ok) return 0;
+  if (is_nullish(env, v)) { *out = def; return 1; }
+  double x;
+  if (napi_get_value_double(env, v, &x) != napi_ok) return 0;
+  *out = (float)x;
+  return 1;
+}
+
+static int get_ptr(napi_env env, napi_value v, void** out) {
+  uint64_t x;
+  bool lossless = false;
+  if (napi_get_value_bigint_uint64(env, v, &x, &lossless) != napi_ok || !lossless) return 0;
+  *out = (void*)(uintptr_t)x;
+  return 1;
+}
+
+static engine_box* get_engine(napi_env env, napi_value v) {
+  void* p = NULL;
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p) return NULL;
+  return (engine_box*)p;
+}
+
+static snap_box* get_snap(napi_env env, napi_value v) {
+  void* p = NULL;
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p) return NULL;
+  return (snap_box*)p;
+}
+
+/* host bytes of a TypedArray / ArrayBuffer view */
+static int get_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
+  bool is_ta = false;
+  if (napi_is_typedarray(env, v, &is_ta) != napi_ok || !is_ta) return 0;
+  napi_typedarray_type type;
+  size_t len, off;
+  napi_value ab;
+  void* d;
+  if (napi_get_typedarray_info(env, v, &type, &len, &d, &ab, &off) != napi_ok) return 0;
+  size_t esz = 1;
+  switch (type) {
+    case napi_int16_array: case napi_uint16_array: esz = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: esz = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: esz = 8; break;
+    default: esz = 1;
+  }
+  *data = d;
+  *bytes = len * esz;
+  return 1;
+}
+
+/* ---- finalizers ---- */
+
+static void engine_finalize(napi_env env, void* data, void* hint) {
+  (void)env; (void)hint;
+  engine_box* b = (engine_box*)data;
+  if (b->e) ha_destroy(b->e);
+  free(b);
+}
+
+static void snap_finalize(napi_env env, void* data, void* hint) {
+  (void)env; (void)hint;
+  snap_box* b = (snap_box*)data;
+  if (b->s) ha_snapshot_destroy(b->s);
+  free(b);
+}
+
+/* ---- exports ---- */
+
+static napi_value js_abi_version(napi_env env, napi_callback_info info) {
+  (void)info;
+  napi_value r;
+  CHECK_NAPI(napi_create_int32(env, ha_abi_version(), &r));
+  return r;
+}
+
+static napi_value js_last_error(napi_env env, napi_callback_info info) {
+  (void)info;
+  napi_value r;
+  CHECK_NAPI(napi_create_string_utf8(env, ha_last_error(), NAPI_AUTO_LENGTH, &r));
+  return r;
+}
+
+/* create(cfg, device) -> engine. cfg uses the C field names; layerKinds is an array of 0 (linear_attention) /
+   1 (full_attention). */
+static napi_value js_create(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return type_error(env, "create(cfg, device)");
+  napi_value cfgv = argv[0];
+  napi_value kinds;
+  bool is_arr = false;
+  CHECK_NAPI(napi_get_named_property(env, cfgv, "layerKinds", &kinds));
+  CHECK_NAPI(napi_is_array(env, kinds, &is_arr));
+  if (!is_arr) return type_error(env, "cfg.layerKinds must be an array of 0/1");
+  uint32_t n = 0;
+  CHECK_NAPI(napi_get_array_length(env, kinds, &n));
+  unsigned char* lk = (unsigned char*)malloc(n ? n : 1);
+  if (!lk) return type_error(env, "out of host memory");
+  for (uint32_t i = 0; i < n; i++) {
+    napi_value v;
+    int32_t k;
+    if (napi_get_element(env, kinds, i, &v) != napi_ok || napi_get_value_int32(env, v, &k) != napi_ok) {
+      free(lk);
+      return type_error(env, "cfg.layerKinds must hold integers");
+    }
+    lk[i] = (unsigned char)k;
+  }
+  ha_config c;
+  memset(&c, 0, sizeof(c));
+  c.n_layers = (int)n;
+  c.layer_kind = lk;
+  int ok = get_int(env, cfgv, "batch", 1, &c.batch) && get_int(env, cfgv, "maxCtx", 4096, &c.max_ctx) &&
+           get_int(env, cfgv, "H", 16, &c.H) && get_int(env, cfgv, "DK", 128, &c.DK) &&
+           get_int(env, cfgv, "DV", 128, &c.DV) && get_int(env, cfgv, "convK", 4, &c.conv_k) &&
+           get_int(env, cfgv, "linStride", 8256, &c.lin_stride) && get_int(env, cfgv, "linDtype", HA_F32, &c.lin_dtype) &&
+           get_int(env, cfgv, "linGnorm", 1, &c.lin_gnorm) && get_int(env, cfgv, "HQ", 8, &c.HQ) &&
+           get_int(env, cfgv, "HK", 2, &c.HK) && get_int(env, cfgv, "HD", 256, &c.HD) &&
+           get_int(env, cfgv, "rotDim", 64, &c.rot_dim) && get_int(env, cfgv, "fullStride", 5120, &c.full_stride) &&
+           get_int(env, cfgv, "fullDtype", HA_F16, &c.full_dtype) &&
+           get_float(env, cfgv, "ropeTheta", 1e7f, &c.rope_theta) && get_float(env, cfgv, "eps", 1e-6f, &c.eps);
+  if (!ok) {
+    free(lk);
+    return type_error(env, "invalid engine config field");
+  }
+  int32_t device = 0;
+  if (!is_nullish(env, argv[1]) && napi_get_value_int32(env, argv[1], &device) != napi_ok) {
+    free(lk);
+    return type_error(env, "device must be an integer");
+  }
+  ha_engine* e = NULL;
+  int rc = ha_create(&c, device, &e);
+  free(lk);
+  if (rc) return throw_status(env, rc);
+  engine_box* b = (engine_box*)malloc(sizeof(engine_box));
+  if (!b) {
+    ha_destroy(e);
+    return type_error(env, "out of host memory");
+  }
+  b->e = e;
+  napi_value r;
+  if (napi_create_external(env, b, engine_finalize, NULL, &r) != napi_ok) {
+    ha_destroy(e);
+    free(b);
+    napi_throw_error(env, NULL, "napi_create_external failed");
+    return NULL;
+  }
+  return r;
+}
+
+static napi_value js_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  engine_box* b = get_engine(env, argv[0]);
+  if (!b) return type_error(env, "not an engine handle");
+  if (b->e) {
+    ha_engine* e = b->e;
+    b->e = NULL;
+    CHECK_HA(ha_destroy(e));
+  }
+  return NULL;
+}
+
+#define ENGINE_ARG(v)                                                  \
+  engine_box* eb_ = get_engine(env, (v));                              \
+  if (!eb_) return type_error(env, "not an engine handle");            \
+  if (!eb_->e) return type_error(env, "engine was destroyed");         \
+  ha_engine* e = eb_->e
+
+/* setParam(engine, layer, name, Float32Array) */
+static napi_value js_set_param(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  if (!get_args(env, info, 4, argv)) return NULL;
+  ENGINE_ARG(argv[0]);
+  int32_t layer;
+  char name[64];
+  size_t nlen = 0;
+  if (napi_get_value_int32(env, argv[1], &layer) != napi_ok) return type_error(env, "layer must be an integer");
+  if (napi_get_value_string_utf8(env, argv[2], name, sizeof(name), &nlen) != napi_ok)
+    return type_error(env, "name must be a string");
+  napi_typedarray_type type;
+  size_t len, off;
+  napi_value ab;
+  void* d;
+  bool is_ta = false;
+  if (napi_is_typedarray(env, argv[3], &is_ta) != napi_ok || !is_ta ||
+      napi_get_typedarray_info(env, argv[3], &type, &len, &d, &ab, &off) != napi_ok || type != napi_float32_array)
+    return type_error(env, "data must be a Float32Array");
+  CHECK_HA(ha_set_param(e, layer, name, (const float*)d, len));
+  return NULL;
+}
+
+/* forward(engine, L, inputs: BigInt[], outputs: BigInt[], resume: snapshot|null, keep: bool,
+           opts: {recurrence, timestamps, layerMs, sync}) -> {snapshot, gpuMs, layerMs} */
+static napi_value js_forward(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (!get_args(env, info, 7, argv)) return NULL;
+  ENGINE_ARG(argv[0]);
+  int32_t L;
+  if (napi_get_value_int32(env, argv[1], &L) != napi_ok) return type_error(env, "L must be an integer");
+  uint32_t ni = 0, no = 0;
+  bool arr = false;
+  CHECK_NAPI(napi_is_array(env, argv[2], &arr));
+  if (!arr) return type_error(env, "inputs must be an array of device pointers");
+  CHECK_NAPI(napi_is_array(env, argv[3], &arr));
+  if (!arr) return type_error(env, "outputs must be an array of device pointers");
+  CHECK_NAPI(napi_get_array_length(env, argv[2], &ni));
+  CHECK_NAPI(napi_get_array_length(env, argv[3], &no));
+  if (ni != no) return type_error(env, "inputs and outputs must have one entry per layer");
+  void** ins = (void**)calloc(ni ? ni : 1, sizeof(void*));
+  void** outs = (void**)calloc(no ? no : 1, sizeof(void*));
+  float* lms = NULL;
+  if (!ins || !outs) {
+    free(ins); free(outs);
+    return type_error(env, "out of host memory");
+  }
+  for (uint32_t i = 0; i < ni; i++) {
+    napi_value v, w;
+    if (napi_get_element(env, argv[2], i, &v) != napi_ok || !get_ptr(env, v, &ins[i]) ||
+        napi_get_element(env, argv[3], i, &w) != napi_ok || !get_ptr(env, w, &outs[i])) {
+      free(ins); free(outs);
+      return type_error(env, "device pointers must be BigInt");
+    }
+  }
+  const ha_snapshot* resume = NULL;
+  if (!is_nullish(env, argv[4])) {
+    snap_box* sb = get_snap(env, argv[4]);
+    if (!sb || !sb->s) { free(ins); free(outs); return type_error(env, "resume must be a snapshot handle"); }
+    resume = sb->s;
+  }
+  bool keep = false;
+  if (!is_nullish(env, argv[5])) napi_get_value_bool(env, argv[5], &keep);
+  ha_forward_opts o;
+  memset(&o, 0, sizeof(o));
+  int want_lms = 0;
+  if (!is_nullish(env, argv[6])) {
+    if (!get_int(env, argv[6], "recurrence", HA_CHUNKED, &o.recurrence) ||
+        !get_int(env, argv[6], "timestamps", 0, &o.timestamps) || !get_int(env, argv[6], "sync", 0, &o.sync) ||
+        !get_int(env, argv[6], "layerMs", 0, &want_lms)) {
+      free(ins); free(outs);
+      return type_error(env, "invalid forward options");
+    }
+  }
+  if (want_lms) {
+    lms = (float*)calloc(ni ? ni : 1, sizeof(float));
+    o.layer_ms = lms;
+  }
+  ha_snapshot* snap = NULL;
+  int rc = ha_forward(e, L, (const void* const*)ins, (void* const*)outs, resume, keep ? &snap : NULL, &o);
+  free(ins);
+  free(outs);
+  if (rc) {
+    free(lms);
+    return throw_status(env, rc);
+  }
+  napi_value res, v;
+  CHECK_NAPI(napi_create_object(env, &res));
+  if (snap) {
+    snap_box* sb = (snap_box*)malloc(sizeof(snap_box));
+    if (!sb) {
+      ha_snapshot_destroy(snap);
+      free(lms);
+      return type_error(env, "out of host memory");
+    }
+    sb->s = snap;
+    if (napi_create_external(env, sb, snap_finalize, NULL, &v) != napi_ok) {
+      ha_snapshot_destroy(snap);
+      free(sb);
+      free(lms);
+      napi_throw_error(env, NULL, "napi_create_external failed");
+      return NULL;
+    }
+  } else {
+    napi_get_null(env, &v);
+  }
+  CHECK_NAPI(napi_set_named_property(env, res, "snapshot", v));
+  if (o.timestamps) {
+    CHECK_NAPI(napi_create_double(env, o.gpu_ms, &v));
+    CHECK_NAPI(napi_set_named_property(env, res, "gpuMs", v));
+  }
+  if (lms) {
+    napi_value arrv;
+    CHECK_NAPI(napi_create_array_with_length(env, ni, &arrv));
+    for (uint32_t i = 0; i < ni; i++) {
+      napi_value x;
+      napi_create_double(env, lms[i], &x);
+      napi_set_element(env, arrv, i, x);
+    }
+    free(lms);
+    CHECK_NAPI(napi_set_named_property(env, res, "layerMs", arrv));
+  }
+  return res;
+}
+
+#define SNAP_ARG(v)                                                      \
+  snap_box* sb_ = get_snap(env, (v));                                    \
+  if (!sb_ || !sb_->s) return type_error(env, "not a snapshot handle");  \
+  ha_snapshot* s = sb_->s
+
+static napi_value js_snapshot_tokens(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  SNAP_ARG(argv[0]);
+  int P = 0;
+  CHECK_HA(ha_snapshot_tokens(s, &P));
+  napi_value r;
+  CHECK_NAPI(napi_create_int32(env, P, &r));
+  return r;
+}
+
+static napi_value js_snapshot_layout(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  SNAP_ARG(argv[0]);
+  int sp = 0, tr = 0;
+  CHECK_HA(ha_snapshot_layout(s, &sp, &tr));
+  napi_value r, a, b;
+  CHECK_NAPI(napi_create_object(env, &r));
+  CHECK_NAPI(napi_create_int32(env, sp, &a));
+  CHECK_NAPI(napi_create_int32(env, tr, &b));
+  CHECK_NAPI(napi_set_named_property(env, r, "statePos", a));
+  CHECK_NAPI(napi_set_named_property(env, r, "tailRows", b));
+  return r;
+}
+
+/* snapshotRead(snap, layer, what, TypedArray) */
+static napi_value js_snapshot_read(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  if (!get_args(env, info, 4, argv)) return NULL;
+  SNAP_ARG(argv[0]);
+  int32_t layer;
+  char what[16];
+  size_t wl = 0;
+  void* d;
+  size_t bytes;
+  if (napi_get_value_int32(env, argv[1], &layer) != napi_ok) return type_error(env, "layer must be an integer");
+  if (napi_get_value_string_utf8(env, argv[2], what, sizeof(what), &wl) != napi_ok)
+    return type_error(env, "what must be a string");
+  if (!get_bytes(env, argv[3], &d, &bytes)) return type_error(env, "destination must be a TypedArray");
+  CHECK_HA(ha_snapshot_read(s, layer, what, d, bytes));
+  return NULL;
+}
+
+static napi_value js_snapshot_release(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  SNAP_ARG(argv[0]);
+  CHECK_HA(ha_snapshot_release(s));
+  return NULL;
+}
+
+static napi_value js_device_alloc(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  ENGINE_ARG(argv[0]);
+  double bytes;
+  if (napi_get_value_double(env, argv[1], &bytes) != napi_ok || bytes < 0) return type_error(env, "bytes must be >= 0");
+  void* p = NULL;
+  CHECK_HA(ha_device_alloc(e, (size_t)bytes, &p));
+  napi_value r;
+  CHECK_NAPI(napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)p, &r));
+  return r;
+}
+
+static napi_value js_device_free(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  ENGINE_ARG(argv[0]);
+  void* p;
+  if (!get_ptr(env, argv[1], &p)) return type_error(env, "pointer must be a BigInt");
+  CHECK_HA(ha_device_free(e, p));
+  return NULL;
+}
+
+/* copyToDevice(engine, dptr, TypedArray) */
+static napi_value js_copy_to_device(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return NULL;
+  ENGINE_ARG(argv[0]);
+  void* p;
+  void* d;
+  size_t bytes;
+  if (!get_ptr(env, argv[1], &p)) return type_error(env, "pointer must be a BigInt");
+  if (!get_bytes(env, argv[2], &d, &bytes)) return type_error(env, "source must be a TypedArray");
+  CHECK_HA(ha_copy_to_device(e, p, d, bytes));
+  return NULL;
+}
+
+/* copyToHost(engine, TypedArray, dptr) */
+static napi_value js_copy_to_host(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return NULL;
+  ENGINE_ARG(argv[0]);
+  void* p;
+  void* d;
+  size_t bytes;
+  if (!get_bytes(env, argv[1], &d, &bytes)) return type_error(env, "destination must be a TypedArray");
+  if (!get_ptr(env, argv[2], &p)) return type_error(env, "pointer must be a BigInt");
+  CHECK_HA(ha_copy_to_host(e, d, p, bytes));
+  return NULL;
+}
+
+static napi_value js_synchronize(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  ENGINE_ARG(argv[0]);
+  CHECK_HA(ha_synchronize(e));
+  return NULL;
+}
+
+static napi_value init(napi_env env, napi_value exports) {
+  const struct {
+    const char* name;
+    napi_callback fn;
+  } fns[] = {
+      {"abiVersion", js_abi_version},       {"lastError", js_last_error},
+      {"create", js_create},                {"destroy", js_destroy},
+      {"setParam", js_set_param},           {"forward", js_forward},
+      {"snapshotTokens", js_snapshot_tokens}, {"snapshotLayout", js_snapshot_layout},
+      {"snapshotRead", js_snapshot_read},   {"snapshotRelease", js_snapshot_release},
+      {"deviceAlloc", js_device_alloc},     {"deviceFree", js_device_free},
+      {"copyToDevice", js_copy_to_device},  {"copyToHost", js_copy_to_host},
+      {"synchronize", js_synchronize},
+  };
+  for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); i++) {
+    napi_value f;
+    if (napi_create_function(env, fns[i].name, NAPI_AUTO_LENGTH, fns[i].fn, NULL, &f) != napi_ok ||
+        napi_set_named_property(env, exports, fns[i].name, f) != napi_ok)
+      return NULL;
+  }
+  return exports;
+}
+
+#ifndef NODE_GYP_MODULE_NAME
+#define NODE_GYP_MODULE_NAME ha_napi
+#endif
+NAPI_MODULE(NODE_GYP_MODULE_NAME, init)

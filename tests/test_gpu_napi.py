@@ -1,0 +1,75 @@
+"""The Node host path on the GPU: tests/js/napi_forward.js drives engine.js -> ha_napi.node -> libha.so through a
+prefix forward with keepCache, a suffix forward resumed from the snapshot, and release() (engine.js:313-375 usage).
+Its outputs must equal, bit for bit, the same calls made through the C ABI from Python on the same inputs (same
+kernels, same order), and the prefix must match the CPU oracle within the north-star tolerances."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import synth
+from harness import Runner, oracle_gdn, oracle_gqa, rel_err
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")]
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+KINDS = ["linear_attention", "full_attention"]
+B, T0, T1 = 2, 100, 40
+
+
+def _inputs(T, part):
+    return [synth.gdn_rows(T, B, seed=5, layer=0, part=part).astype(np.float32),
+            synth.gqa_rows(T, B, seed=5, layer=1, part=part).astype(np.float16)]
+
+
+def _params():
+    return [synth.gdn_params(seed=5, layer=0), synth.gqa_params(seed=5, layer=1, noise=0.1)]
+
+
+def test_node_forward_resume_release(tmp_path):
+    d = str(tmp_path)
+    params = _params()
+    spec = {"kinds": KINDS, "batch": B, "maxCtx": 4096, "T0": T0, "T1": T1, "params": []}
+    for i, p in enumerate(params):
+        names = {}
+        for k, v in p.items():
+            f = "p_%d_%s.bin" % (i, k)
+            np.ascontiguousarray(v, dtype=np.float32).tofile(os.path.join(d, f))
+            names[k] = f
+        spec["params"].append(names)
+    ins = {0: _inputs(T0, 0), 1: _inputs(T1, 1)}
+    for part, xs in ins.items():
+        for i, x in enumerate(xs):
+            x.tofile(os.path.join(d, "in_%d_%d.bin" % (i, part)))
+    with open(os.path.join(d, "spec.json"), "w") as f:
+        json.dump(spec, f)
+    print("node forward: B=%d T0=%d T1=%d" % (B, T0, T1), flush=True)
+    r = subprocess.run([shutil.which("node"), os.path.join(ROOT, "tests", "js", "napi_forward.js"), d],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert json.loads(r.stdout.strip().splitlines()[-1])["ok"]
+
+    def js_out(i, part, T):
+        dt = np.float32 if i == 0 else np.float16
+        return np.fromfile(os.path.join(d, "out_%d_%d.bin" % (i, part)), dtype=dt).reshape(B, T, 2048).astype(np.float32)
+
+    run = Runner(KINDS, batch=B)
+    for i, p in enumerate(params):
+        run.set_params(i, p)
+    out0, snap = run.forward(ins[0], keep=True)
+    out1, _ = run.forward(ins[1], cache=snap)
+    for i in range(2):
+        assert np.array_equal(js_out(i, 0, T0), out0[i]), "prefix layer %d differs from the C ABI run" % i
+        assert np.array_equal(js_out(i, 1, T1), out1[i]), "suffix layer %d differs from the C ABI run" % i
+    st = np.zeros((B, 16, 128, 128), np.float32)
+    snap.read(0, "state", st)
+    assert np.array_equal(np.fromfile(os.path.join(d, "state_0.bin"), dtype=np.float32).reshape(st.shape), st)
+
+    ref_g, _ = oracle_gdn(ins[0][0], params[0], gnorm=True)
+    ref_a, _ = oracle_gqa(ins[0][1], params[1], 4096)
+    e_g, e_a = rel_err(js_out(0, 0, T0), ref_g), rel_err(js_out(1, 0, T0), ref_a)
+    print("node prefix vs oracle: gated-delta %.2e, gqa %.2e" % (e_g, e_a))
+    assert e_g < 2e-3 and e_a < 1e-2

@@ -1,0 +1,55 @@
+"""The Node host side over the N-API addon, without a GPU: the addon builds and loads under the image's Node, the
+manifest config maps to the engine config the C ABI expects, and a failing C call surfaces as a thrown Error with
+the C status as its code (the reference throws Errors from Engine.create / forward, engine.js:66,316,373)."""
+import json
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ADDON = os.path.join(ROOT, "strands-decider-web_amd", "js", "ha_napi.node")
+NODE = shutil.which("node")
+
+pytestmark = pytest.mark.skipif(NODE is None or not os.path.exists(ADDON), reason="node or the built addon is missing")
+
+SCRIPT = r"""
+const m = require(%r);
+const out = {abi: m.abiVersion(), exports: Object.keys(m).sort()};
+out.cfg = m.configFromManifest({layer_types: ['linear_attention', 'linear_attention', 'linear_attention',
+  'full_attention'], linear_num_key_heads: 16, linear_key_head_dim: 128, linear_value_head_dim: 128,
+  linear_conv_kernel_dim: 4, num_attention_heads: 8, num_key_value_heads: 2, head_dim: 256,
+  partial_rotary_factor: 0.25, rope_theta: 10000000, rms_norm_eps: 1e-6}, {batch: 8});
+try { m.configFromManifest({layer_types: ['adapter']}); } catch (e) { out.bad_kind = e.message; }
+try { m.Engine.createSync(out.cfg, {device: 0}); out.created = true; } catch (e) { out.err = [e.code, e.message]; }
+m.Engine.create(out.cfg).then(function () { out.async = 'resolved'; }, function (e) { out.async = e.code; })
+  .then(function () { console.log(JSON.stringify(out)); });
+"""
+
+
+def _run():
+    js = SCRIPT % os.path.join(ROOT, "strands-decider-web_amd", "js", "engine.js")
+    r = subprocess.run([NODE, "-e", js], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def test_addon_loads_and_maps_manifest_config():
+    out = _run()
+    assert out["abi"] == 1
+    assert {"Engine", "Snapshot", "DeviceBuffer", "configFromManifest", "CHUNKED", "SEQUENTIAL"} <= set(out["exports"])
+    c = out["cfg"]
+    assert c["layerKinds"] == [0, 0, 0, 1] and c["batch"] == 8
+    # the engine's fused row strides (export_engine.py:52,61): 8256 = 64-padded q|k|v|z|a|b, 5120 = q|gate|k|v
+    assert c["linStride"] == 8256 and c["fullStride"] == 5120 and c["rotDim"] == 64
+    assert c["ropeTheta"] == 1e7 and abs(c["eps"] - 1e-6) < 1e-12
+    assert "unsupported layer type adapter" in out["bad_kind"]
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is visible: creation would succeed")
+def test_create_without_device_throws_with_status_code():
+    out = _run()
+    assert "created" not in out
+    assert out["err"][0] == "HA_4" and "no HIP device" in out["err"][1]
+    assert out["async"] == "HA_4"
