@@ -252,7 +252,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "gdn_chunk_kernel (+ its 3-row tail copy)",
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic(),
-                     "bytes_per_launch": gdn_bytes, "launch_ms": round(gdn_launch_ms, 5)},
+                     "bytes_per_launch": gdn_bytes, "bytes_per_token": gdn_bytes_per_token(),
+                     "launch_ms": round(gdn_launch_ms, 5)},
         "roofline_gqa": {"bound": "mfma", "kernel": "gqa_prep_kernel + gqa_attn_kernel",
                          "achieved": round(gqa_tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": round(gqa_tf / 2500.0, 4), "flops_per_launch": B * gqa_flops(T),
