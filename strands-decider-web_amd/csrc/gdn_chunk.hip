@@ -10,22 +10,21 @@
 //   o_t = exp(gc_t) q^_t S + sum_{t'<=t} (q^_t . k^_t') exp(gc_t - gc_t') V_new_t'
 //   S  <- exp(gc_63) S + k^T diag(exp(gc_63 - gc)) V_new                 (complete chunks only)
 //
-// One workgroup of 8 waves per (sequence, head) walks the chunks in order; the fp32 state stays in MFMA
-// accumulator registers for the whole call (wave w owns value columns 16w..16w+15). Five workgroup barriers per
-// chunk separate:
-//   1. conv (4 taps) + SiLU of raw rows fetched one chunk ahead (their loads overlap the previous chunk's solve and
-//      state update), l2 norms by 16-lane DPP reductions -> f16 tiles of q^, k^, k^T and v^T in LDS; one wave turns
-//      the a/b columns into the chunk's gate vectors (cumulative log decay, e^gc, beta, e^(gc_63 - gc)) in LDS. The
-//      per-row gate factors go onto T's columns and V_new's rows instead of onto copies of k;
-//   2. K K^T and Q K^T on v_mfma_f32_16x16x32_f16 -> A (fp32) and the decay-masked scores (f16);
-//   3. T = (I + A)^-1: one wave solves the four 16x16 diagonal blocks (left-looking, A rows read as LDS
-//      broadcasts) while the others compute q^ S and k^ S; then waves 0..2 each own one block column of the
-//      off-diagonal blocks (fp32 MFMA 16x16x4, the column kept in registers), with no barrier between block rows;
-//      T diag(beta) and T diag(beta e^gc) are stored f16;
-//   4. V_new = T diag(beta) v - T diag(beta e^gc) (k^ S), o and the state update on f16 MFMA with fp32
-//      accumulation, S as f16 B operands built in registers; 5. gated RMSNorm epilogue (GNORM) and the store.
-// Memory is addressed from wave-uniform (SGPR) row bases plus 32-bit lane offsets on the common path (chunks with
-// no replay rows and no rows past the end); the first and last chunk of a call take a general path.
+// One workgroup of 8 waves per (sequence, head) walks the chunks in order, as a two-stage pipeline:
+//   consumer waves 0..3 each own 32 value columns of the fp32 state, held in MFMA accumulator registers for the
+//     whole call, and do chunk p's state-dependent work: q^ S, k^ S, V_new, o, the state update and the gated
+//     RMSNorm epilogue (GNORM);
+//   producer waves 4..7 meanwhile run chunk p+1's q/k conv (4 taps) + SiLU + l2 norm in registers from raw rows
+//     fetched a chunk ahead, and one of them turns the a/b columns into the gate vectors.
+// Per period p the workgroup passes five barriers:
+//   A: consumers chunk p  |  producers conv(p+1), prefetch raw q/k rows of p+2
+//   B: consumers store chunk p's output  |  producers write q^, k^, k^T of p+1 and the gate vectors to LDS
+//   C: all waves: K K^T and Q K^T of p+1 on v_mfma_f32_16x16x32_f16 -> A (fp32) and the decay-masked scores
+//   D: one producer solves the diagonal 16x16 blocks of T = (I + A)^-1  |  consumers: v conv(p+1), first half
+//   E: three producers own one block column each of T's off-diagonal blocks (fp32 MFMA 16x16x4, no barrier
+//      between block rows)  |  consumers: v conv(p+1), second half
+// so the VALU-heavy conv overlaps the MFMA-heavy state work instead of following it. A tile is written only in a
+// segment after its last reader of the previous chunk, so every LDS tile is single-buffered.
 // Chunk boundaries sit at s0 + 64k, so a row is processed identically however a sequence is split into calls;
 // only complete chunks advance the stored state.
 //
@@ -44,20 +43,23 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kDK = 128, kDV = 128, kCH = 64, kKC = 4, kNW = 8, kNT = 64 * kNW;
+constexpr int kNC = 4;        // consumer waves (0..3), 32 value columns each; producers are waves 4..7
 constexpr int kQP = kDK + 8;  // row pitch (halves) of [64][128] f16 tiles
 constexpr int kTP = kCH + 8;  // row pitch (halves) of [*][64] f16 tiles
 constexpr int kAP = kCH + 4;  // row pitch (floats) of the fp32 A / T tile
-constexpr int kGW = kNW - 1;  // the wave that computes the gate vectors and the diagonal blocks of T
+constexpr int kGW = kNW - 1;  // the producer that computes the gate vectors and the diagonal blocks of T
+constexpr int kSP = 36;       // row pitch (floats) of a consumer's output staging area (16 rows x 32 columns)
+constexpr int kRG = 8;        // rows per conv lane
 
 struct Lds {
   _Float16 Qs[kCH * kQP];   // q^ / sqrt(DK), [t][i]
   _Float16 Ks[kCH * kQP];   // k^, [t][i]
-  _Float16 KT[kDK * kTP];   // k^ transposed, [i][t], 4-column groups swizzled by kt_at
-  _Float16 VT[kDV * kTP];   // v transposed, [j][t], 4-column groups swizzled by vt_at
+  _Float16 KT[kDK * kTP];   // k^ transposed, [i][t], 8-column groups swizzled by kt16
+  _Float16 VT[kDV * kTP];   // v transposed, [j][t], 8-column groups swizzled by vt16
   _Float16 Tb[kCH * kTP];   // T diag(beta), f16, [t][t']
   _Float16 Tw[kCH * kTP];   // T diag(beta e^gc), f16
   _Float16 Att[kCH * kTP];  // decay-masked causal q^ k^T, [t][t']
-  float Tm[kCH * kAP];      // A, then T, fp32
+  float Tm[kCH * kAP];      // A, then T, fp32; the consumers' output staging area while the producers convolve
   // this head's conv taps, laid out so that the 32 conv lanes of a half wave read consecutive 16-byte entries:
   // q/k channel 8 g + c (g < 32: q then k) at cwq[c][g], v channel 4 g + c at cwv[c][g]
   float cwq[8][32][kKC];
@@ -69,31 +71,36 @@ struct Lds {
   float rowf[kCH];          // e^(gc_t - gc_16(t/16)), in (0, 1]
   float brow[kCH];          // beta_t rowf_t
   float colf[3][kCH];       // colf[i-1][t'] = e^(gc_16i - gc_t') for t' < 16 i, in (0, 1]
-  float red[kCH * kNW];     // gated-norm partial sums, [t][wave]
-  float inv[kNW][kCH];      // per-wave copy of the row inverse norms
+  float red[kCH * kNC];     // gated-norm partial sums, [t][consumer]
+  float inv[kNC][kCH];      // per-consumer copy of the row inverse norms
 };
-// After the solve, Tm is free until the next chunk's K K^T: each wave stages 32 x 16 floats of its output there.
-static_assert(sizeof(float) * kCH * kAP >= kNW * 32 * 16 * sizeof(float), "staging area");
+static_assert(sizeof(float) * kCH * kAP >= kNC * 16 * kSP * sizeof(float), "staging area");
 
-// Row permutation of the staging area: rows 4 g + e (fixed e) of a D tile land in different quarters of the banks.
-__device__ __forceinline__ int stage_row(int r) { return (r & ~3) | ((r + (r >> 2)) & 3); }
-
-// Quad sums (lanes 4q..4q+3) with DPP quad permutations.
-__device__ __forceinline__ float quad_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
-  return v;
-}
+// Transposed tiles are written 8 rows of one column (16 bytes) per lane; the 8-column group index is XORed with a
+// function of the row so those writes spread over the banks. Element (row, col) lives at
+// row * kTP + 8 * (col / 8 ^ f(row)) + col % 8; every 16-byte read stays contiguous.
+__device__ __forceinline__ int kt16(int i, int g8) { return i * kTP + 8 * (g8 ^ ((i >> 3) & 7)); }
+__device__ __forceinline__ int vt16(int j, int g8) { return j * kTP + 8 * (g8 ^ ((j >> 4) & 7)); }
 
 // SiLU / sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE division sequence
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
+#define DPP_F(v, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xf, 0xf, false))
+
 // Sum over the 16 lanes of a DPP row (lanes 16r..16r+15) with row rotations; every lane gets the sum.
 __device__ __forceinline__ float row_sum16(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
+  v += DPP_F(v, 0x128);
+  v += DPP_F(v, 0x124);
+  v += DPP_F(v, 0x122);
+  v += DPP_F(v, 0x121);
+  return v;
+}
+
+// Sum over aligned groups of 8 lanes: quad permutations, then the half-row mirror (lane i <-> 7 - i).
+__device__ __forceinline__ float sum8(float v) {
+  v += DPP_F(v, 0xB1);
+  v += DPP_F(v, 0x4E);
+  v += DPP_F(v, 0x141);
   return v;
 }
 
@@ -104,8 +111,8 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// An identity the compiler cannot see through: per-lane indices re-derived from it every chunk keep the address
-// arithmetic built on them inside the chunk loop instead of being hoisted out of it and spilled.
+// An identity the compiler cannot see through: per-lane indices re-derived from it every period keep the address
+// arithmetic built on them inside the loop instead of being hoisted out of it and spilled.
 __device__ __forceinline__ int opaque(int x) {
   asm volatile("" : "+v"(x));
   return x;
@@ -143,7 +150,6 @@ __device__ __forceinline__ void load4(gptr<_Float16> p, float* o) {
   const h4 x = *(gptr<h4>)(p);
   o[0] = (float)x[0]; o[1] = (float)x[1]; o[2] = (float)x[2]; o[3] = (float)x[3];
 }
-
 __device__ __forceinline__ f4 ld4(gptr<float> p) { return *(gptr<f4>)(p); }
 __device__ __forceinline__ f4 ld4(gptr<_Float16> p) {
   const h4 x = *(gptr<h4>)(p);
@@ -164,17 +170,11 @@ __device__ __forceinline__ h8 perm_a(const _Float16* base, int pitch, int r, int
   return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Transposed tiles are written one 4-row strip per lane (8 bytes) down the rows of the transpose, which would put
-// the lanes of a write 8 (k^T) or 4 (v^T) rows apart and in the same banks; the 4-column group index is XORed
-// with a function of the row so those writes spread over the banks. Element (row, col) lives at
-// row * kTP + 4 * (col / 4 ^ f(row)) + col % 4. For v^T, f is even, so 8-column (16-byte) reads stay contiguous.
-__device__ __forceinline__ int kt_at(int i, int g4) { return i * kTP + 4 * (g4 ^ ((i >> 3) & 15)); }
-__device__ __forceinline__ int vt_at(int j, int g4) { return j * kTP + 4 * (g4 ^ (2 * ((j >> 4) & 7))); }
-
 // perm_a for the swizzled k^T tile
 __device__ __forceinline__ h8 perm_a_kt(const _Float16* kt, int r, int kb, int grp) {
-  const h4 lo = *reinterpret_cast<const h4*>(kt + kt_at(r, 8 * kb + grp));
-  const h4 hi = *reinterpret_cast<const h4*>(kt + kt_at(r, 8 * kb + 4 + grp));
+  const int sub = 4 * (grp & 1);
+  const h4 lo = *reinterpret_cast<const h4*>(kt + kt16(r, 4 * kb + (grp >> 1)) + sub);
+  const h4 hi = *reinterpret_cast<const h4*>(kt + kt16(r, 4 * kb + 2 + (grp >> 1)) + sub);
   return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -189,6 +189,11 @@ __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
 }
 
 __device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+
+template <int N>
+struct Width {
+  static constexpr int value = N;
+};
 
 // Block column J of T below the diagonal: T_iJ = -T_ii sum_{k=J}^{i-1} A_ik T_kJ for block rows i = J+1..3, in
 // order. The column's blocks stay in registers (D layout: rows 4 grp + e, column c16), so A is never overwritten
@@ -232,19 +237,15 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   Lds& sm = *reinterpret_cast<Lds*>(lds_raw);
   const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
   const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  const bool consumer = w < kNC;
   const int end = a.P + a.L;
+  const int nchunks = (a.L + (a.P - a.s0) + kCH - 1) / kCH;
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
-  const unsigned rowb = (unsigned)a.stride * sizeof(T);         // bytes per input row
-  const unsigned orowb = (unsigned)(a.H * kDV) * sizeof(T);     // bytes per output row
+  const unsigned rowb = (unsigned)a.stride * sizeof(T);      // bytes per input row
+  const unsigned orowb = (unsigned)(a.H * kDV) * sizeof(T);  // bytes per output row
+  const char* const seq_in = (const char*)a.in + (size_t)b * a.L * rowb;  // row P of this sequence
 
-  // state: S[it][e] = S[16 it + 4 grp + e][16 w + c16]
-  f4 S[8];
   const size_t sbase = ((size_t)b * a.H + h) * kDK * kDV;
-#pragma unroll
-  for (int it = 0; it < 8; it++)
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-      S[it][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * it + 4 * ((tid0 & 63) >> 4) + e) * kDV + 16 * w + (tid0 & 15)] : 0.0f;
 
   // this head's conv taps: local channel q 0..127, k 128..255, v 256..383
   for (int i = tid0; i < 3 * 128 * kKC; i += kNT) {
@@ -267,84 +268,139 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   }
   const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
   const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
-  // epilogue layout: lane l holds rows 16 q + l / 4 (q < 4) of columns 16 w + 4 (l % 4) .. +3
-  f4 gw = {1.0f, 1.0f, 1.0f, 1.0f};
-  if (a.gnorm) gw = ld4(gp<float>(a.gnorm) + 16 * w + 4 * (tid0 & 3));
 
-  // raw rows of a chunk (and, on the gate wave, its a/b inputs), fetched one chunk ahead
-  float x[7][8], xv[7][4], ga = 0.0f, gb = 0.0f;
-  __syncthreads();  // conv taps and zero blocks visible
+  // raw rows: producers hold q/k rows (11 rows x 8 channels) of the chunk they convolve next, consumers v rows
+  // (11 rows x 4 channels); the gate producer also holds that chunk's a/b inputs
+  float xq[kRG + kKC - 1][8], xv[kRG + kKC - 1][4], ga = 0.0f, gb = 0.0f;
 
-  for (int c0 = a.s0; c0 < end; c0 += kCH) {
-    const int m = min(kCH, end - c0);
-    const bool full = m == kCH;
-    const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
-    // conv tasks: rows 4 rg .. 4 rg + 3 of the chunk; 8 q-or-k channels and 4 v channels
-    const int rg = tid >> 5, cgi = tid & 31, qk = cgi >> 4, cg = cgi & 15;
-    const int chq = (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, chv = 2 * a.H * kDK + h * kDV + 4 * cgi;
-
-    // rows i0..i1-1 of the 7 conv input rows of this lane (chunk rows cs-3 .. cs+63; rows past the end read as 0),
-    // and with the first group the gate wave's a/b inputs. The groups are issued at different points of the
-    // previous chunk so that the whole workgroup's loads do not reach the memory system in one burst.
-    auto fetch = [&](int cs, int i0, int i1) {
-      if (cs - (kKC - 1) >= a.P && cs + kCH <= end) {
-        // common path: all 67 rows come from `in`; uniform row bases, 32-bit lane offsets
-        const char* base = (const char*)a.in + ((size_t)b * a.L + (cs - (kKC - 1) - a.P)) * (size_t)rowb;
-        const unsigned oq = 4u * rg * rowb + chq * (unsigned)sizeof(T), ov = 4u * rg * rowb + chv * (unsigned)sizeof(T);
+  // Loads rows cs-3 .. cs+63 of the chunk starting at cs: lane rows 8 rg - 3 .. 8 rg + 7 of the chunk, at column
+  // offset `col` (element) of the row, `n` channels. Rows past the end read as 0. Uniform row bases and 32-bit lane
+  // offsets when no row is a replay row or past the end; the general path otherwise.
+  auto fetch_rows = [&](int cs, int rg, int col, auto& x, auto nch) {
+    constexpr int N = decltype(nch)::value;
+    if (cs - (kKC - 1) >= a.P && cs + kCH <= end) {
+      const char* base = seq_in + (ptrdiff_t)(cs - (kKC - 1) - a.P) * rowb;
+      const unsigned off = (unsigned)(kRG * rg) * rowb + (unsigned)col * (unsigned)sizeof(T);
 #pragma unroll
-        for (int i = i0; i < i1; i++) {
-          const char* rb = base + (size_t)i * rowb;
-          load8(gp<T>(rb + oq), x[i]);
-          load4(gp<T>(rb + ov), xv[i]);
-        }
-        if (w == kGW && i0 == 0) {
-          const char* gb0 = base + (size_t)(kKC - 1) * rowb;
-          const unsigned og = (unsigned)lane * rowb;
-          ga = (float)*gp<T>(gb0 + og + aoff * sizeof(T));
-          gb = (float)*gp<T>(gb0 + og + boff * sizeof(T));
-        }
-      } else {
+      for (int i = 0; i < kRG + kKC - 1; i++) {
+        const char* rb = base + (size_t)i * rowb;
+        if constexpr (N == 8)
+          load8(gp<T>(rb + off), x[i]);
+        else
+          load4(gp<T>(rb + off), x[i]);
+      }
+    } else {
 #pragma unroll
-        for (int i = i0; i < i1; i++) {
-          const int r = cs + 4 * rg - 3 + i, rc = min(r, end - 1);
-          const gptr<T> row = row_of<T>(a, b, rc);
-          load8(row + chq, x[i]);
-          load4(row + chv, xv[i]);
-          if (r >= end) {
+      for (int i = 0; i < kRG + kKC - 1; i++) {
+        const int r = cs + kRG * rg - (kKC - 1) + i, rc = min(r, end - 1);
+        const gptr<T> row = row_of<T>(a, b, rc) + col;
+        if constexpr (N == 8)
+          load8(row, x[i]);
+        else
+          load4(row, x[i]);
+        if (r >= end) {
 #pragma unroll
-            for (int c = 0; c < 8; c++) x[i][c] = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4; c++) xv[i][c] = 0.0f;
-          }
-        }
-        if (w == kGW && i0 == 0) {
-          const gptr<T> grow = row_of<T>(a, b, min(cs + lane, end - 1));
-          ga = cs + lane < end ? (float)grow[aoff] : 0.0f;
-          gb = cs + lane < end ? (float)grow[boff] : 0.0f;
+          for (int c = 0; c < N; c++) x[i][c] = 0.0f;
         }
       }
-    };
-    if (c0 == a.s0) fetch(c0, 0, 7);
-
-    // ---- 1. gate vectors (one wave, lane = row), conv + SiLU + norms (all waves) ----
+    }
+  };
+  // producer lane pt = tid - 256: rows 8 (pt / 32) .., channels 8 (pt % 16) of q (pt % 32 < 16) or k
+  auto fetch_qk = [&](int cs) {
+    const int pt = opaque(tid0) - 64 * kNC, rg = pt >> 5, cgi = pt & 31, qk = cgi >> 4, cg = cgi & 15;
+    fetch_rows(cs, rg, (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, xq, Width<8>{});
     if (w == kGW) {
-      float gcr = 0.0f, btr = 0.0f;
-      if (lane < m) {
-        btr = __builtin_amdgcn_rcpf(1.0f + __expf(-gb));
-        const float xs = ga + db;
-        gcr = na * (xs > 20.0f ? xs : log1pf(__expf(xs)));
+      const int lane = pt & 63;
+      if (cs >= a.P && cs + kCH <= end) {
+        const char* g0 = seq_in + (size_t)(cs - a.P) * rowb;
+        const unsigned og = (unsigned)lane * rowb;
+        ga = (float)*gp<T>(g0 + og + (unsigned)aoff * sizeof(T));
+        gb = (float)*gp<T>(g0 + og + (unsigned)boff * sizeof(T));
+      } else {
+        const gptr<T> grow = row_of<T>(a, b, min(cs + lane, end - 1));
+        ga = cs + lane < end ? (float)grow[aoff] : 0.0f;
+        gb = cs + lane < end ? (float)grow[boff] : 0.0f;
       }
+    }
+  };
+  // consumer lane ct = tid: rows 8 (ct / 32) .., v channels 4 (ct % 32)
+  auto fetch_v = [&](int cs) {
+    const int ct = opaque(tid0), rg = ct >> 5, cvg = ct & 31;
+    fetch_rows(cs, rg, 2 * a.H * kDK + h * kDV + 4 * cvg, xv, Width<4>{});
+  };
+
+  // producer: normalized conv outputs of the chunk being prepared, rows 8 rg + r, channels 8 cg + c
+  float uq[kRG][8];
+  float gcr = 0.0f, btr = 0.0f;
+  auto produce_conv = [&](int cs) {
+    const int pt = opaque(tid0) - 64 * kNC, rg = pt >> 5, cgi = pt & 31, qk = cgi >> 4;
+    const int m = min(kCH, end - cs);
+    float ss[kRG];
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float o = __shfl_up(gcr, d);
-        if (lane >= d) gcr += o;
+    for (int r = 0; r < kRG; r++) ss[r] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const f4 wc = lds4(sm.cwq[c][cgi]);
+#pragma unroll
+      for (int r = 0; r < kRG; r++) {
+        float sv = wc[0] * xq[r][c];
+        sv = fmaf(wc[1], xq[r + 1][c], sv);
+        sv = fmaf(wc[2], xq[r + 2][c], sv);
+        sv = fmaf(wc[3], xq[r + 3][c], sv);
+        uq[r][c] = kRG * rg + r < m ? silu(sv) : 0.0f;
+        ss[r] = fmaf(uq[r][c], uq[r][c], ss[r]);
       }
+    }
+#pragma unroll
+    for (int r = 0; r < kRG; r++) {
+      const float rs = rsqrtf(row_sum16(ss[r]) + 1e-6f) * (qk ? 1.0f : qscale);
+#pragma unroll
+      for (int c = 0; c < 8; c++) uq[r][c] *= rs;
+    }
+  };
+  // gate producer: beta and the cumulative log decay of the chunk at cs from its a/b inputs (lane = row)
+  auto produce_gates = [&](int cs) {
+    const int lane = opaque(tid0) & 63;
+    const int m = min(kCH, end - cs);
+    gcr = 0.0f;
+    btr = 0.0f;
+    if (lane < m) {
+      btr = __builtin_amdgcn_rcpf(1.0f + __expf(-gb));
+      const float xs = ga + db;
+      gcr = na * (xs > 20.0f ? xs : log1pf(__expf(xs)));
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float o = __shfl_up(gcr, d);
+      if (lane >= d) gcr += o;
+    }
+  };
+  auto produce_write = [&]() {
+    const int pt = opaque(tid0) - 64 * kNC, rg = pt >> 5, cgi = pt & 31, qk = cgi >> 4, cg = cgi & 15;
+#pragma unroll
+    for (int r = 0; r < kRG; r++) {
+      h8 hv;
+#pragma unroll
+      for (int c = 0; c < 8; c++) hv[c] = (_Float16)uq[r][c];
+      *reinterpret_cast<h8*>((qk ? sm.Ks : sm.Qs) + (kRG * rg + r) * kQP + 8 * cg) = hv;
+    }
+    if (qk) {
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        h8 kt;
+#pragma unroll
+        for (int r = 0; r < kRG; r++) kt[r] = (_Float16)uq[r][c];
+        *reinterpret_cast<h8*>(sm.KT + kt16(8 * cg + c, rg)) = kt;
+      }
+    }
+    if (w == kGW) {
+      const int lane = pt & 63;
       const float gl = __shfl(gcr, 63);
+      const float rf = __expf(gcr - __shfl(gcr, lane & ~15));
       sm.gc[lane] = gcr;
       sm.eg[lane] = __expf(gcr);
       sm.bt[lane] = btr;
       sm.ed[lane] = __expf(gl - gcr);
-      const float rf = __expf(gcr - __shfl(gcr, lane & ~15));
       sm.rowf[lane] = rf;
       sm.brow[lane] = btr * rf;
 #pragma unroll
@@ -353,80 +409,31 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         sm.colf[i - 1][lane] = lane < 16 * i ? __expf(gi - gcr) : 0.0f;
       }
     }
-    {
-      float u[4][8], ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int c = 0; c < 8; c++) {
-        const f4 wc = lds4(sm.cwq[c][cgi]);
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-          float sv = wc[0] * x[rr][c];
-          sv = fmaf(wc[1], x[rr + 1][c], sv);
-          sv = fmaf(wc[2], x[rr + 2][c], sv);
-          sv = fmaf(wc[3], x[rr + 3][c], sv);
-          u[rr][c] = 4 * rg + rr < m ? silu(sv) : 0.0f;
-          ss[rr] = fmaf(u[rr][c], u[rr][c], ss[rr]);
-        }
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        const float rs = rsqrtf(row_sum16(ss[rr]) + 1e-6f) * (qk ? 1.0f : qscale);
-#pragma unroll
-        for (int c = 0; c < 8; c++) u[rr][c] *= rs;
-        h8 hv;
-#pragma unroll
-        for (int c = 0; c < 8; c++) hv[c] = (_Float16)u[rr][c];
-        *reinterpret_cast<h8*>((qk ? sm.Ks : sm.Qs) + (4 * rg + rr) * kQP + 8 * cg) = hv;
-      }
-      if (qk) {
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-          h4 kt;
-#pragma unroll
-          for (int rr = 0; rr < 4; rr++) kt[rr] = (_Float16)u[rr][c];
-          *reinterpret_cast<h4*>(sm.KT + kt_at(8 * cg + c, rg)) = kt;
-        }
-      }
-    }
+  };
+  // consumer: v conv of rows 8 rg + r0 .. r0 + 3 of the chunk at cs -> v^T (8 bytes per channel)
+  auto consume_vconv = [&](int cs, int r0) {
+    const int ct = opaque(tid0), rg = ct >> 5, cvg = ct & 31;
+    const int m = min(kCH, end - cs);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const f4 wc = lds4(sm.cwv[c][cgi]);
+      const f4 wc = lds4(sm.cwv[c][cvg]);
       h4 vt;
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        float sv = wc[0] * xv[rr][c];
-        sv = fmaf(wc[1], xv[rr + 1][c], sv);
-        sv = fmaf(wc[2], xv[rr + 2][c], sv);
-        sv = fmaf(wc[3], xv[rr + 3][c], sv);
-        vt[rr] = (_Float16)(4 * rg + rr < m ? silu(sv) : 0.0f);
+      for (int r = 0; r < 4; r++) {
+        float sv = wc[0] * xv[r0 + r][c];
+        sv = fmaf(wc[1], xv[r0 + r + 1][c], sv);
+        sv = fmaf(wc[2], xv[r0 + r + 2][c], sv);
+        sv = fmaf(wc[3], xv[r0 + r + 3][c], sv);
+        vt[r] = (_Float16)(kRG * rg + r0 + r < m ? silu(sv) : 0.0f);
       }
-      *reinterpret_cast<h4*>(sm.VT + vt_at(4 * cgi + c, rg)) = vt;
+      *reinterpret_cast<h4*>(sm.VT + vt16(4 * cvg + c, rg) + r0) = vt;
     }
-    __syncthreads();  // B1
-    fetch(c0 + kCH, 0, 3);
-    // z of this chunk for the gated-norm epilogue (epilogue layout), in flight from here to the epilogue
-    const bool plain = c0 >= a.P && full;  // no replay rows, no rows past the end
-    const int er = lane >> 2, ec = 16 * w + 4 * (lane & 3);  // epilogue row within a 16-row block, column
-    f4 zq[4];
-    if (plain) {
-      const char* zb = (const char*)a.in + ((size_t)b * a.L + (c0 - a.P)) * (size_t)rowb + (a.C + h * kDV) * sizeof(T);
-      const unsigned oz = (unsigned)er * rowb + ec * (unsigned)sizeof(T);
-#pragma unroll
-      for (int q = 0; q < 4; q++) zq[q] = ld4(gp<T>(zb + (size_t)(16 * q) * rowb + oz));
-    } else {
-      const gptr<T> zb = gp<T>(a.in) + (size_t)b * a.L * a.stride + a.C + h * kDV + ec;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int rr = min(max(c0 + 16 * q + er - a.P, 0), a.L - 1);
-        zq[q] = ld4(zb + (size_t)rr * a.stride);
-      }
-    }
+  };
 
-
-    // ---- 2. K K^T -> A (fp32), Q K^T -> decay-masked scores (f16); the 10 lower 16x16 tiles of each ----
-    for (int job = w; job < 20; job += kNW) {
-      const bool isq = job >= 10;
-      const int jt = isq ? job - 10 : job;
+  // One 16x16 tile of K K^T -> A (fp32) or Q K^T -> decay-masked scores (f16) of the chunk in Qs / Ks; tile jt of
+  // the 10 on or below the diagonal (row block ti, column block tj)
+  auto kkt_qkt_tile = [&](bool isq, int jt, int grp, int c16) {
+    {
       const int ti = jt >= 6 ? 3 : jt >= 3 ? 2 : jt >= 1 ? 1 : 0;
       const int tj = jt - ti * (ti + 1) / 2;
       const _Float16* ab = (isq ? sm.Qs : sm.Ks) + (16 * ti + c16) * kQP + 8 * grp;
@@ -462,162 +469,311 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         }
       }
     }
-    __syncthreads();  // B2
+  };
+  // The 16 tiles other than the diagonal blocks of A, over waves 0..6 (the gate producer does the diagonal blocks
+  // of A itself, right before solving them)
+  auto kkt_qkt = [&](int grp, int c16) {
+    for (int j = w; j < 16; j += kNW - 1) {
+      const int off[6] = {1, 3, 4, 6, 7, 8};  // below-diagonal tiles of A
+      if (j < 6)
+        kkt_qkt_tile(false, off[j], grp, c16);
+      else
+        kkt_qkt_tile(true, j - 6, grp, c16);
+    }
+  };
 
-    // ---- 3. T = (I + A)^-1; q^ S and k^ S ----
-    h8 S16[4], KSb[2];
-    f4 O[4];
-    auto qk_times_s = [&]() {
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++) S16[kb] = pack_b(S[2 * kb], S[2 * kb + 1]);
-      f4 ksd[4];
-#pragma unroll
-      for (int ti = 0; ti < 4; ti++) {
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, acck = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-          acc = mfma16(perm_a(sm.Qs, kQP, 16 * ti + c16, kb, grp), S16[kb], acc);
-          acck = mfma16(perm_a(sm.Ks, kQP, 16 * ti + c16, kb, grp), S16[kb], acck);
-        }
-        O[ti] = acc;
-        ksd[ti] = acck;
-      }
-      KSb[0] = pack_b(ksd[0], ksd[1]);
-      KSb[1] = pack_b(ksd[2], ksd[3]);
-    };
-    if (w == kGW) {
-      // lane (grp, c16): column c16 of diagonal block grp, rows in order (left-looking); row r of A is read as a
-      // broadcast shared by the 16 lanes of the block
-      const int base = 16 * grp;
-      float p[16];
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float* ar = &sm.Tm[(base + r) * kAP + base];
-        float acc = r == c16 ? 1.0f : 0.0f;
-#pragma unroll
-        for (int j = 0; j < r; j++) acc = fmaf(-ar[j], p[j], acc);
-        p[r] = acc;
-      }
-      const float cb = sm.bt[base + c16], cbw = cb * sm.eg[base + c16];
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        sm.Tm[(base + r) * kAP + base + c16] = p[r];
-        sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(p[r] * cb);
-        sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(p[r] * cbw);
-      }
-      fetch(c0 + kCH, 3, 5);
-    } else {
-      fetch(c0 + kCH, 3, 5);
-      qk_times_s();
-    }
-    __syncthreads();  // B3
-    if (w == 0)
-      t_column<0>(sm, grp, c16);
-    else if (w == 1)
-      t_column<1>(sm, grp, c16);
-    else if (w == 2)
-      t_column<2>(sm, grp, c16);
-    else if (w == kGW)
-      qk_times_s();
-    // the next chunk's raw rows load from here on, behind the state update and the epilogue (issued after the
-    // solve on the waves that do it, so address-unit back-pressure from the other waves' loads does not delay it)
-    fetch(c0 + kCH, 5, 7);
-    __syncthreads();  // B4
+  __syncthreads();  // conv taps and zero blocks visible
 
-    // ---- 4. V_new = T diag(beta) v - T diag(beta e^gc) (k^ S); o = e^gc (q^ S) + scores V_new; state ----
-    f4 Vn[4];
-    const int col = 16 * w + c16;
-#pragma unroll
-    for (int ti = 0; ti < 4; ti++) {
-      f4 u = {0.0f, 0.0f, 0.0f, 0.0f}, ws = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int kb = 0; kb <= (ti >> 1); kb++) {
-        u = mfma16(*reinterpret_cast<const h8*>(sm.Tb + (16 * ti + c16) * kTP + 32 * kb + 8 * grp),
-                   *reinterpret_cast<const h8*>(sm.VT + vt_at(col, 8 * kb + 2 * grp)), u);
-        ws = mfma16(perm_a(sm.Tw, kTP, 16 * ti + c16, kb, grp), KSb[kb], ws);
-      }
-      Vn[ti] = u - ws;
-    }
-#pragma unroll
-    for (int ti = 0; ti < 4; ti++) O[ti] *= lds4(&sm.eg[16 * ti + 4 * grp]);
-    const h8 Vb0 = pack_b(Vn[0], Vn[1]), Vb1 = pack_b(Vn[2], Vn[3]);
-#pragma unroll
-    for (int ti = 0; ti < 4; ti++) {
-      O[ti] = mfma16(perm_a(sm.Att, kTP, 16 * ti + c16, 0, grp), Vb0, O[ti]);
-      if (ti >= 2) O[ti] = mfma16(perm_a(sm.Att, kTP, 16 * ti + c16, 1, grp), Vb1, O[ti]);
-    }
-    if (full) {
-      // rows of V_new scaled by e^(gl - gc_t), then S <- e^gl S + k^T (scaled V_new)
-#pragma unroll
-      for (int ti = 0; ti < 4; ti++) Vn[ti] *= lds4(&sm.ed[16 * ti + 4 * grp]);
-      const h8 Vd0 = pack_b(Vn[0], Vn[1]), Vd1 = pack_b(Vn[2], Vn[3]);
-      const float el = sm.eg[kCH - 1];
-#pragma unroll
-      for (int it = 0; it < 8; it++) {
-        f4 acc = S[it] * el;
-        acc = mfma16(perm_a_kt(sm.KT, 16 * it + c16, 0, grp), Vd0, acc);
-        acc = mfma16(perm_a_kt(sm.KT, 16 * it + c16, 1, grp), Vd1, acc);
-        S[it] = acc;
-      }
-    }
-    // O (D layout) -> epilogue layout (4 consecutive columns of a row per lane) through this wave's slice of Tm,
-    // 32 rows at a time, so that the z loads and the output stores are 16-byte accesses
-    f4 Y[4];
+  // The two roles run separate loops with the same barrier sequence (the role is uniform per wave, and every
+  // condition that skips a barrier depends only on p and nchunks), so each loop keeps only its own registers live.
+  if (consumer) {
+    // ---- consumer state: S[ct][it][e] = S[16 it + 4 grp + e][32 w + 16 ct + c16] ----
+    f4 S[2][8];
     {
-      float* stg = sm.Tm + w * (32 * 16);
+      const int g0 = (tid0 & 63) >> 4, l16 = tid0 & 15;
 #pragma unroll
-      for (int hf = 0; hf < 2; hf++) {
+      for (int ct = 0; ct < 2; ct++)
 #pragma unroll
-        for (int ti = 0; ti < 2; ti++)
+        for (int it = 0; it < 8; it++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) stg[stage_row(16 * ti + 4 * grp + e) * 16 + c16] = O[2 * hf + ti][e];
-        wave_sync();
-#pragma unroll
-        for (int s = 0; s < 2; s++) Y[2 * hf + s] = lds4(stg + stage_row(16 * s + er) * 16 + 4 * (lane & 3));
-        wave_sync();
-      }
+          for (int e = 0; e < 4; e++)
+            S[ct][it][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16]
+                                  : 0.0f;
     }
-    if (a.gnorm) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float sq = quad_sum((Y[q][0] * Y[q][0] + Y[q][1] * Y[q][1]) + (Y[q][2] * Y[q][2] + Y[q][3] * Y[q][3]));
-        if ((lane & 3) == 0) sm.red[(16 * q + er) * kNW + w] = sq;
-      }
-    }
-    __syncthreads();  // B5: every wave is done with this chunk's tiles; the next chunk may overwrite them
+    // consumer epilogue layout: lane l holds rows 8 q + l / 8 (q < 8) of columns 32 w + 4 (l % 8) .. +3
+    f4 gw = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (a.gnorm) gw = ld4(gp<float>(a.gnorm) + 32 * w + 4 * (tid0 & 7));
+    f4 Y[8], zq[8];
+    // period p: chunk p (p >= 0) here, chunk p + 1 (p + 1 < nchunks) on the producers
+    for (int p = -1; p < nchunks; p++) {
+      const int c0 = a.s0 + kCH * p, c1 = c0 + kCH;
+      const int m = min(kCH, end - c0);
+      const bool full = m == kCH;
+      const bool plain = c0 >= a.P && full;  // no replay rows, no rows past the end
+      const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
+      const int er = lane >> 3, ec = 32 * w + 4 * (lane & 7);  // epilogue row (within 8) and column
 
-    // ---- 5. gated RMSNorm over the head's 128 columns and the store ----
-    if (a.gnorm) {
-      const f4 r0 = lds4(&sm.red[lane * kNW]), r1 = lds4(&sm.red[lane * kNW + 4]);
-      const float sq = ((r0[0] + r0[1]) + (r0[2] + r0[3])) + ((r1[0] + r1[1]) + (r1[2] + r1[3]));
-      sm.inv[w][lane] = rsqrtf(sq / kDV + 1e-6f);
-      wave_sync();
+      // ---- A: chunk p ----
+      if (p >= 0) {
+          // k^ S (K block outermost: only that block's f16 copy of S is live at a time); q^ S comes after V_new,
+          // so the two never hold their accumulators at the same time
+          f4 O[2][4], Vn[2][4];
+          h8 KSb[2][2];
+          {
+            f4 KS[2][4];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float iv = sm.inv[w][16 * q + er];
+            for (int kb = 0; kb < 4; kb++) {
+              h8 S16[2];
 #pragma unroll
-        for (int c = 0; c < 4; c++) Y[q][c] = gw[c] * Y[q][c] * iv * silu(zq[q][c]);
+              for (int ct = 0; ct < 2; ct++) S16[ct] = pack_b(S[ct][2 * kb], S[ct][2 * kb + 1]);
+#pragma unroll
+              for (int ti = 0; ti < 4; ti++) {
+                const h8 ka = perm_a(sm.Ks, kQP, 16 * ti + c16, kb, grp);
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                  const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                  KS[ct][ti] = mfma16(ka, S16[ct], kb ? KS[ct][ti] : z4);
+                }
+              }
+            }
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+              KSb[ct][0] = pack_b(KS[ct][0], KS[ct][1]);
+              KSb[ct][1] = pack_b(KS[ct][2], KS[ct][3]);
+            }
+          }
+          // z of this chunk for the epilogue, in flight behind the rest of the chunk's MFMA work
+          if (plain) {
+            const char* zb = seq_in + (size_t)(c0 - a.P) * rowb + (a.C + h * kDV) * sizeof(T);
+            const unsigned oz = (unsigned)er * rowb + ec * (unsigned)sizeof(T);
+#pragma unroll
+            for (int q = 0; q < 8; q++) zq[q] = ld4(gp<T>(zb + (size_t)(8 * q) * rowb + oz));
+          } else {
+            const gptr<T> zb = gp<T>(seq_in) + a.C + h * kDV + ec;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+              const int rr = min(max(c0 + 8 * q + er - a.P, 0), a.L - 1);
+              zq[q] = ld4(zb + (size_t)rr * a.stride);
+            }
+          }
+          // V_new = T diag(beta) v - T diag(beta e^gc) (k^ S)
+#pragma unroll
+          for (int ti = 0; ti < 4; ti++) {
+            f4 u[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}}, ws[2] = {u[0], u[0]};
+#pragma unroll
+            for (int kb = 0; kb <= (ti >> 1); kb++) {
+              const h8 tb = *reinterpret_cast<const h8*>(sm.Tb + (16 * ti + c16) * kTP + 32 * kb + 8 * grp);
+              const h8 tw = perm_a(sm.Tw, kTP, 16 * ti + c16, kb, grp);
+#pragma unroll
+              for (int ct = 0; ct < 2; ct++) {
+                const int col = 32 * w + 16 * ct + c16;
+                u[ct] = mfma16(tb, *reinterpret_cast<const h8*>(sm.VT + vt16(col, 4 * kb + grp)), u[ct]);
+                ws[ct] = mfma16(tw, KSb[ct][kb], ws[ct]);
+              }
+            }
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) Vn[ct][ti] = u[ct] - ws[ct];
+          }
+          // q^ S
+#pragma unroll
+          for (int kb = 0; kb < 4; kb++) {
+            h8 S16[2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) S16[ct] = pack_b(S[ct][2 * kb], S[ct][2 * kb + 1]);
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) {
+              const h8 qa = perm_a(sm.Qs, kQP, 16 * ti + c16, kb, grp);
+#pragma unroll
+              for (int ct = 0; ct < 2; ct++) {
+                const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+                O[ct][ti] = mfma16(qa, S16[ct], kb ? O[ct][ti] : z4);
+              }
+            }
+          }
+          // o = e^gc (q^ S) + scores V_new
+#pragma unroll
+          for (int ti = 0; ti < 4; ti++) {
+            const f4 eg = lds4(&sm.eg[16 * ti + 4 * grp]);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) O[ct][ti] *= eg;
+          }
+          {
+            h8 Vb[2][2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+              Vb[ct][0] = pack_b(Vn[ct][0], Vn[ct][1]);
+              Vb[ct][1] = pack_b(Vn[ct][2], Vn[ct][3]);
+            }
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) {
+              const h8 a0 = perm_a(sm.Att, kTP, 16 * ti + c16, 0, grp);
+#pragma unroll
+              for (int ct = 0; ct < 2; ct++) O[ct][ti] = mfma16(a0, Vb[ct][0], O[ct][ti]);
+              if (ti >= 2) {
+                const h8 a1 = perm_a(sm.Att, kTP, 16 * ti + c16, 1, grp);
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) O[ct][ti] = mfma16(a1, Vb[ct][1], O[ct][ti]);
+              }
+            }
+          }
+          if (full) {
+            // rows of V_new scaled by e^(gl - gc_t), then S <- e^gl S + k^T (scaled V_new)
+            h8 Vd[2][2];
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) {
+              const f4 ed = lds4(&sm.ed[16 * ti + 4 * grp]);
+#pragma unroll
+              for (int ct = 0; ct < 2; ct++) Vn[ct][ti] *= ed;
+            }
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+              Vd[ct][0] = pack_b(Vn[ct][0], Vn[ct][1]);
+              Vd[ct][1] = pack_b(Vn[ct][2], Vn[ct][3]);
+            }
+            const float el = sm.eg[kCH - 1];
+#pragma unroll
+            for (int it = 0; it < 8; it++) {
+              const h8 k0 = perm_a_kt(sm.KT, 16 * it + c16, 0, grp), k1 = perm_a_kt(sm.KT, 16 * it + c16, 1, grp);
+#pragma unroll
+              for (int ct = 0; ct < 2; ct++) S[ct][it] = mfma16(k1, Vd[ct][1], mfma16(k0, Vd[ct][0], S[ct][it] * el));
+            }
+          }
+          // O (D layout) -> epilogue layout through this consumer's slice of Tm, 16 rows at a time
+          {
+            float* stg = sm.Tm + w * (16 * kSP);
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) {
+#pragma unroll
+              for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) stg[(4 * grp + e) * kSP + 16 * ct + c16] = O[ct][ti][e];
+              wave_sync();
+#pragma unroll
+              for (int s = 0; s < 2; s++) Y[2 * ti + s] = lds4(stg + (8 * s + er) * kSP + 4 * (lane & 7));
+              wave_sync();
+            }
+          }
+          if (a.gnorm) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+              const float sq = sum8((Y[q][0] * Y[q][0] + Y[q][1] * Y[q][1]) + (Y[q][2] * Y[q][2] + Y[q][3] * Y[q][3]));
+              if ((lane & 7) == 0) sm.red[(8 * q + er) * kNC + w] = sq;
+            }
+            // the gate factor w * silu(z) of the gated norm, here where the consumers have slack
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+#pragma unroll
+              for (int c = 0; c < 4; c++) zq[q][c] = gw[c] * silu(zq[q][c]);
+          }
       }
+      __syncthreads();  // B
+
+      // ---- B: chunk p's gated norm and store; the v rows of chunk p+1 ----
+      if (p >= 0) {
+        if (a.gnorm) {
+          const f4 r = lds4(&sm.red[lane * kNC]);
+          sm.inv[w][lane] = rsqrtf(((r[0] + r[1]) + (r[2] + r[3])) / kDV + 1e-6f);
+          wave_sync();
+#pragma unroll
+          for (int q = 0; q < 8; q++) {
+            const float iv = sm.inv[w][8 * q + er];
+#pragma unroll
+            for (int c = 0; c < 4; c++) Y[q][c] = Y[q][c] * iv * zq[q][c];
+          }
+        }
+        if (plain) {
+          char* ob = (char*)a.out + ((size_t)b * a.L + (c0 - a.P)) * (size_t)orowb + (size_t)h * kDV * sizeof(T);
+          const unsigned oo = (unsigned)er * orowb + ec * (unsigned)sizeof(T);
+#pragma unroll
+          for (int q = 0; q < 8; q++) store4(gpw<T>(ob + (size_t)(8 * q) * orowb + oo), Y[q]);
+        } else {
+          __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + ec;
+#pragma unroll
+          for (int q = 0; q < 8; q++) {
+            const int t = 8 * q + er, r = c0 + t;
+            if (t < m && r >= a.P) store4(ob + (size_t)(r - a.P) * (a.H * kDV), Y[q]);
+          }
+        }
+      }
+      if (p + 1 >= nchunks) break;
+      fetch_v(c1);
+      __syncthreads();  // C
+      // ---- C: score / A tiles of chunk p+1, then the first half of its v conv ----
+      kkt_qkt(grp, c16);
+      consume_vconv(c1, 0);
+      __syncthreads();  // E
+      consume_vconv(c1, 4);
+      __syncthreads();  // A
     }
-    if (plain) {
-      char* ob = (char*)a.out + ((size_t)b * a.L + (c0 - a.P)) * (size_t)orowb + (size_t)h * kDV * sizeof(T);
-      const unsigned oo = (unsigned)er * orowb + ec * (unsigned)sizeof(T);
+    const int g0 = (tid0 & 63) >> 4, l16 = tid0 & 15;
 #pragma unroll
-      for (int q = 0; q < 4; q++) store4(gpw<T>(ob + (size_t)(16 * q) * orowb + oo), Y[q]);
-    } else {
-      __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + ec;
+    for (int ct = 0; ct < 2; ct++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int t = 16 * q + er, r = c0 + t;
-        if (t < m && r >= a.P) store4(ob + (size_t)(r - a.P) * (a.H * kDV), Y[q]);
+      for (int it = 0; it < 8; it++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16] = S[ct][it][e];
+  } else {
+    fetch_qk(a.s0);
+    if (w == kGW) produce_gates(a.s0);
+    for (int p = -1; p < nchunks; p++) {
+      const int c1 = a.s0 + kCH * (p + 1);
+      const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
+
+      // ---- A: conv of chunk p+1 in registers; raw q/k rows (and a/b) of chunk p+2 ----
+      if (p + 1 < nchunks) {
+        produce_conv(c1);
+        if (p + 2 < nchunks) fetch_qk(c1 + kCH);
       }
+      __syncthreads();  // B
+
+      // ---- B: q^, k^, k^T and the gate vectors of chunk p+1 to LDS ----
+      if (p + 1 >= nchunks) break;
+      produce_write();
+      __syncthreads();  // C
+
+      // ---- C: score / A tiles; the gate producer makes the diagonal blocks of A and solves them ----
+      if (w == kGW) {
+#pragma unroll
+        for (int d = 0; d < 4; d++) kkt_qkt_tile(false, d * (d + 3) / 2, grp, c16);
+        wave_sync();
+        // lane (grp, c16): column c16 of diagonal block grp, rows in order (left-looking); row r of A is read as a
+        // broadcast shared by the 16 lanes of the block
+        const int base = 16 * grp;
+        float pc[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float* ar = &sm.Tm[(base + r) * kAP + base];
+          float acc = r == c16 ? 1.0f : 0.0f;
+#pragma unroll
+          for (int j = 0; j < r; j++) acc = fmaf(-ar[j], pc[j], acc);
+          pc[r] = acc;
+        }
+        const float cb = sm.bt[base + c16], cbw = cb * sm.eg[base + c16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          sm.Tm[(base + r) * kAP + base + c16] = pc[r];
+          sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cb);
+          sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cbw);
+        }
+      } else {
+        kkt_qkt(grp, c16);
+      }
+      __syncthreads();  // E
+
+      // ---- E: off-diagonal block columns of T; the gate vectors of chunk p+2 ----
+      if (w == kNC)
+        t_column<0>(sm, grp, c16);
+      else if (w == kNC + 1)
+        t_column<1>(sm, grp, c16);
+      else if (w == kNC + 2)
+        t_column<2>(sm, grp, c16);
+      else if (p + 2 < nchunks)
+        produce_gates(c1 + kCH);
+      __syncthreads();  // A
+      (void)lane;
     }
   }
-#pragma unroll
-  for (int it = 0; it < 8; it++)
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-      gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * ((tid0 & 63) >> 4) + e) * kDV + 16 * w + (tid0 & 15)] = S[it][e];
 }
 
 template <typename T>
