@@ -42,6 +42,31 @@ constexpr int kHD = 256, kBQ = 32, kBK = 64;
 constexpr size_t kAttnLds = sizeof(_Float16) * (size_t)(4 * kBK * kHD);  // two K + V^T tile buffers
 constexpr float kRescale = 8.0f;    // log2 headroom before the reference max is raised
 
+// An identity the compiler cannot see through: lane indices re-derived from it on every tile keep the address
+// arithmetic built on them inside the loop instead of hoisted out of it (and spilled).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// max / sum of x over lanes l and l ^ 32: v_permlane32_swap hands every lane both values (in an order that depends
+// on the half, which neither a max nor a two-term sum sees)
+__device__ __forceinline__ void both_halves(float x, float& u, float& v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+  u = __builtin_bit_cast(float, (unsigned)r[0]);
+  v = __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ float max_halves(float x) {
+  float u, v;
+  both_halves(x, u, v);
+  return fmaxf(u, v);
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  float u, v;
+  both_halves(x, u, v);
+  return u + v;
+}
+
 __device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 template <typename T>
@@ -125,7 +150,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   const int id = blockIdx.x;
   const int pair = id % npair, qb = nqb - 1 - id / npair;
   const int b = pair / a.HK, kh = pair % a.HK;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int h = kh * 4 + (wave & 3);
   const int half = lane >> 5, c32 = lane & 31;
   const int q0 = qb * kRows + 32 * (wave >> 2);
@@ -138,32 +163,38 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   gptr<_Float16> Kg = gp<_Float16>(a.K) + kvb;
   gptr<_Float16> Vg = gp<_Float16>(a.V) + kvb;
 
-  // a tile = 32 K instructions (2 keys each) + 32 V^T instructions (8 dims each); each wave issues 4 + 4
-  auto issue = [&](int kt, int buf) {
+  // a tile = 32 K instructions (2 keys each) + 32 V^T instructions (8 dims each); each wave issues 4 + 4. The
+  // lane's share of the addresses is re-derived from `ln` on every call (cheap VALU) rather than kept live across the
+  // loop: spilled addresses would be reloaded through the same counter the tile loads are waited on.
+  auto issue = [&](int kt, int buf, int ln) {
     _Float16* kb = lds + (size_t)buf * 2 * kTileHalves;
     _Float16* vb = kb + kTileHalves;
+    const char* kg = (const char*)(Kg + (size_t)kt * kBK * kHD);
+    const char* vg = (const char*)(Vg + (size_t)kt * kBK);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int ins = wave + kWaves * i;             // 0..31
-      const int r = 2 * ins + (lane >> 5), js = lane & 31;
+      const int r = 2 * ins + (ln >> 5), js = ln & 31;
       const int j = js ^ (r & 31);                   // global chunk that belongs in slot js
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(Kg + (size_t)(kt * kBK + r) * kHD + 8 * j),
+      const unsigned ko = (unsigned)(r * kHD + 8 * j) * 2u;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kg + ko),
                                        (__attribute__((address_space(3))) void*)(kb + (size_t)ins * 512), 16, 0, 0);
-      const int d = 8 * ins + (lane >> 3), cs = lane & 7;
-      const int c = cs ^ (d & 7);
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(Vg + (size_t)d * a.LT + kt * kBK + 8 * c),
+      const int d = 8 * ins + (ln >> 3), cs = ln & 7;
+      const int c = cs ^ ((d >> 1) & 7);
+      const unsigned vo = ((unsigned)d * (unsigned)a.LT + 8u * c) * 2u;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vg + vo),
                                        (__attribute__((address_space(3))) void*)(vb + (size_t)ins * 512), 16, 0, 0);
     }
   };
-  issue(0, 0);
+  issue(0, 0, lane);
 
   // Q as the B operand of S^T = K Q^T (32x32x16): qreg[ks] = q[q0 + c32][16 ks + 8 half .. +7], prepared here:
   // RMSNorm (the two halves of a row sit in lanes l and l + 32), RoPE (dim i < 32 in ks 0/1 pairs with i + 32 in
-  // ks 2/3 of the same lane and element), then f16(f16(.) / sqrt(HD)).
+  // ks 2/3 of the same lane and element), then f16(f16(.) / sqrt(HD)). A row past the end (t >= L) repeats row
+  // L - 1: rows are independent and such a row is never stored, so every load here is unconditional.
   h8 qreg[16];
   {
-    const int t = q0 + c32;
-    const int tc = min(t, a.L - 1);
+    const int tc = min(q0 + c32, a.L - 1);
     gptr<T> src = gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD;
     float ss = 0.0f;
 #pragma unroll
@@ -171,38 +202,42 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
       float qv[8];
       load8f<T>(src + 16 * ks + 8 * half, qv);
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        ss += qv[e] * qv[e];
-        qreg[ks][e] = (_Float16)0.0f;
-      }
+      for (int e = 0; e < 8; e++) ss += qv[e] * qv[e];
     }
     ss += __shfl_xor(ss, 32);
+    asm volatile("" ::: "memory");
     const float inv = rsqrtf(ss / kHD + 1e-6f);
     const int pos = a.P + tc;
     const float scale = rsqrtf((float)kHD);
+    gptr<float> rp = gp<float>(a.rope) + (size_t)pos * RD;
     // dims 0..63 (slots ks 0..3): normalise, rotate pairs (ks, ks + 2), scale
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      float x1[8], x2[8];
+      float x1[8], x2[8], w1[8], w2[8], cz[16];
       load8f<T>(src + 16 * ks + 8 * half, x1);
       load8f<T>(src + 16 * (ks + 2) + 8 * half, x2);
+      load8f<float>(gp<float>(a.qw) + 16 * ks + 8 * half, w1);
+      load8f<float>(gp<float>(a.qw) + 16 * ks + 8 * half + 32, w2);
+      load8f<float>(rp + 2 * (16 * ks + 8 * half), cz);
+      load8f<float>(rp + 2 * (16 * ks + 8 * half) + 8, cz + 8);
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const int i = 16 * ks + 8 * half + e;
-        const float n1 = x1[e] * inv * gp<float>(a.qw)[i], n2 = x2[e] * inv * gp<float>(a.qw)[i + 32];
-        const float cs = gp<float>(a.rope)[(size_t)pos * RD + 2 * i], sn = gp<float>(a.rope)[(size_t)pos * RD + 2 * i + 1];
-        qreg[ks][e] = t < a.L ? (_Float16)((float)(_Float16)(n1 * cs - n2 * sn) * scale) : (_Float16)0.0f;
-        qreg[ks + 2][e] = t < a.L ? (_Float16)((float)(_Float16)(n2 * cs + n1 * sn) * scale) : (_Float16)0.0f;
+        const float n1 = x1[e] * inv * w1[e], n2 = x2[e] * inv * w2[e];
+        const float cs = cz[2 * e], sn = cz[2 * e + 1];
+        qreg[ks][e] = (_Float16)((float)(_Float16)(n1 * cs - n2 * sn) * scale);
+        qreg[ks + 2][e] = (_Float16)((float)(_Float16)(n2 * cs + n1 * sn) * scale);
       }
+      // pins the finished operands here and keeps later loads below this point: registers are scarce
+      asm volatile("" : "+v"(qreg[ks]), "+v"(qreg[ks + 2])::"memory");
     }
 #pragma unroll
     for (int ks = 4; ks < 16; ks++) {
-      float qv[8];
+      float qv[8], wv[8];
       load8f<T>(src + 16 * ks + 8 * half, qv);
+      load8f<float>(gp<float>(a.qw) + 16 * ks + 8 * half, wv);
 #pragma unroll
-      for (int e = 0; e < 8; e++)
-        qreg[ks][e] = t < a.L ? (_Float16)((float)(_Float16)(qv[e] * inv * gp<float>(a.qw)[16 * ks + 8 * half + e]) * scale)
-                              : (_Float16)0.0f;
+      for (int e = 0; e < 8; e++) qreg[ks][e] = (_Float16)((float)(_Float16)(qv[e] * inv * wv[e]) * scale);
+      asm volatile("" : "+v"(qreg[ks])::"memory");
     }
   }
 
@@ -216,31 +251,46 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // the lowest query position of this wave: tiles whose keys all lie at or below it need no causal mask
+  const int minpos = a.P + q0;
   for (int kt = 0; kt < ntiles; kt++) {
     const int cur = kt & 1;
-    if (kt + 1 < ntiles) issue(kt + 1, cur ^ 1);
-    const _Float16* ks_l = lds + (size_t)cur * 2 * kTileHalves;
-    const _Float16* vs_l = ks_l + kTileHalves;
+    const int ln = opaque(tid) & 63;
+    if (kt + 1 < ntiles) issue(kt + 1, cur ^ 1, ln);
+    // S^T row i of a 32-key half holds key pi(i) (bits 2 and 3 of i swapped): then the eight S^T values a lane
+    // holds for one 16-key step of P V are eight consecutive keys, and that step's V^T operand is one 16-byte read.
+    // K operand of k-step ks for key row r = pi(c32): chunk j = 2 ks + half sits in slot j ^ r, i.e. at byte
+    // (16 (r ^ half)) ^ (32 ks) of the row. V^T operand of dim d = 32 dt + c32, keys 8 c .. 8 c + 7: slot
+    // c ^ ((d >> 1) & 7) of the row.
+    const int lc = ln & 31, lh = ln >> 5;
+    const int pr = (lc & 19) | ((lc & 4) << 1) | ((lc & 8) >> 1);
+    const unsigned kbase = (unsigned)(cur * 2 * kTileHalves * 2) + (unsigned)pr * (kHD * 2) + 16u * (unsigned)(pr ^ lh);
+    const unsigned vbase = (unsigned)((cur * 2 + 1) * kTileHalves * 2) + (unsigned)lc * (kBK * 2) + 16u * (unsigned)((lc >> 1) & 7);
+    const bool masked = kt * kBK + kBK - 1 > minpos;
 
-    // the 64-key tile in two 32-key halves kk; S^T[key 32 kk + 8 (v/4) + 4 half + v%4][row c32]
+    // the 64-key tile in two 32-key halves kk; st[v] = S^T[key 32 kk + 16 (v/8) + 8 half + v%8][row c32]
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
       f16v st = f16v{};
 #pragma unroll
       for (int ks = 0; ks < 16; ks++) {
-        const int r = 32 * kk + c32, j = 2 * ks + half;
-        const h8 ka = *reinterpret_cast<const h8*>(ks_l + (size_t)r * kHD + 8 * (j ^ (r & 31)));
+        const h8 ka = *reinterpret_cast<const h8*>(lds_raw + ((kbase + (unsigned)(kk * 32 * kHD * 2)) ^ (32u * ks)));
         st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[ks], st, 0, 0, 0);
       }
       float mx = -INFINITY;
+      if (masked) {
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int key = kt * kBK + 32 * kk + 8 * (v >> 2) + 4 * half + (v & 3);
-        const float sv = key <= rowpos ? st[v] * log2e : -INFINITY;
-        st[v] = sv;
-        mx = fmaxf(mx, sv);
+        for (int v = 0; v < 16; v++) {
+          const int key = kt * kBK + 32 * kk + 16 * (v >> 3) + 8 * half + (v & 7);
+          st[v] = key <= rowpos ? st[v] * log2e : -INFINITY;
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; v++) st[v] *= log2e;
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+#pragma unroll
+      for (int v = 0; v < 16; v++) mx = fmaxf(mx, st[v]);
+      mx = max_halves(mx);
       // raise the reference max only when a score would exceed it by 2^kRescale (decided per row)
       const float mnew = mx > mref + kRescale ? mx : mref;
       const float alpha = __builtin_amdgcn_exp2f(mref - mnew);  // exactly 1 when unchanged, 0 on a row's first keys
@@ -253,34 +303,27 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
         st[v] = pv;
         sum += pv;
       }
-      sum += __shfl_xor(sum, 32);
+      sum = sum_halves(sum);
       lsum = lsum * alpha + sum;
       if (__any(need)) {
         // O rows 8 (v/4) + 4 half + v%4 take alpha from lane (row) in the low half
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-          const float al = __shfl(alpha, 8 * (v >> 2) + 4 * half + (v & 3));
+          const float al = __shfl(alpha, 8 * (v >> 2) + 4 * (opaque(lane) >> 5) + (v & 3));
 #pragma unroll
           for (int dt = 0; dt < 8; dt++) O[dt][v] *= al;
         }
       }
-      // P V: k-step kb covers keys 32 kk + 16 kb + {4 half + r, 8 + 4 half + r} (the S^T accumulator order)
+      // P V: k-step kb covers keys 32 kk + 16 kb + 8 half + e, e < 8, which are st[8 kb + e]
 #pragma unroll
       for (int kb = 0; kb < 2; kb++) {
         h8 pa;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          pa[r] = (_Float16)st[8 * kb + r];
-          pa[4 + r] = (_Float16)st[8 * kb + 4 + r];
-        }
-        const int c0 = 2 * (2 * kk + kb);  // V^T chunks c0, c0 + 1 hold these 16 positions
+        for (int e = 0; e < 8; e++) pa[e] = (_Float16)st[8 * kb + e];
+        const unsigned vo = vbase ^ (unsigned)(16 * (4 * kk + 2 * kb + lh));
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-          const int d = 32 * dt + c32;
-          const _Float16* vr = vs_l + (size_t)d * kBK;
-          const h4 lo = *reinterpret_cast<const h4*>(vr + 8 * (c0 ^ (d & 7)) + 4 * half);
-          const h4 hi = *reinterpret_cast<const h4*>(vr + 8 * ((c0 + 1) ^ (d & 7)) + 4 * half);
-          const h8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const h8 vb = *reinterpret_cast<const h8*>(lds_raw + vo + (unsigned)(dt * 32 * kBK * 2));
           O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, vb, O[dt], 0, 0, 0);
         }
       }
@@ -289,19 +332,21 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
     __syncthreads();                // ... and every wave's; nobody reads the current buffer any more
   }
 
-  // epilogue: out[t][h][d] = O / l * sigmoid(gate)
+  // epilogue: out[t][h][d] = O / l * sigmoid(gate); gate loads are unconditional (row clamped), stores predicated
 #pragma unroll
   for (int v = 0; v < 16; v++) {
     const float linv = 1.0f / __shfl(lsum, 8 * (v >> 2) + 4 * half + (v & 3));
-    const int t = q0 + 8 * (v >> 2) + 4 * half + (v & 3);
-    if (t >= a.L) continue;
-    gptr<T> grow = gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)h * 2 * kHD + kHD;
-    __attribute__((address_space(1))) T* orow = gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD;
+    const int t = q0 + 8 * (v >> 2) + 4 * half + (v & 3), tc = min(t, a.L - 1);
+    gptr<T> grow = gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD;
+    __attribute__((address_space(1))) T* orow = gpw<T>(a.out) + ((size_t)b * a.L + tc) * (size_t)(a.HQ * kHD) + (size_t)h * kHD;
+    float g[8];
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-      const int d = 32 * dt + c32;
-      orow[d] = (T)(O[dt][v] * linv * sigmoid((float)grow[d]));
+    for (int dt = 0; dt < 8; dt++) g[dt] = (float)grow[32 * dt + c32];
+    if (t < a.L) {
+#pragma unroll
+      for (int dt = 0; dt < 8; dt++) orow[32 * dt + c32] = (T)(O[dt][v] * linv * sigmoid(g[dt]));
     }
+    asm volatile("" ::: "memory");  // one row's gate loads in flight at a time (O holds half the registers)
   }
 }
 
