@@ -39,7 +39,12 @@ template <typename T>
 __device__ __forceinline__ __attribute__((address_space(1))) T* gpw(void* p) { return (__attribute__((address_space(1))) T*)(p); }
 
 constexpr int kHD = 256, kBQ = 32, kBK = 64;
-constexpr size_t kAttnLds = sizeof(_Float16) * (size_t)(4 * kBK * kHD);  // two K + V^T tile buffers
+constexpr int kEP = 136;  // row pitch (floats) of the epilogue staging area: rows r and r + 4 sit 32 banks apart
+// two K + V^T tile buffers; after the tile loop, each wave's 32 x 128 f32 epilogue staging area
+constexpr int kTileBytes = kBK * kHD * 2;  // one K tile or one V^T tile (f16)
+// LDS: two (K, V^T) tile buffers; after the tile loop, each wave's 32 x 128 f32 epilogue staging area
+constexpr size_t kAttnLds = 4 * (size_t)kTileBytes > sizeof(float) * 8 * 32 * kEP ? 4 * (size_t)kTileBytes
+                                                                                  : sizeof(float) * 8 * 32 * kEP;
 constexpr float kRescale = 8.0f;    // log2 headroom before the reference max is raised
 
 // An identity the compiler cannot see through: lane indices re-derived from it on every tile keep the address
@@ -47,6 +52,27 @@ constexpr float kRescale = 8.0f;    // log2 headroom before the reference max is
 __device__ __forceinline__ int opaque(int x) {
   asm volatile("" : "+v"(x));
   return x;
+}
+
+__device__ __forceinline__ f4 ld4(gptr<float> p) { return *(gptr<f4>)(p); }
+__device__ __forceinline__ f4 ld4(gptr<_Float16> p) {
+  const h4 x = *(gptr<h4>)(p);
+  return f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+}
+__device__ __forceinline__ void store4(__attribute__((address_space(1))) float* p, const f4& v) {
+  *(__attribute__((address_space(1))) f4*)(p) = v;
+}
+__device__ __forceinline__ void store4(__attribute__((address_space(1))) _Float16* p, const f4& v) {
+  *(__attribute__((address_space(1))) h4*)(p) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+}
+
+__device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+
+// Orders a wave's LDS writes before its later reads of other lanes' entries (no workgroup barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // max / sum of x over lanes l and l ^ 32: v_permlane32_swap hands every lane both values (in an order that depends
@@ -135,10 +161,10 @@ constexpr int kWaves = 8;
 
 template <typename T>
 __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
-  // Two LDS buffers of one 64-key tile each. K tile: key r at [r][32 chunks of 8 dims], chunk j stored in slot
-  // j ^ (r & 31); V^T tile: dim d at [d][8 chunks of 8 positions], chunk c stored in slot c ^ (d & 7). A wave's
-  // global_load_lds_dwordx4 covers whole 512 B K rows or 128 B V^T rows (coalesced), and the XOR swizzle spreads
-  // the 32 rows an MFMA operand read touches over the LDS banks.
+  // LDS: tile buffer i (i < 2) at i * 2 kTileBytes: K tile, then V^T tile.
+  // K tile: key r at [r][32 chunks of 8 dims], chunk j stored in slot j ^ (r & 31); V^T tile: dim d at [d][8 chunks
+  // of 8 positions], chunk c stored in slot c ^ ((d >> 1) & 7). A wave's global_load_lds_dwordx4 covers whole 512 B
+  // K rows or 128 B V^T rows (coalesced), and the XOR swizzles make every MFMA operand read conflict-free.
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   constexpr int kTileHalves = kBK * kHD;
   _Float16* lds = reinterpret_cast<_Float16*>(lds_raw);
@@ -166,8 +192,8 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   // a tile = 32 K instructions (2 keys each) + 32 V^T instructions (8 dims each); each wave issues 4 + 4. The
   // lane's share of the addresses is re-derived from `ln` on every call (cheap VALU) rather than kept live across the
   // loop: spilled addresses would be reloaded through the same counter the tile loads are waited on.
-  auto issue = [&](int kt, int buf, int ln) {
-    _Float16* kb = lds + (size_t)buf * 2 * kTileHalves;
+  auto issue = [&](int kt, int ln) {
+    _Float16* kb = lds + (size_t)(kt & 1) * 2 * kTileHalves;
     _Float16* vb = kb + kTileHalves;
     const char* kg = (const char*)(Kg + (size_t)kt * kBK * kHD);
     const char* vg = (const char*)(Vg + (size_t)kt * kBK);
@@ -186,167 +212,250 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
                                        (__attribute__((address_space(3))) void*)(vb + (size_t)ins * 512), 16, 0, 0);
     }
   };
-  issue(0, 0, lane);
+  issue(0, lane);
 
   // Q as the B operand of S^T = K Q^T (32x32x16): qreg[ks] = q[q0 + c32][16 ks + 8 half .. +7], prepared here:
   // RMSNorm (the two halves of a row sit in lanes l and l + 32), RoPE (dim i < 32 in ks 0/1 pairs with i + 32 in
   // ks 2/3 of the same lane and element), then f16(f16(.) / sqrt(HD)). A row past the end (t >= L) repeats row
   // L - 1: rows are independent and such a row is never stored, so every load here is unconditional.
+  // qw (the stored 1 + w) is staged in LDS (tile buffer 1, unused until the loop): every lane needs 128 of the 256
+  // weights, the same ones as every other lane of its half.
+  float* qw_l = reinterpret_cast<float*>(lds_raw + 2 * (size_t)kTileBytes);
+  if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = *(gptr<f4>)(gp<float>(a.qw) + 4 * tid);
   h8 qreg[16];
   {
     const int tc = min(q0 + c32, a.L - 1);
     gptr<T> src = gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD;
-    float ss = 0.0f;
+    // cos/sin pairs of dims i = 16 ks + 8 half + e (ks < 2): rz[ks] holds rope[pos][2 i], rope[pos][2 i + 1]
+    gptr<float> rp = gp<float>(a.rope) + (size_t)(a.P + tc) * RD + 16 * half;
+    f4 rz[2][4];
 #pragma unroll
-    for (int ks = 0; ks < 16; ks++) {
-      float qv[8];
-      load8f<T>(src + 16 * ks + 8 * half, qv);
+    for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-      for (int e = 0; e < 8; e++) ss += qv[e] * qv[e];
-    }
-    ss += __shfl_xor(ss, 32);
-    asm volatile("" ::: "memory");
-    const float inv = rsqrtf(ss / kHD + 1e-6f);
-    const int pos = a.P + tc;
+      for (int j = 0; j < 4; j++) rz[ks][j] = *(gptr<f4>)(rp + 32 * ks + 4 * j);
     const float scale = rsqrtf((float)kHD);
-    gptr<float> rp = gp<float>(a.rope) + (size_t)pos * RD;
-    // dims 0..63 (slots ks 0..3): normalise, rotate pairs (ks, ks + 2), scale
+    float ss = 0.0f;
+    // n(ks, e) = q * inv * w for dim 16 ks + 8 half + e, from the raw value x
+    auto finish = [&](int ks, const float* x, float inv) {
+      const f4 w0 = lds4(qw_l + 16 * ks + 8 * half), w1 = lds4(qw_l + 16 * ks + 8 * half + 4);
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      float x1[8], x2[8], w1[8], w2[8], cz[16];
-      load8f<T>(src + 16 * ks + 8 * half, x1);
-      load8f<T>(src + 16 * (ks + 2) + 8 * half, x2);
-      load8f<float>(gp<float>(a.qw) + 16 * ks + 8 * half, w1);
-      load8f<float>(gp<float>(a.qw) + 16 * ks + 8 * half + 32, w2);
-      load8f<float>(rp + 2 * (16 * ks + 8 * half), cz);
-      load8f<float>(rp + 2 * (16 * ks + 8 * half) + 8, cz + 8);
+      for (int e = 0; e < 8; e++) qreg[ks][e] = (_Float16)((float)(_Float16)(x[e] * inv * (e < 4 ? w0[e] : w1[e - 4])) * scale);
+    };
+    auto rotate = [&](int ks, const float* x1, const float* x2, float inv) {
+      const f4 w10 = lds4(qw_l + 16 * ks + 8 * half), w11 = lds4(qw_l + 16 * ks + 8 * half + 4);
+      const f4 w20 = lds4(qw_l + 16 * ks + 8 * half + 32), w21 = lds4(qw_l + 16 * ks + 8 * half + 36);
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const float n1 = x1[e] * inv * w1[e], n2 = x2[e] * inv * w2[e];
-        const float cs = cz[2 * e], sn = cz[2 * e + 1];
+        const float n1 = x1[e] * inv * (e < 4 ? w10[e] : w11[e - 4]), n2 = x2[e] * inv * (e < 4 ? w20[e] : w21[e - 4]);
+        const f4 c = rz[ks][e >> 1];
+        const float cs = c[2 * (e & 1)], sn = c[2 * (e & 1) + 1];
         qreg[ks][e] = (_Float16)((float)(_Float16)(n1 * cs - n2 * sn) * scale);
         qreg[ks + 2][e] = (_Float16)((float)(_Float16)(n2 * cs + n1 * sn) * scale);
       }
-      // pins the finished operands here and keeps later loads below this point: registers are scarce
-      asm volatile("" : "+v"(qreg[ks]), "+v"(qreg[ks + 2])::"memory");
-    }
+    };
+    if constexpr (sizeof(T) == 2) {
+      // f16 rows: the whole row slice (16 x 16 B) is loaded at once and converted in place
+      h8 raw[16];
 #pragma unroll
-    for (int ks = 4; ks < 16; ks++) {
-      float qv[8], wv[8];
-      load8f<T>(src + 16 * ks + 8 * half, qv);
-      load8f<float>(gp<float>(a.qw) + 16 * ks + 8 * half, wv);
+      for (int ks = 0; ks < 16; ks++) raw[ks] = *(gptr<h8>)(src + 16 * ks + 8 * half);
 #pragma unroll
-      for (int e = 0; e < 8; e++) qreg[ks][e] = (_Float16)((float)(_Float16)(qv[e] * inv * wv[e]) * scale);
-      asm volatile("" : "+v"(qreg[ks])::"memory");
+      for (int ks = 0; ks < 16; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss += (float)raw[ks][e] * (float)raw[ks][e];
+      const float inv = rsqrtf(sum_halves(ss) / kHD + 1e-6f);
+      __syncthreads();  // qw staged
+      // dims 0..63 (slots ks 0..3): normalise, rotate pairs (ks, ks + 2), scale
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        float x1[8], x2[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          x1[e] = (float)raw[ks][e];
+          x2[e] = (float)raw[ks + 2][e];
+        }
+        rotate(ks, x1, x2, inv);
+      }
+#pragma unroll
+      for (int ks = 4; ks < 16; ks++) {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = (float)raw[ks][e];
+        finish(ks, x, inv);
+      }
+    } else {
+      // f32 rows: two passes over the row slice, eight 32-byte loads in flight at a time
+#pragma unroll
+      for (int bt = 0; bt < 2; bt++) {
+        float qv[8][8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) load8f<T>(src + 16 * (8 * bt + k) + 8 * half, qv[k]);
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+          for (int e = 0; e < 8; e++) ss += qv[k][e] * qv[k][e];
+        asm volatile("" : "+v"(ss)::"memory");
+      }
+      const float inv = rsqrtf(sum_halves(ss) / kHD + 1e-6f);
+      __syncthreads();  // qw staged
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        float x1[8], x2[8];
+        load8f<T>(src + 16 * ks + 8 * half, x1);
+        load8f<T>(src + 16 * (ks + 2) + 8 * half, x2);
+        rotate(ks, x1, x2, inv);
+      }
+#pragma unroll
+      for (int bt = 0; bt < 3; bt++) {
+        float qv[4][8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) load8f<T>(src + 16 * (4 + 4 * bt + k) + 8 * half, qv[k]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) finish(4 + 4 * bt + k, qv[k], inv);
+        asm volatile("" : "+v"(qreg[4 + 4 * bt]), "+v"(qreg[5 + 4 * bt]), "+v"(qreg[6 + 4 * bt]), "+v"(qreg[7 + 4 * bt])::"memory");
+      }
     }
   }
 
   // row state: this lane's S^T columns are query row c32 (both halves hold it after the xor-32 reductions)
   float mref = -INFINITY, lsum = 0.0f;
-  f16v O[8];  // O[dt][v] = out row 8 (v/4) + 4 half + v%4, dim 32 dt + c32
-#pragma unroll
-  for (int dt = 0; dt < 8; dt++) O[dt] = f16v{};
   const int rowpos = a.P + q0 + c32;
   const float log2e = 1.4426950408889634f;
 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // O is zeroed from a value produced here, so its 128 registers are not claimed during the prologue's loads
+  f16v O[8];  // O[dt][v] = out row 8 (v/4) + 4 half + v%4, dim 32 dt + c32
+  {
+    float z = 0.0f;
+    asm volatile("" : "+v"(z));
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) O[dt] = f16v{} + z;
+  }
   // the lowest query position of this wave: tiles whose keys all lie at or below it need no causal mask
   const int minpos = a.P + q0;
-  for (int kt = 0; kt < ntiles; kt++) {
-    const int cur = kt & 1;
-    const int ln = opaque(tid) & 63;
-    if (kt + 1 < ntiles) issue(kt + 1, cur ^ 1, ln);
-    // S^T row i of a 32-key half holds key pi(i) (bits 2 and 3 of i swapped): then the eight S^T values a lane
-    // holds for one 16-key step of P V are eight consecutive keys, and that step's V^T operand is one 16-byte read.
-    // K operand of k-step ks for key row r = pi(c32): chunk j = 2 ks + half sits in slot j ^ r, i.e. at byte
-    // (16 (r ^ half)) ^ (32 ks) of the row. V^T operand of dim d = 32 dt + c32, keys 8 c .. 8 c + 7: slot
-    // c ^ ((d >> 1) & 7) of the row.
+
+  // S^T row i of a 32-key half holds key pi(i) (bits 2 and 3 of i swapped): then the eight S^T values a lane holds
+  // for one 16-key step of P V are eight consecutive keys, and that step's V^T operand is one 16-byte read.
+  // K operand of k-step ks for key row r = pi(c32): chunk j = 2 ks + half sits in slot j ^ r, i.e. at byte
+  // (16 (r ^ half)) ^ (32 ks) of the row. V^T operand of dim d = 32 dt + c32, keys 8 c .. 8 c + 7: slot
+  // c ^ ((d >> 1) & 7) of the row.
+  auto kbase_of = [&](int kt, int kk, int ln) {
     const int lc = ln & 31, lh = ln >> 5;
     const int pr = (lc & 19) | ((lc & 4) << 1) | ((lc & 8) >> 1);
-    const unsigned kbase = (unsigned)(cur * 2 * kTileHalves * 2) + (unsigned)pr * (kHD * 2) + 16u * (unsigned)(pr ^ lh);
-    const unsigned vbase = (unsigned)((cur * 2 + 1) * kTileHalves * 2) + (unsigned)lc * (kBK * 2) + 16u * (unsigned)((lc >> 1) & 7);
-    const bool masked = kt * kBK + kBK - 1 > minpos;
-
-    // the 64-key tile in two 32-key halves kk; st[v] = S^T[key 32 kk + 16 (v/8) + 8 half + v%8][row c32]
+    return (unsigned)((kt & 1) * 2 * kTileBytes + kk * 32 * kHD * 2) + (unsigned)pr * (kHD * 2) + 16u * (unsigned)(pr ^ lh);
+  };
+  auto vbase_of = [&](int kt, int ln) {
+    const int lc = ln & 31;
+    return (unsigned)(((kt & 1) * 2 + 1) * kTileBytes) + (unsigned)lc * (kBK * 2) + 16u * (unsigned)((lc >> 1) & 7);
+  };
+  // S^T = K Q^T for the 32-key half at kb (byte address of this lane's row in the K tile)
+  auto qk = [&](unsigned kb) {
+    f16v st = f16v{};
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-      f16v st = f16v{};
-#pragma unroll
-      for (int ks = 0; ks < 16; ks++) {
-        const h8 ka = *reinterpret_cast<const h8*>(lds_raw + ((kbase + (unsigned)(kk * 32 * kHD * 2)) ^ (32u * ks)));
-        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[ks], st, 0, 0, 0);
-      }
-      float mx = -INFINITY;
-      if (masked) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const int key = kt * kBK + 32 * kk + 16 * (v >> 3) + 8 * half + (v & 7);
-          st[v] = key <= rowpos ? st[v] * log2e : -INFINITY;
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; v++) st[v] *= log2e;
-      }
-#pragma unroll
-      for (int v = 0; v < 16; v++) mx = fmaxf(mx, st[v]);
-      mx = max_halves(mx);
-      // raise the reference max only when a score would exceed it by 2^kRescale (decided per row)
-      const float mnew = mx > mref + kRescale ? mx : mref;
-      const float alpha = __builtin_amdgcn_exp2f(mref - mnew);  // exactly 1 when unchanged, 0 on a row's first keys
-      const bool need = mnew != mref && mref != -INFINITY;
-      mref = mnew;
-      float sum = 0.0f;
+    for (int ks = 0; ks < 16; ks++) {
+      const h8 ka = *reinterpret_cast<const h8*>(lds_raw + (kb ^ (32u * ks)));
+      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[ks], st, 0, 0, 0);
+    }
+    return st;
+  };
+  // online softmax of one 32-key half (keys kt * 64 + 32 kk + 16 (v/8) + 8 half + v%8 in st[v]) -> f16 P in pa
+  auto softmax = [&](f16v& st, int kt, int kk, h8* pa) {
+    if (kt * kBK + kBK - 1 > minpos) {
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const float pv = __builtin_amdgcn_exp2f(st[v] - mnew);
-        st[v] = pv;
-        sum += pv;
+        const int key = kt * kBK + 32 * kk + 16 * (v >> 3) + 8 * half + (v & 7);
+        st[v] = key <= rowpos ? st[v] : -INFINITY;
       }
-      sum = sum_halves(sum);
-      lsum = lsum * alpha + sum;
-      if (__any(need)) {
-        // O rows 8 (v/4) + 4 half + v%4 take alpha from lane (row) in the low half
+    }
+    float mx = -INFINITY;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const float al = __shfl(alpha, 8 * (v >> 2) + 4 * (opaque(lane) >> 5) + (v & 3));
+    for (int v = 0; v < 16; v++) mx = fmaxf(mx, st[v]);
+    mx = max_halves(mx) * log2e;
+    // raise the reference max only when a score would exceed it by 2^kRescale (decided per row)
+    const float mnew = mx > mref + kRescale ? mx : mref;
+    const float alpha = __builtin_amdgcn_exp2f(mref - mnew);  // exactly 1 when unchanged, 0 on a row's first keys
+    const bool need = mnew != mref && mref != -INFINITY;
+    mref = mnew;
+    float sum = 0.0f;
 #pragma unroll
-          for (int dt = 0; dt < 8; dt++) O[dt][v] *= al;
-        }
+    for (int v = 0; v < 16; v++) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(st[v], log2e, -mnew));
+      st[v] = pv;
+      sum += pv;
+    }
+    lsum = lsum * alpha + sum_halves(sum);
+    if (__any(need)) {
+      // O rows 8 (v/4) + 4 half + v%4 take alpha from lane (row) in the low half
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const float al = __shfl(alpha, 8 * (v >> 2) + 4 * (opaque(lane) >> 5) + (v & 3));
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) O[dt][v] *= al;
       }
-      // P V: k-step kb covers keys 32 kk + 16 kb + 8 half + e, e < 8, which are st[8 kb + e]
+    }
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        h8 pa;
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) pa[e] = (_Float16)st[8 * kb + e];
-        const unsigned vo = vbase ^ (unsigned)(16 * (4 * kk + 2 * kb + lh));
+      for (int e = 0; e < 8; e++) pa[kb][e] = (_Float16)st[8 * kb + e];
+  };
+  // O += P V for the 32-key half kk: k-step kb covers keys 32 kk + 16 kb + 8 half + e (vb = this lane's V^T row)
+  auto pv = [&](const h8* pa, int kk, unsigned vb, int ln) {
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-          const h8 vb = *reinterpret_cast<const h8*>(lds_raw + vo + (unsigned)(dt * 32 * kBK * 2));
-          O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, vb, O[dt], 0, 0, 0);
-        }
+    for (int kb = 0; kb < 2; kb++) {
+      const unsigned vo = vb ^ (unsigned)(16 * (4 * kk + 2 * kb + (ln >> 5)));
+#pragma unroll
+      for (int dt = 0; dt < 8; dt++) {
+        const h8 vv = *reinterpret_cast<const h8*>(lds_raw + vo + (unsigned)(dt * 32 * kBK * 2));
+        O[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[kb], vv, O[dt], 0, 0, 0);
       }
+    }
+  };
+
+  for (int kt = 0; kt < ntiles; kt++) {
+    const int ln = opaque(tid) & 63;
+    if (kt + 1 < ntiles) issue(kt + 1, ln);
+    h8 pa[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      f16v st = qk(kbase_of(kt, kk, ln));
+      softmax(st, kt, kk, pa);
+      pv(pa, kk, vbase_of(kt, ln), ln);
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next tile has landed
     __syncthreads();                // ... and every wave's; nobody reads the current buffer any more
   }
 
-  // epilogue: out[t][h][d] = O / l * sigmoid(gate); gate loads are unconditional (row clamped), stores predicated
+  // epilogue: out[t][h][d] = O / l * sigmoid(gate), through LDS (free after the loop's last barrier). Each wave
+  // stages 32 rows x 128 dims of O / l at a time; then a lane handles 4 consecutive dims of a row (rows 2 i + er),
+  // so gate loads and output stores are 8- or 16-byte accesses, all issued before they are needed.
+  float* ep = reinterpret_cast<float*>(lds_raw) + (size_t)wave * 32 * kEP;
+  float linv[16];
 #pragma unroll
-  for (int v = 0; v < 16; v++) {
-    const float linv = 1.0f / __shfl(lsum, 8 * (v >> 2) + 4 * half + (v & 3));
-    const int t = q0 + 8 * (v >> 2) + 4 * half + (v & 3), tc = min(t, a.L - 1);
-    gptr<T> grow = gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD;
-    __attribute__((address_space(1))) T* orow = gpw<T>(a.out) + ((size_t)b * a.L + tc) * (size_t)(a.HQ * kHD) + (size_t)h * kHD;
-    float g[8];
+  for (int v = 0; v < 16; v++) linv[v] = 1.0f / __shfl(lsum, 8 * (v >> 2) + 4 * half + (v & 3));
+  const int er = lane >> 5, ec = 4 * (lane & 31);
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) g[dt] = (float)grow[32 * dt + c32];
-    if (t < a.L) {
+  for (int p = 0; p < 2; p++) {
+    f4 g[16];
 #pragma unroll
-      for (int dt = 0; dt < 8; dt++) orow[32 * dt + c32] = (T)(O[dt][v] * linv * sigmoid(g[dt]));
+    for (int i = 0; i < 16; i++) {
+      const int tc = min(q0 + 2 * i + er, a.L - 1);
+      g[i] = ld4(gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD + 128 * p + ec);
     }
-    asm volatile("" ::: "memory");  // one row's gate loads in flight at a time (O holds half the registers)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) ep[(8 * (v >> 2) + 4 * half + (v & 3)) * kEP + 32 * j + c32] = O[4 * p + j][v] * linv[v];
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int t = q0 + 2 * i + er;
+      const f4 o = lds4(ep + (2 * i + er) * kEP + ec);
+      f4 r;
+#pragma unroll
+      for (int c = 0; c < 4; c++) r[c] = o[c] * sigmoid(g[i][c]);
+      if (t < a.L) store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + 128 * p + ec, r);
+    }
+    wave_sync();
   }
 }
 
