@@ -721,6 +721,9 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
 
       // ---- A: conv of chunk p+1 in registers; raw q/k rows (and a/b) of chunk p+2 ----
+      // Wave priorities: each segment's longest wave (the gate producer in B and C, the block-column-0 wave in E) is
+      // raised so the SIMD it shares with a consumer issues for it first; in A all run at the base priority.
+      __builtin_amdgcn_s_setprio(0);
       if (p + 1 < nchunks) {
         produce_conv(c1);
         if (p + 2 < nchunks) fetch_qk(c1 + kCH);
@@ -729,6 +732,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
 
       // ---- B: q^, k^, k^T and the gate vectors of chunk p+1 to LDS ----
       if (p + 1 >= nchunks) break;
+      if (w == kGW) __builtin_amdgcn_s_setprio(2);
       produce_write();
       __syncthreads();  // C
 
@@ -762,6 +766,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       __syncthreads();  // E
 
       // ---- E: off-diagonal block columns of T; the gate vectors of chunk p+2 ----
+      if (w == kNC)
+        __builtin_amdgcn_s_setprio(2);
+      else
+        __builtin_amdgcn_s_setprio(0);
       if (w == kNC)
         t_column<0>(sm, grp, c16);
       else if (w == kNC + 1)
