@@ -207,21 +207,37 @@ __device__ __forceinline__ void t_column(Lds& sm, int grp, int c16) {
   f4 Tc[4];
 #pragma unroll
   for (int e = 0; e < 4; e++) Tc[J][e] = sm.Tm[(16 * J + 4 * grp + e) * kAP + cj];
+  // X[bi] accumulates sum_k A_bi,k T_kJ. The terms with k = J only need the diagonal block, so they are all issued
+  // first; after that each block row adds just the term of the block found last, so the dependent chain per block
+  // row is one product plus the multiplication by T_ii.
+  f4 X[4];
+#pragma unroll
+  for (int bi = J + 1; bi < 4; bi++) {
+    const f4 av = lds4(&sm.Tm[(16 * bi + c16) * kAP + 16 * J + 4 * grp]);
+    X[bi] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 4; e++) X[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[J][e], X[bi], 0, 0, 0);
+  }
 #pragma unroll
   for (int bi = J + 1; bi < 4; bi++) {
     const float* arow = &sm.Tm[(16 * bi + c16) * kAP];
-    f4 X = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bi > J + 1) {
+      const f4 av = lds4(arow + 16 * (bi - 1) + 4 * grp);
 #pragma unroll
-    for (int k = J; k < bi; k++) {
-      const f4 av = lds4(arow + 16 * k + 4 * grp);
-#pragma unroll
-      for (int e = 0; e < 4; e++) X = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[k][e], X, 0, 0, 0);
+      for (int e = 0; e < 4; e++) X[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[bi - 1][e], X[bi], 0, 0, 0);
     }
     const f4 tv = lds4(arow + 16 * bi + 4 * grp);
     f4 Y = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int e = 0; e < 4; e++) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(tv[e], X[e], Y, 0, 0, 0);
+    for (int e = 0; e < 4; e++) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(tv[e], X[bi][e], Y, 0, 0, 0);
     Tc[bi] = -Y;
+    // the middle terms A_b,bi T_bi,J of the rows below, now that T_bi,J is known
+#pragma unroll
+    for (int b2 = bi + 2; b2 < 4; b2++) {
+      const f4 av = lds4(&sm.Tm[(16 * b2 + c16) * kAP + 16 * bi + 4 * grp]);
+#pragma unroll
+      for (int e = 0; e < 4; e++) X[b2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[bi][e], X[b2], 0, 0, 0);
+    }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const int t = 16 * bi + 4 * grp + e;
