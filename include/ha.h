@@ -46,7 +46,10 @@ typedef enum ha_status {
 
 typedef enum ha_layer_kind {
   HA_LINEAR_ATTENTION = 0, /* manifest layer_types "linear_attention" */
-  HA_FULL_ATTENTION = 1    /* manifest layer_types "full_attention" */
+  HA_FULL_ATTENTION = 1,   /* manifest layer_types "full_attention" */
+  HA_ADAPTER = 2           /* manifest layer_types "adapter": a projection + bias stand-in with no token mixer
+                              (engine.js:256-261); the engine keeps no state for it and ha_forward skips it, so its
+                              layer_in / layer_out entries may be NULL */
 } ha_layer_kind;
 
 typedef enum ha_dtype { HA_F32 = 0, HA_F16 = 1 } ha_dtype;

@@ -121,6 +121,7 @@ int check_config(const ha_config* c) {
   for (int i = 0; i < c->n_layers; i++) {
     if (c->layer_kind[i] == HA_LINEAR_ATTENTION) lin = true;
     else if (c->layer_kind[i] == HA_FULL_ATTENTION) full = true;
+    else if (c->layer_kind[i] == HA_ADAPTER) continue;
     else return fail(HA_ERR_ARG, "layer " + std::to_string(i) + ": unknown layer kind " + std::to_string(c->layer_kind[i]));
   }
   if (lin) {
@@ -243,7 +244,7 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
           hipMemset(l.dtb, 0, sizeof(float) * c.H) != hipSuccess || hipMemset(l.tail, 0, esz * B * kTailCap * c.lin_stride) != hipSuccess)
         return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
       if ((rc = fill_f32(l.gnorm, c.DV, 1.0f))) return bail(rc);
-    } else {
+    } else if (l.kind == HA_FULL_ATTENTION) {
       e->any_full = true;
       const size_t kv = B * c.HK * (size_t)c.max_ctx * c.HD;
       if ((rc = dalloc(&l.qn, sizeof(float) * c.HD)) || (rc = dalloc(&l.kn, sizeof(float) * c.HD)) ||
@@ -303,7 +304,7 @@ int ha_set_param(ha_engine* e, int layer, const char* name, const float* host, s
     else if (n == "neg_exp_A") { dst = l.negA; want = c.H; }
     else if (n == "dt_bias") { dst = l.dtb; want = c.H; }
     else if (n == "gnorm") { dst = l.gnorm; want = c.DV; }
-  } else {
+  } else if (l.kind == HA_FULL_ATTENTION) {
     if (n == "q_norm") { dst = l.qn; want = c.HD; }
     else if (n == "k_norm") { dst = l.kn; want = c.HD; }
   }
@@ -324,7 +325,8 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   if (L <= 0) return fail(HA_ERR_ARG, "L must be > 0");
   if (!layer_in || !layer_out) return fail(HA_ERR_ARG, "layer_in and layer_out must be non-NULL");
   for (int i = 0; i < c.n_layers; i++)
-    if (!layer_in[i] || !layer_out[i]) return fail(HA_ERR_ARG, "layer " + std::to_string(i) + ": NULL input or output");
+    if (e->layers[i].kind != HA_ADAPTER && (!layer_in[i] || !layer_out[i]))
+      return fail(HA_ERR_ARG, "layer " + std::to_string(i) + ": NULL input or output");
   if (resume) {
     if (resume->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
     if (resume->owner != e || resume->owner_id != e->id) return fail(HA_ERR_HANDLE, "snapshot belongs to another engine");
@@ -377,7 +379,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       t.dst_first = s1 - (kKC - 1); t.dtype = a.dtype; t.in = a.in; t.tail = a.tail; t.tail_out = l.tail;
       he = ha::launch_tail_update(t, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " tail update: " + hipGetErrorString(he));
-    } else {
+    } else if (l.kind == HA_FULL_ATTENTION) {
       ha::GqaArgs a{};
       a.B = c.batch; a.HQ = c.HQ; a.HK = c.HK; a.HD = c.HD; a.RD = c.rot_dim; a.stride = c.full_stride; a.LT = c.max_ctx;
       a.P = P; a.L = L; a.dtype = c.full_dtype == HA_F16 ? 1 : 0;
@@ -385,7 +387,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.K = l.K; a.V = l.V;
       hipError_t he = ha::launch_gqa(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " attention launch: " + hipGetErrorString(he));
-    }
+    }  // HA_ADAPTER: no token mixer, nothing to run
   }
   if (opts && opts->layer_ms) HA_HIP(hipEventRecord(e->lev[c.n_layers], st));
   if (timing) HA_HIP(hipEventRecord(e->ev[1], st));
@@ -408,7 +410,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
             hipMemcpy2DAsync(p.tail, rowb * s->tail_rows, l.tail, rowb * kTailCap, rowb * s->tail_rows, B,
                              hipMemcpyDeviceToDevice, st) != hipSuccess)
           return bail(fail(HA_ERR_DEVICE, "snapshot copy failed"));
-      } else {
+      } else if (l.kind == HA_FULL_ATTENTION) {
         const size_t w = (size_t)end * c.HD * sizeof(_Float16), sp = (size_t)c.max_ctx * c.HD * sizeof(_Float16);
         const size_t vw = (size_t)end * sizeof(_Float16), vp = (size_t)c.max_ctx * sizeof(_Float16);
         if ((rc = dalloc(&p.K, w * B * c.HK)) || (rc = dalloc(&p.V, w * B * c.HK))) return bail(rc);
@@ -456,10 +458,10 @@ int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* ho
   const std::string w(what);
   const void* src = nullptr;
   size_t want = 0;
-  const bool lin = e->layers[layer].kind == HA_LINEAR_ATTENTION;
+  const bool lin = e->layers[layer].kind == HA_LINEAR_ATTENTION, full = e->layers[layer].kind == HA_FULL_ATTENTION;
   if (lin && w == "state") { src = s->layers[layer].S; want = sizeof(float) * B * c.H * c.DK * c.DV; }
   else if (lin && w == "tail") { src = s->layers[layer].tail; want = dtype_size(c.lin_dtype) * B * s->tail_rows * c.lin_stride; }
-  else if (!lin && (w == "K" || w == "V")) {
+  else if (full && (w == "K" || w == "V")) {
     src = w == "K" ? (const void*)s->layers[layer].K : (const void*)s->layers[layer].V;
     want = sizeof(_Float16) * B * c.HK * (size_t)s->P * c.HD;
   } else return fail(HA_ERR_PARAM, "no part '" + w + "' for this layer kind");

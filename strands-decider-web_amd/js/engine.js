@@ -21,7 +21,8 @@ const F32 = 0;
 const F16 = 1;
 const CHUNKED = 0;
 const SEQUENTIAL = 1;
-const LAYER_KIND = { linear_attention: 0, full_attention: 1 };
+// adapter: a projection stand-in with no token mixer (engine.js:256-261); its forward buffers may be null
+const LAYER_KIND = { linear_attention: 0, full_attention: 1, adapter: 2 };
 
 function pick(obj, key, def) {
   return obj !== undefined && obj !== null && obj[key] !== undefined && obj[key] !== null ? obj[key] : def;
@@ -120,6 +121,7 @@ class Snapshot {
 }
 
 function ptrOf(x) {
+  if (x === null || x === undefined) return BigInt(0);  // only an adapter layer may pass none
   if (typeof x === 'bigint') return x;
   if (x instanceof DeviceBuffer) {
     if (x.ptr === null) throw new Error('device buffer was freed');

@@ -21,7 +21,8 @@ out.cfg = m.configFromManifest({layer_types: ['linear_attention', 'linear_attent
   'full_attention'], linear_num_key_heads: 16, linear_key_head_dim: 128, linear_value_head_dim: 128,
   linear_conv_kernel_dim: 4, num_attention_heads: 8, num_key_value_heads: 2, head_dim: 256,
   partial_rotary_factor: 0.25, rope_theta: 10000000, rms_norm_eps: 1e-6}, {batch: 8});
-try { m.configFromManifest({layer_types: ['adapter']}); } catch (e) { out.bad_kind = e.message; }
+try { m.configFromManifest({layer_types: ['mamba']}); } catch (e) { out.bad_kind = e.message; }
+out.adapter = m.configFromManifest({layer_types: ['linear_attention', 'adapter', 'full_attention']}).layerKinds;
 try { m.Engine.createSync(out.cfg, {device: 0}); out.created = true; } catch (e) { out.err = [e.code, e.message]; }
 m.Engine.create(out.cfg).then(function () { out.async = 'resolved'; }, function (e) { out.async = e.code; })
   .then(function () { console.log(JSON.stringify(out)); });
@@ -44,7 +45,9 @@ def test_addon_loads_and_maps_manifest_config():
     # the engine's fused row strides (export_engine.py:52,61): 8256 = 64-padded q|k|v|z|a|b, 5120 = q|gate|k|v
     assert c["linStride"] == 8256 and c["fullStride"] == 5120 and c["rotDim"] == 64
     assert c["ropeTheta"] == 1e7 and abs(c["eps"] - 1e-6) < 1e-12
-    assert "unsupported layer type adapter" in out["bad_kind"]
+    assert "unsupported layer type mamba" in out["bad_kind"]
+    # adapter layers (engine.js:256-261) carry no token mixer: kind 2, skipped by the forward
+    assert out["adapter"] == [0, 2, 1]
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is visible: creation would succeed")
