@@ -55,8 +55,13 @@ typedef enum ha_layer_kind {
 typedef enum ha_dtype { HA_F32 = 0, HA_F16 = 1 } ha_dtype;
 
 typedef enum ha_recurrence {
-  HA_CHUNKED = 0,   /* prefill form: chunks of 64 rows at absolute positions, MFMA products (default) */
-  HA_SEQUENTIAL = 1 /* token-by-token fp32 rule with the state in registers (decode / resume) */
+  HA_CHUNKED = 0,       /* prefill form: chunks of 64 rows at absolute positions, MFMA products (default; the
+                           engine picks one of the two implementations below from its batch and head count: the
+                           split form for at most 32 sequence-heads, the fused kernel otherwise) */
+  HA_SEQUENTIAL = 1,    /* token-by-token fp32 rule with the state in registers (decode / resume) */
+  HA_CHUNKED_FUSED = 2, /* the chunked form in one kernel per layer: one workgroup per (sequence, head) */
+  HA_CHUNKED_SPLIT = 3  /* the chunked form in two kernels: every chunk's state-independent part at once, then the
+                           recurrence over the chunks */
 } ha_recurrence;
 
 /* Engine shape. Field names follow the manifest config keys (export_engine.py:83). */

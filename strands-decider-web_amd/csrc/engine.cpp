@@ -77,6 +77,8 @@ struct ha_engine {
   std::vector<Layer> layers;
   float* rope = nullptr;
   void* zero_tail = nullptr;  // [B][3][lin_stride] zeros: the history of an empty context
+  void* img = nullptr;        // [B][H][img_chunks] chunk images of the two-kernel chunked form
+  int img_chunks = 0;
   hipEvent_t ev[2] = {nullptr, nullptr};
   std::vector<hipEvent_t> lev;
   int C = 0;
@@ -169,6 +171,7 @@ void free_engine(ha_engine* e) {
   }
   if (e->rope) (void)hipFree(e->rope);
   if (e->zero_tail) (void)hipFree(e->zero_tail);
+  if (e->img) (void)hipFree(e->img);
   for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
   for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
   if (e->own) (void)hipStreamDestroy(e->own);
@@ -259,6 +262,9 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
     const size_t bytes = dtype_size(c.lin_dtype) * B * (kKC - 1) * c.lin_stride;
     if ((rc = dalloc(&e->zero_tail, bytes))) return bail(rc);
     if (hipMemset(e->zero_tail, 0, bytes) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
+    // chunk images: every chunk a call can touch (max_ctx / 64, plus the replayed open chunk)
+    e->img_chunks = (c.max_ctx + ha::kChunk - 1) / ha::kChunk + 1;
+    if ((rc = dalloc(&e->img, ha::gdn_split_image_bytes() * B * c.H * e->img_chunks))) return bail(rc);
   }
   if (e->any_full) {
     // RoPE table as engine.js:105-106 builds it: angle t / theta^(2i/RD) in f64, stored as f32 (cos, sin)
@@ -338,7 +344,8 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   if ((long)P + L > c.max_ctx)
     return fail(HA_ERR_CONTEXT, "context " + std::to_string((long)P + L) + " exceeds " + std::to_string(c.max_ctx));
   const int mode = opts ? opts->recurrence : HA_CHUNKED;
-  if (mode != HA_CHUNKED && mode != HA_SEQUENTIAL) return fail(HA_ERR_ARG, "unknown recurrence mode");
+  if (mode < HA_CHUNKED || mode > HA_CHUNKED_SPLIT) return fail(HA_ERR_ARG, "unknown recurrence mode");
+  const bool chunked = mode != HA_SEQUENTIAL;
   const bool timing = opts && (opts->timestamps || opts->layer_ms);
   HA_HIP(hipSetDevice(e->device));
   hipStream_t st = e->stream;
@@ -356,7 +363,12 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       }
 
   const int end = P + L;
-  const int s1 = mode == HA_CHUNKED ? s0 + ha::kChunk * ((end - s0) / ha::kChunk) : end;  // new state position
+  const int s1 = chunked ? s0 + ha::kChunk * ((end - s0) / ha::kChunk) : end;  // new state position
+  // HA_CHUNKED picks the implementation from the engine's shape alone: the two-kernel form when there are few
+  // (sequence, head) recurrences for the 256 CUs (measured crossover at T = 2048: B*H between 32 and 48), the fused
+  // kernel otherwise. The two round differently, so the choice must not depend on the call (a resumed suffix must
+  // match the same rows of one longer forward bit for bit).
+  const bool split = mode == HA_CHUNKED_SPLIT || (mode == HA_CHUNKED && c.batch * c.H <= 32);
   if (timing) HA_HIP(hipEventRecord(e->ev[0], st));
   for (int i = 0; i < c.n_layers; i++) {
     Layer& l = e->layers[i];
@@ -371,7 +383,10 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.in = layer_in[i]; a.out = layer_out[i];
       a.S_in = resume ? resume->layers[i].S : nullptr; a.S_out = l.S;
       a.conv_w = l.conv; a.negA = l.negA; a.dtb = l.dtb; a.gnorm = c.lin_gnorm ? l.gnorm : nullptr;
-      hipError_t he = mode == HA_CHUNKED ? ha::launch_gdn_chunked(a, st) : ha::launch_gdn_sequential(a, st);
+      a.img = e->img; a.img_chunks = e->img_chunks;
+      hipError_t he = !chunked ? ha::launch_gdn_sequential(a, st)
+                      : split ? ha::launch_gdn_split(a, st)
+                              : ha::launch_gdn_chunked(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " gated-delta launch: " + hipGetErrorString(he));
       ha::TailArgs t{};
       t.B = c.batch; t.stride = c.lin_stride; t.C = e->C; t.ab_off = e->C + c.H * c.DV; t.ab_n = 2 * c.H;

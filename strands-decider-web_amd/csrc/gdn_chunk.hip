@@ -33,20 +33,13 @@
 // as long as A and B use the same one. The result D holds rows 4 (l >> 4) + e, e < 4, of column l & 15. That
 // lets a D tile be reused as a B operand (K = its rows) without moving data between lanes: the matching A
 // operand is read with the same "permuted" K order {32 kb + 4 grp + e} U {32 kb + 16 + 4 grp + e}.
-#include "ha_kernels.h"
+#include "gdn_common.h"
 
 namespace ha {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-constexpr int kDK = 128, kDV = 128, kCH = 64, kKC = 4, kNW = 8, kNT = 64 * kNW;
+constexpr int kNW = 8, kNT = 64 * kNW;
 constexpr int kNC = 4;        // consumer waves (0..3), 32 value columns each; producers are waves 4..7
-constexpr int kQP = kDK + 8;  // row pitch (halves) of [64][128] f16 tiles
-constexpr int kTP = kCH + 8;  // row pitch (halves) of [*][64] f16 tiles
-constexpr int kAP = kCH + 4;  // row pitch (floats) of the fp32 A / T tile
 constexpr int kGW = kNW - 1;  // the producer that computes the gate vectors and the diagonal blocks of T
 constexpr int kSP = 36;       // row pitch (floats) of a consumer's output staging area (16 rows x 32 columns)
 constexpr int kRG = 8;        // rows per conv lane
@@ -75,177 +68,6 @@ struct Lds {
   float inv[kNC][kCH];      // per-consumer copy of the row inverse norms
 };
 static_assert(sizeof(float) * kCH * kAP >= kNC * 16 * kSP * sizeof(float), "staging area");
-
-// Transposed tiles are written 8 rows of one column (16 bytes) per lane; the 8-column group index is XORed with a
-// function of the row so those writes spread over the banks. Element (row, col) lives at
-// row * kTP + 8 * (col / 8 ^ f(row)) + col % 8; every 16-byte read stays contiguous.
-__device__ __forceinline__ int kt16(int i, int g8) { return i * kTP + 8 * (g8 ^ ((i >> 3) & 7)); }
-__device__ __forceinline__ int vt16(int j, int g8) { return j * kTP + 8 * (g8 ^ ((j >> 4) & 7)); }
-
-// SiLU / sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE division sequence
-__device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
-
-#define DPP_F(v, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xf, 0xf, false))
-
-// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15) with row rotations; every lane gets the sum.
-__device__ __forceinline__ float row_sum16(float v) {
-  v += DPP_F(v, 0x128);
-  v += DPP_F(v, 0x124);
-  v += DPP_F(v, 0x122);
-  v += DPP_F(v, 0x121);
-  return v;
-}
-
-// Sum over aligned groups of 8 lanes: quad permutations, then the half-row mirror (lane i <-> 7 - i).
-__device__ __forceinline__ float sum8(float v) {
-  v += DPP_F(v, 0xB1);
-  v += DPP_F(v, 0x4E);
-  v += DPP_F(v, 0x141);
-  return v;
-}
-
-// Orders a wave's LDS writes before its later reads of other lanes' entries (no workgroup barrier).
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// An identity the compiler cannot see through: per-lane indices re-derived from it every period keep the address
-// arithmetic built on them inside the loop instead of being hoisted out of it and spilled.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
-// Global (address space 1) pointers: loads through them are global_load_*, not flat_load_*, so they are not
-// counted by the LDS wait counter and outstanding global loads do not stall LDS traffic.
-template <typename T>
-using gptr = const __attribute__((address_space(1))) T*;
-template <typename T>
-__device__ __forceinline__ gptr<T> gp(const void* p) { return (gptr<T>)(p); }
-template <typename T>
-__device__ __forceinline__ __attribute__((address_space(1))) T* gpw(void* p) { return (__attribute__((address_space(1))) T*)(p); }
-
-template <typename T>
-__device__ __forceinline__ gptr<T> row_of(const GdnArgs& a, int b, int r) {
-  if (r < a.P) return gp<T>(a.tail) + ((size_t)b * a.tail_cap + (r - (a.s0 - (kKC - 1)))) * a.stride;
-  return gp<T>(a.in) + ((size_t)b * a.L + (r - a.P)) * a.stride;
-}
-
-__device__ __forceinline__ void load8(gptr<float> p, float* o) {
-  const f4 x = *(gptr<f4>)(p), y = *(gptr<f4>)(p + 4);
-  o[0] = x[0]; o[1] = x[1]; o[2] = x[2]; o[3] = x[3]; o[4] = y[0]; o[5] = y[1]; o[6] = y[2]; o[7] = y[3];
-}
-__device__ __forceinline__ void load8(gptr<_Float16> p, float* o) {
-  const h8 x = *(gptr<h8>)(p);
-#pragma unroll
-  for (int i = 0; i < 8; i++) o[i] = (float)x[i];
-}
-__device__ __forceinline__ void load4(gptr<float> p, float* o) {
-  const f4 x = *(gptr<f4>)(p);
-  o[0] = x[0]; o[1] = x[1]; o[2] = x[2]; o[3] = x[3];
-}
-__device__ __forceinline__ void load4(gptr<_Float16> p, float* o) {
-  const h4 x = *(gptr<h4>)(p);
-  o[0] = (float)x[0]; o[1] = (float)x[1]; o[2] = (float)x[2]; o[3] = (float)x[3];
-}
-__device__ __forceinline__ f4 ld4(gptr<float> p) { return *(gptr<f4>)(p); }
-__device__ __forceinline__ f4 ld4(gptr<_Float16> p) {
-  const h4 x = *(gptr<h4>)(p);
-  return f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
-}
-__device__ __forceinline__ void store4(__attribute__((address_space(1))) float* p, const f4& v) {
-  *(__attribute__((address_space(1))) f4*)(p) = v;
-}
-__device__ __forceinline__ void store4(__attribute__((address_space(1))) _Float16* p, const f4& v) {
-  *(__attribute__((address_space(1))) h4*)(p) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-}
-
-// A operand read in the permuted K order matching a D tile pair used as B: row r of a [*][pitch] f16 tile,
-// K block kb (32 wide), lane group grp.
-__device__ __forceinline__ h8 perm_a(const _Float16* base, int pitch, int r, int kb, int grp) {
-  const _Float16* p = base + r * pitch + 32 * kb + 4 * grp;
-  const h4 lo = *reinterpret_cast<const h4*>(p), hi = *reinterpret_cast<const h4*>(p + 16);
-  return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-// perm_a for the swizzled k^T tile
-__device__ __forceinline__ h8 perm_a_kt(const _Float16* kt, int r, int kb, int grp) {
-  const int sub = 4 * (grp & 1);
-  const h4 lo = *reinterpret_cast<const h4*>(kt + kt16(r, 4 * kb + (grp >> 1)) + sub);
-  const h4 hi = *reinterpret_cast<const h4*>(kt + kt16(r, 4 * kb + 2 + (grp >> 1)) + sub);
-  return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-// Two D tiles (rows 32kb..32kb+15 and 32kb+16..+31 of a column) as one f16 B operand.
-__device__ __forceinline__ h8 pack_b(const f4& x, const f4& y) {
-  return h8{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3],
-            (_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
-}
-
-__device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
-
-template <int N>
-struct Width {
-  static constexpr int value = N;
-};
-
-// Block column J of T below the diagonal: T_iJ = -T_ii sum_{k=J}^{i-1} A_ik T_kJ for block rows i = J+1..3, in
-// order. The column's blocks stay in registers (D layout: rows 4 grp + e, column c16), so A is never overwritten
-// and the three column waves need no barrier between block rows; only the f16 copies T diag(beta) and
-// T diag(beta e^gc) are stored. The D layout is used directly as the B operand of v_mfma_f32_16x16x4f32 by giving
-// step e the K index 4 grp + e, and the A operand is read in the same order.
-template <int J>
-__device__ __forceinline__ void t_column(Lds& sm, int grp, int c16) {
-  const int cj = 16 * J + c16;
-  const float fb = sm.bt[cj], fw = fb * sm.eg[cj];
-  f4 Tc[4];
-#pragma unroll
-  for (int e = 0; e < 4; e++) Tc[J][e] = sm.Tm[(16 * J + 4 * grp + e) * kAP + cj];
-  // X[bi] accumulates sum_k A_bi,k T_kJ. The terms with k = J only need the diagonal block, so they are all issued
-  // first; after that each block row adds just the term of the block found last, so the dependent chain per block
-  // row is one product plus the multiplication by T_ii.
-  f4 X[4];
-#pragma unroll
-  for (int bi = J + 1; bi < 4; bi++) {
-    const f4 av = lds4(&sm.Tm[(16 * bi + c16) * kAP + 16 * J + 4 * grp]);
-    X[bi] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int e = 0; e < 4; e++) X[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[J][e], X[bi], 0, 0, 0);
-  }
-#pragma unroll
-  for (int bi = J + 1; bi < 4; bi++) {
-    const float* arow = &sm.Tm[(16 * bi + c16) * kAP];
-    if (bi > J + 1) {
-      const f4 av = lds4(arow + 16 * (bi - 1) + 4 * grp);
-#pragma unroll
-      for (int e = 0; e < 4; e++) X[bi] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[bi - 1][e], X[bi], 0, 0, 0);
-    }
-    const f4 tv = lds4(arow + 16 * bi + 4 * grp);
-    f4 Y = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int e = 0; e < 4; e++) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(tv[e], X[bi][e], Y, 0, 0, 0);
-    Tc[bi] = -Y;
-    // the middle terms A_b,bi T_bi,J of the rows below, now that T_bi,J is known
-#pragma unroll
-    for (int b2 = bi + 2; b2 < 4; b2++) {
-      const f4 av = lds4(&sm.Tm[(16 * b2 + c16) * kAP + 16 * bi + 4 * grp]);
-#pragma unroll
-      for (int e = 0; e < 4; e++) X[b2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], Tc[bi][e], X[b2], 0, 0, 0);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int t = 16 * bi + 4 * grp + e;
-      sm.Tb[t * kTP + cj] = (_Float16)(Tc[bi][e] * fb);
-      sm.Tw[t * kTP + cj] = (_Float16)(Tc[bi][e] * fw);
-    }
-  }
-}
 
 template <typename T>
 __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
@@ -290,8 +112,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
   float xq[kRG + kKC - 1][8], xv[kRG + kKC - 1][4], ga = 0.0f, gb = 0.0f;
 
   // Loads rows cs-3 .. cs+63 of the chunk starting at cs: lane rows 8 rg - 3 .. 8 rg + 7 of the chunk, at column
-  // offset `col` (element) of the row, `n` channels. Rows past the end read as 0. Uniform row bases and 32-bit lane
-  // offsets when no row is a replay row or past the end; the general path otherwise.
+  // offset `col` (element) of the row, `n` channels. Uniform row bases and 32-bit lane offsets when no row is a
+  // replay row or past the end; per-lane row pointers otherwise. Rows past the end repeat the last row: they only
+  // feed conv outputs past the end, which are masked.
+  const RowSrc src = row_src(a);
   auto fetch_rows = [&](int cs, int rg, int col, auto& x, auto nch) {
     constexpr int N = decltype(nch)::value;
     if (cs - (kKC - 1) >= a.P && cs + kCH <= end) {
@@ -309,15 +133,11 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
 #pragma unroll
       for (int i = 0; i < kRG + kKC - 1; i++) {
         const int r = cs + kRG * rg - (kKC - 1) + i, rc = min(r, end - 1);
-        const gptr<T> row = row_of<T>(a, b, rc) + col;
+        const gptr<T> row = row_of<T>(a, src, b, rc) + col;
         if constexpr (N == 8)
           load8(row, x[i]);
         else
           load4(row, x[i]);
-        if (r >= end) {
-#pragma unroll
-          for (int c = 0; c < N; c++) x[i][c] = 0.0f;
-        }
       }
     }
   };
@@ -327,16 +147,11 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
     fetch_rows(cs, rg, (qk ? a.H * kDK : 0) + h * kDK + 8 * cg, xq, Width<8>{});
     if (w == kGW) {
       const int lane = pt & 63;
-      if (cs >= a.P && cs + kCH <= end) {
-        const char* g0 = seq_in + (size_t)(cs - a.P) * rowb;
-        const unsigned og = (unsigned)lane * rowb;
-        ga = (float)*gp<T>(g0 + og + (unsigned)aoff * sizeof(T));
-        gb = (float)*gp<T>(g0 + og + (unsigned)boff * sizeof(T));
-      } else {
-        const gptr<T> grow = row_of<T>(a, b, min(cs + lane, end - 1));
-        ga = cs + lane < end ? (float)grow[aoff] : 0.0f;
-        gb = cs + lane < end ? (float)grow[boff] : 0.0f;
-      }
+      // rows past the end: their gates are never used (the gate lanes mask them)
+      const gptr<T> grow = cs >= a.P && cs + kCH <= end ? gp<T>(seq_in + (size_t)(cs - a.P + lane) * rowb)
+                                                         : row_of<T>(a, src, b, min(cs + lane, end - 1));
+      ga = (float)grow[aoff];
+      gb = (float)grow[boff];
     }
   };
   // consumer lane ct = tid: rows 8 (ct / 32) .., v channels 4 (ct % 32)
@@ -519,6 +334,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
     // consumer epilogue layout: lane l holds rows 8 q + l / 8 (q < 8) of columns 32 w + 4 (l % 8) .. +3
     f4 gw = {1.0f, 1.0f, 1.0f, 1.0f};
     if (a.gnorm) gw = ld4(gp<float>(a.gnorm) + 32 * w + 4 * (tid0 & 7));
+    // Drain these loads here: the compiler's wait counting merges the loop's entry state into every period, so a
+    // state load still outstanding at the loop head would make each period's first use of S wait for every
+    // global access issued before it (the previous chunk's output stores included).
+    __builtin_amdgcn_s_waitcnt(0);
     f4 Y[8], zq[8];
     // period p: chunk p (p >= 0) here, chunk p + 1 (p + 1 < nchunks) on the producers
     for (int p = -1; p < nchunks; p++) {
@@ -558,7 +377,8 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
               KSb[ct][1] = pack_b(KS[ct][2], KS[ct][3]);
             }
           }
-          // z of this chunk for the epilogue, in flight behind the rest of the chunk's MFMA work
+          // z of this chunk for the epilogue, in flight behind the rest of the chunk's MFMA work (one load site:
+          // rows outside [P, P + L) are clamped, their outputs are not stored)
           if (plain) {
             const char* zb = seq_in + (size_t)(c0 - a.P) * rowb + (a.C + h * kDV) * sizeof(T);
             const unsigned oz = (unsigned)er * rowb + ec * (unsigned)sizeof(T);
@@ -730,6 +550,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
         for (int e = 0; e < 4; e++)
           gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16] = S[ct][it][e];
   } else {
+    const int last_cs = a.s0 + kCH * (nchunks - 1);
     fetch_qk(a.s0);
     if (w == kGW) produce_gates(a.s0);
     for (int p = -1; p < nchunks; p++) {
@@ -739,11 +560,12 @@ __global__ __launch_bounds__(512) void gdn_chunk_kernel(GdnArgs a) {
       // ---- A: conv of chunk p+1 in registers; raw q/k rows (and a/b) of chunk p+2 ----
       // Wave priorities: each segment's longest wave (the gate producer in B and C, the block-column-0 wave in E) is
       // raised so the SIMD it shares with a consumer issues for it first; in A all run at the base priority.
+      // Both run every period, past the last chunk on clamped rows whose results are never used: conditional
+      // loads would make the loop-carried rows a merge of old and new values, which the compiler resolves with
+      // copies that wait for the loads right after they are issued.
       __builtin_amdgcn_s_setprio(0);
-      if (p + 1 < nchunks) {
-        produce_conv(c1);
-        if (p + 2 < nchunks) fetch_qk(c1 + kCH);
-      }
+      produce_conv(c1);
+      fetch_qk(min(c1 + kCH, last_cs));
       __syncthreads();  // B
 
       // ---- B: q^, k^, k^T and the gate vectors of chunk p+1 to LDS ----

@@ -24,6 +24,8 @@ struct GdnArgs {
   const float* negA;                // [H]
   const float* dtb;                 // [H]
   const float* gnorm;               // [DV], or nullptr to output the raw core output
+  void* img;                        // chunk-image scratch of the two-kernel form: [B][H][img_chunks] images
+  int img_chunks;                   // image slots per (sequence, head)
 };
 
 // Full-attention prep (q/k RMSNorm, partial RoPE, K/V cache write) and attention for rows [P, P + L).
@@ -52,6 +54,8 @@ struct TailArgs {
 
 hipError_t launch_gdn_sequential(const GdnArgs& a, hipStream_t s);
 hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t s);
+hipError_t launch_gdn_split(const GdnArgs& a, hipStream_t s);  // chunk-parallel preparation + recurrence
+size_t gdn_split_image_bytes();                                // bytes of one chunk image
 hipError_t launch_gqa(const GqaArgs& a, hipStream_t s);
 hipError_t launch_tail_update(const TailArgs& a, hipStream_t s);
 

@@ -1,5 +1,7 @@
-"""GPU parity of the chunked (MFMA) gated-delta prefill kernel against the fp64 sequential oracle and against the
-GPU's own fp32 sequential kernel, plus bit-exact prefix + suffix for aligned and unaligned splits."""
+"""GPU parity of the chunked (MFMA) gated-delta prefill against the fp64 sequential oracle and against the GPU's own
+fp32 sequential kernel, plus bit-exact prefix + suffix for aligned and unaligned splits. Every test runs both
+implementations of the chunked form: the single fused kernel and the two-kernel split (chunk images, then the
+recurrence)."""
 import numpy as np
 import pytest
 
@@ -11,18 +13,23 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3  # north-star bar for the recurrence (max |err| / max |ref|)
 
 
+@pytest.fixture(params=[ha.CHUNKED_FUSED, ha.CHUNKED_SPLIT], ids=["fused", "split"])
+def mode(request):
+    return request.param
+
+
 def _state(snap, B=1):
     s = np.zeros((B, 16, 128, 128), np.float32)
     return snap.read(0, "state", s)
 
 
 @pytest.mark.parametrize("gnorm", [False, True])
-def test_config0_chunked(gnorm):
+def test_config0_chunked(gnorm, mode):
     x = gdn_inputs(64)
     p = synth.gdn_params()
     r = Runner(["linear_attention"], gnorm=gnorm)
     r.set_params(0, p)
-    (out,), snap = r.forward([x], keep=True)
+    (out,), snap = r.forward([x], keep=True, recurrence=mode)
     ref, st = oracle_gdn(x, p, gnorm=gnorm)
     e, es = rel_err(out, ref), rel_err(_state(snap)[0], st[0].S)
     print("config0 chunked gnorm=%s rel_err out %.2e state %.2e" % (gnorm, e, es))
@@ -30,13 +37,13 @@ def test_config0_chunked(gnorm):
     assert snap.state_pos == 64 and snap.tail_rows == 3
 
 
-def test_config2_T2048_against_oracle_and_sequential():
+def test_config2_T2048_against_oracle_and_sequential(mode):
     # config-0 distributions at T=2048; chunked result vs the sequential fp32 recurrence
     x = gdn_inputs(2048, seed=7)
     p = synth.gdn_params(seed=7)
     r = Runner(["linear_attention"], gnorm=False)
     r.set_params(0, p)
-    (chunk,), csnap = r.forward([x], keep=True)
+    (chunk,), csnap = r.forward([x], keep=True, recurrence=mode)
     (seq,), ssnap = r.forward([x], keep=True, recurrence=ha.SEQUENTIAL)
     ref, st = oracle_gdn(x, p, gnorm=False)
     e_o, e_s = rel_err(chunk, ref), rel_err(_state(csnap)[0], st[0].S)
@@ -47,13 +54,13 @@ def test_config2_T2048_against_oracle_and_sequential():
     assert rel_err(_state(csnap)[0], _state(ssnap)[0]) < TOL
 
 
-def test_slow_decay_state_carry():
+def test_slow_decay_state_carry(mode):
     # alpha close to 1 keeps the state alive across many chunks, so inter-chunk error would compound
     x = gdn_inputs(1024, 2, seed=8)
     p = synth.gdn_params(seed=8, neg_exp_A=-0.02, dt_bias=-2.0)
     r = Runner(["linear_attention"], batch=2, gnorm=True)
     r.set_params(0, p)
-    (out,), snap = r.forward([x], keep=True)
+    (out,), snap = r.forward([x], keep=True, recurrence=mode)
     ref, st = oracle_gdn(x, p, gnorm=True)
     e, es = rel_err(out, ref), max(rel_err(_state(snap, 2)[b], st[b].S) for b in range(2))
     print("slow decay rel_err out %.2e state %.2e" % (e, es))
@@ -61,13 +68,13 @@ def test_slow_decay_state_carry():
 
 
 @pytest.mark.parametrize("T", [1, 3, 63, 65, 130, 200])
-def test_unaligned_lengths_f16(T):
+def test_unaligned_lengths_f16(T, mode):
     B = 2
     x = gdn_inputs(T, B, seed=9, dtype=np.float16)
     p = synth.gdn_params(seed=9, neg_exp_A=-0.5, dt_bias=0.3)
     r = Runner(["linear_attention"], batch=B, lin_dtype=ha.F16)
     r.set_params(0, p)
-    (out,), snap = r.forward([x], keep=True)
+    (out,), snap = r.forward([x], keep=True, recurrence=mode)
     ref, _ = oracle_gdn(x.astype(np.float32), p)
     e = rel_err(out, ref)
     print("T=%d f16 rows rel_err %.2e" % (T, e))
@@ -76,30 +83,30 @@ def test_unaligned_lengths_f16(T):
 
 
 @pytest.mark.parametrize("P,L", [(1536, 64), (100, 30), (64, 1), (5, 200), (63, 2), (130, 126)])
-def test_prefix_suffix_bit_exact(P, L):
+def test_prefix_suffix_bit_exact(P, L, mode):
     x = gdn_inputs(P + L, 2, seed=10)
     p = synth.gdn_params(seed=10, neg_exp_A=-0.2)
     r = Runner(["linear_attention"], batch=2)
     r.set_params(0, p)
-    (full,), fsnap = r.forward([x], keep=True)
-    (pre,), snap = r.forward([x[:, :P]], keep=True)
-    (suf,), ssnap = r.forward([x[:, P:]], cache=snap, keep=True)
+    (full,), fsnap = r.forward([x], keep=True, recurrence=mode)
+    (pre,), snap = r.forward([x[:, :P]], keep=True, recurrence=mode)
+    (suf,), ssnap = r.forward([x[:, P:]], cache=snap, keep=True, recurrence=mode)
     np.testing.assert_array_equal(pre, full[:, :P])
     np.testing.assert_array_equal(suf, full[:, P:])
     assert ssnap.state_pos == fsnap.state_pos
     np.testing.assert_array_equal(_state(ssnap, 2), _state(fsnap, 2))
 
 
-def test_three_way_split_and_decode_steps():
+def test_three_way_split_and_decode_steps(mode):
     # prefix, then several short calls (decode-like) must match one forward bit for bit
     x = gdn_inputs(90, 1, seed=11)
     p = synth.gdn_params(seed=11)
     r = Runner(["linear_attention"])
     r.set_params(0, p)
-    (full,), _ = r.forward([x])
-    (o1,), s = r.forward([x[:, :61]], keep=True)
+    (full,), _ = r.forward([x], recurrence=mode)
+    (o1,), s = r.forward([x[:, :61]], keep=True, recurrence=mode)
     outs = [o1]
     for a, bnd in [(61, 62), (62, 66), (66, 67), (67, 90)]:
-        (o,), s = r.forward([x[:, a:bnd]], cache=s, keep=True)
+        (o,), s = r.forward([x[:, a:bnd]], cache=s, keep=True, recurrence=mode)
         outs.append(o)
     np.testing.assert_array_equal(np.concatenate(outs, 1), full)
