@@ -21,6 +21,8 @@
 //   one tile ahead, so no registers hold the prefetch. Online softmax in fp32 with a per-row reference max that is raised only when
 //   a score exceeds it by 2^8, so the 128 O accumulators are rarely rescaled; the decision is per row, which keeps
 //   every row's arithmetic independent of the other rows in its block (prefix + suffix stays bit-identical).
+#include <algorithm>
+
 #include "ha_kernels.h"
 
 namespace ha {
@@ -109,49 +111,73 @@ __device__ __forceinline__ void load8f<_Float16>(gptr<_Float16> p, float* o) {
   for (int i = 0; i < 8; i++) o[i] = (float)x[i];
 }
 
-// K rows and V^T columns for rows [t0, t0 + 64) of one (sequence, KV head).
+// K rows and V^T columns for rows [t0, t0 + 64) of one (sequence, KV head). Wave w takes rows 16 w .. 16 w + 15,
+// lane l dims 4 l .. 4 l + 3: every row's k and v loads are issued before any is used. k: RMSNorm (wave-wide sum
+// of squares), gain, rotate-half RoPE on dims [0, 64) (dim i < 32 pairs with i + 32, held by lane l ^ 8), f16.
+// v: f16 into LDS, then each thread writes one dim's 64 positions of V^T, 16 bytes at a time when aligned.
 template <typename T>
 __global__ __launch_bounds__(256) void gqa_kv_kernel(GqaArgs a) {
   __shared__ _Float16 vs[64][kHD + 8];
   const int t0 = blockIdx.x * 64, kh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int RD = a.RD;
   const size_t kvb = ((size_t)b * a.HK + kh) * a.LT * kHD;
-  // K: wave handles rows wave, wave + 4, ...; lane holds dims lane + 64 i
-  for (int rr = wave; rr < 64; rr += 4) {
-    const int t = t0 + rr;
-    if (t >= a.L) break;
-    const int pos = a.P + t;
-    gptr<T> row = gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride;
-    gptr<T> src = row + (size_t)a.HQ * 2 * kHD + (size_t)kh * kHD;
-    float v[4], ss = 0.0f;
+  const f4 kw = *(gptr<f4>)(gp<float>(a.kw) + 4 * lane);
+  f4 x[16], vv[16];
 #pragma unroll
-    for (int i = 0; i < 4; i++) { v[i] = (float)src[lane + 64 * i]; ss += v[i] * v[i]; }
+  for (int r = 0; r < 16; r++) {
+    const int t = min(t0 + 16 * wave + r, a.L - 1);
+    gptr<T> row = gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)a.HQ * 2 * kHD;
+    x[r] = ld4(row + (size_t)kh * kHD + 4 * lane);
+    vv[r] = ld4(row + (size_t)a.HK * kHD + (size_t)kh * kHD + 4 * lane);
+  }
+  const bool rot = lane < 16;  // dims 0 .. 63 (RD = 64)
+  const int ri = 4 * (lane & 7);
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int t = t0 + 16 * wave + r, pos = a.P + min(t, a.L - 1);
+    float ss = (x[r][0] * x[r][0] + x[r][1] * x[r][1]) + (x[r][2] * x[r][2] + x[r][3] * x[r][3]);
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m);
     const float inv = rsqrtf(ss / kHD + 1e-6f);
+    f4 k = x[r] * inv * kw;
+    f4 pk;
 #pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = v[i] * inv * gp<float>(a.kw)[lane + 64 * i];
-    const float partner = __shfl_xor(v[0], RD / 2);
-    if (lane < RD) {
-      const int i = lane % (RD / 2);
-      const float cs = gp<float>(a.rope)[(size_t)pos * RD + 2 * i], sn = gp<float>(a.rope)[(size_t)pos * RD + 2 * i + 1];
-      v[0] = lane < RD / 2 ? v[0] * cs - partner * sn : v[0] * cs + partner * sn;
+    for (int c = 0; c < 4; c++) pk[c] = __shfl_xor(k[c], 8);
+    if (rot) {
+      const f4 cs0 = *(gptr<f4>)(gp<float>(a.rope) + (size_t)pos * a.RD + 2 * ri);
+      const f4 cs1 = *(gptr<f4>)(gp<float>(a.rope) + (size_t)pos * a.RD + 2 * ri + 4);
+      const float cs[4] = {cs0[0], cs0[2], cs1[0], cs1[2]}, sn[4] = {cs0[1], cs0[3], cs1[1], cs1[3]};
+#pragma unroll
+      for (int c = 0; c < 4; c++) k[c] = lane < 8 ? k[c] * cs[c] - pk[c] * sn[c] : k[c] * cs[c] + pk[c] * sn[c];
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) gpw<_Float16>(a.K)[kvb + (size_t)pos * kHD + lane + 64 * i] = (_Float16)v[i];
-    // raw v row into LDS for the transpose
-    gptr<T> vsrc = row + (size_t)a.HQ * 2 * kHD + (size_t)a.HK * kHD + (size_t)kh * kHD;
-#pragma unroll
-    for (int i = 0; i < 4; i++) vs[rr][lane + 64 * i] = (_Float16)(float)vsrc[lane + 64 * i];
+    if (t < a.L)
+      *(__attribute__((address_space(1))) h4*)(gpw<_Float16>(a.K) + kvb + (size_t)pos * kHD + 4 * lane) =
+          h4{(_Float16)k[0], (_Float16)k[1], (_Float16)k[2], (_Float16)k[3]};
+    *reinterpret_cast<h4*>(&vs[16 * wave + r][4 * lane]) =
+        h4{(_Float16)vv[r][0], (_Float16)vv[r][1], (_Float16)vv[r][2], (_Float16)vv[r][3]};
   }
   __syncthreads();
-  // V^T: thread d writes the positions of this block for dim d
   const int d = tid;
   const int n = min(64, a.L - t0);
   __attribute__((address_space(1))) _Float16* vt = gpw<_Float16>(a.V) + kvb + (size_t)d * a.LT + a.P + t0;
-  for (int r = 0; r < n; r++) vt[r] = vs[r][d];
+  if (n == 64 && ((a.P + t0) & 7) == 0) {
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      h8 v8;
+#pragma unroll
+      for (int e = 0; e < 8; e++) v8[e] = vs[8 * g + e][d];
+      *(__attribute__((address_space(1))) h8*)(vt + 8 * g) = v8;
+    }
+  } else {
+    for (int r = 0; r < n; r++) vt[r] = vs[r][d];
+  }
 }
+
+// 64-key tiles that query block qb (rows P + 64 qb .. +63 of the call) reads under the causal mask
+__device__ __forceinline__ int gqa_ntiles(const GqaArgs& a, int qb) {
+  return min(a.P + qb * 64 + 63, a.P + a.L - 1) / kBK + 1;
+}
+inline int host_ntiles(const GqaArgs& a, int qb) { return std::min(a.P + qb * 64 + 63, a.P + a.L - 1) / kBK + 1; }
 
 // Workgroup = 8 waves: wave w serves query head kh*4 + (w & 3) on rows q0 + 32 (w >> 2) .. +31 (a block of 64
 // query rows for all 4 heads of the KV group), so each staged 64-key K/V tile feeds 8 waves, and two waves share
@@ -169,12 +195,29 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   constexpr int kTileHalves = kBK * kHD;
   _Float16* lds = reinterpret_cast<_Float16*>(lds_raw);
 
-  // heavy-first order over all workgroups; the 16 (sequence, KV head) pairs cycle fastest, so every workgroup of a
+  // heavy-first order over all workgroups; the (sequence, KV head) pairs cycle fastest, so every workgroup of a
   // pair lands on the same XCD (round-robin dispatch over 8 XCDs) and its K/V stays in that XCD's L2
   const int npair = a.B * a.HK;
   const int nqb = (a.L + kRows - 1) / kRows;
   const int id = blockIdx.x;
-  const int pair = id % npair, qb = nqb - 1 - id / npair;
+  const int pair = id % npair;
+  // this workgroup's query block qb and key tiles [kt0, kt1): the whole block, or with split key ranges piece
+  // `piece` of the block's npieces (absolute tile boundaries, a multiple of a.split)
+  int qb = nqb - 1 - id / npair, npieces = 1, piece = 0;
+  if (a.split > 0) {
+    qb = nqb - 1;
+    int item = id / npair;
+    while (qb > 0) {
+      const int np = (gqa_ntiles(a, qb) + a.split - 1) / a.split;
+      if (item < np) break;
+      item -= np;
+      qb--;
+    }
+    npieces = (gqa_ntiles(a, qb) + a.split - 1) / a.split;
+    piece = min(item, npieces - 1);
+  }
+  const int kt0 = piece * (a.split > 0 ? a.split : 0);
+  const int kt1 = a.split > 0 ? min(kt0 + a.split, gqa_ntiles(a, qb)) : gqa_ntiles(a, qb);
   const int b = pair / a.HK, kh = pair % a.HK;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int h = kh * 4 + (wave & 3);
@@ -182,9 +225,6 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   const int q0 = qb * kRows + 32 * (wave >> 2);
   const int RD = a.RD;
 
-  const int nvalid = a.P + a.L;
-  const int last_key = min(a.P + qb * kRows + kRows - 1, nvalid - 1);
-  const int ntiles = last_key / kBK + 1;
   const size_t kvb = ((size_t)b * a.HK + kh) * a.LT * kHD;
   gptr<_Float16> Kg = gp<_Float16>(a.K) + kvb;
   gptr<_Float16> Vg = gp<_Float16>(a.V) + kvb;
@@ -212,7 +252,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
                                        (__attribute__((address_space(3))) void*)(vb + (size_t)ins * 512), 16, 0, 0);
     }
   };
-  issue(0, lane);
+  issue(kt0, lane);
 
   // Q as the B operand of S^T = K Q^T (32x32x16): qreg[ks] = q[q0 + c32][16 ks + 8 half .. +7], prepared here:
   // RMSNorm (the two halves of a row sit in lanes l and l + 32), RoPE (dim i < 32 in ks 0/1 pairs with i + 32 in
@@ -373,13 +413,16 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
     mx = max_halves(mx) * log2e;
     // raise the reference max only when a score would exceed it by 2^kRescale (decided per row)
     const float mnew = mx > mref + kRescale ? mx : mref;
-    const float alpha = __builtin_amdgcn_exp2f(mref - mnew);  // exactly 1 when unchanged, 0 on a row's first keys
+    // 1 when unchanged (also while a row has seen no key: a piece of a split key range can start with tiles that
+    // lie wholly after some of its rows), 0 on a row's first keys
+    const float alpha = mnew == mref ? 1.0f : __builtin_amdgcn_exp2f(mref - mnew);
     const bool need = mnew != mref && mref != -INFINITY;
     mref = mnew;
+    const float msub = mnew == -INFINITY ? 0.0f : mnew;  // masked scores give exp2(-inf) = 0, never NaN
     float sum = 0.0f;
 #pragma unroll
     for (int v = 0; v < 16; v++) {
-      const float pv = __builtin_amdgcn_exp2f(fmaf(st[v], log2e, -mnew));
+      const float pv = __builtin_amdgcn_exp2f(fmaf(st[v], log2e, -msub));
       st[v] = pv;
       sum += pv;
     }
@@ -411,9 +454,9 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
     }
   };
 
-  for (int kt = 0; kt < ntiles; kt++) {
+  for (int kt = kt0; kt < kt1; kt++) {
     const int ln = opaque(tid) & 63;
-    if (kt + 1 < ntiles) issue(kt + 1, ln);
+    if (kt + 1 < kt1) issue(kt + 1, ln);
     h8 pa[2];
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
@@ -425,14 +468,42 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
     __syncthreads();                // ... and every wave's; nobody reads the current buffer any more
   }
 
+  float* ep = reinterpret_cast<float*>(lds_raw) + (size_t)wave * 32 * kEP;
+  const int er = lane >> 5, ec = 4 * (lane & 31);
+  if (npieces > 1) {
+    // one piece of a split key range: unnormalised O and the row's (reference max, sum) to the partial slot
+    // (slot = pair's first slot + pieces of the blocks below qb + piece); gqa_combine_kernel finishes the rows
+    const int per_pair = gridDim.x / npair;
+    const int slot = pair * per_pair + (per_pair - (id / npair - piece) - npieces) + piece;
+    const size_t rbase = ((size_t)slot * 4 + (wave & 3)) * kRows + 32 * (wave >> 2);
+    float* po = a.part + rbase * kHD;
+    float* pml = a.part + (size_t)a.part_slots * 4 * kRows * kHD + rbase * 2;
+    if (half == 0) {
+      pml[2 * c32] = mref;
+      pml[2 * c32 + 1] = lsum;
+    }
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) ep[(8 * (v >> 2) + 4 * half + (v & 3)) * kEP + 32 * j + c32] = O[4 * p + j][v];
+      wave_sync();
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const f4 o = lds4(ep + (2 * i + er) * kEP + ec);
+        *(__attribute__((address_space(1))) f4*)(po + (size_t)(2 * i + er) * kHD + 128 * p + ec) = o;
+      }
+      wave_sync();
+    }
+    return;
+  }
   // epilogue: out[t][h][d] = O / l * sigmoid(gate), through LDS (free after the loop's last barrier). Each wave
   // stages 32 rows x 128 dims of O / l at a time; then a lane handles 4 consecutive dims of a row (rows 2 i + er),
   // so gate loads and output stores are 8- or 16-byte accesses, all issued before they are needed.
-  float* ep = reinterpret_cast<float*>(lds_raw) + (size_t)wave * 32 * kEP;
   float linv[16];
 #pragma unroll
   for (int v = 0; v < 16; v++) linv[v] = 1.0f / __shfl(lsum, 8 * (v >> 2) + 4 * half + (v & 3));
-  const int er = lane >> 5, ec = 4 * (lane & 31);
 #pragma unroll
   for (int p = 0; p < 2; p++) {
     f4 g[16];
@@ -459,18 +530,97 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   }
 }
 
+// Rows of query blocks whose key range was split: out = (O / l) * sigmoid(gate) with O = sum_j 2^(m_j - M) O_j,
+// l = sum_j 2^(m_j - M) l_j over the block's pieces in order, M = max_j m_j. The last two steps are the attention
+// kernel's own epilogue arithmetic, and a piece that holds no key of a row adds exact zeros, so a row comes out
+// the same whichever block and pieces it falls in. Grid (pairs * query blocks * 4 heads, 16): 4 rows per
+// workgroup, one lane per 4 dims of a row, every piece's loads issued together.
+constexpr int kMaxPieces = 16;
+template <typename T>
+__global__ __launch_bounds__(256) void gqa_combine_kernel(GqaArgs a, int per_pair) {
+  const int npair = a.B * a.HK;
+  const int hh = blockIdx.x & 3, pq = blockIdx.x >> 2, pair = pq % npair, qb = pq / npair;
+  const int np = (gqa_ntiles(a, qb) + a.split - 1) / a.split;
+  const int row = 4 * blockIdx.y + ((int)threadIdx.x >> 6), c4 = threadIdx.x & 63;
+  const int t = qb * kRows + row;
+  if (np < 2 || t >= a.L) return;
+  int cum = 0;
+  for (int q = 0; q < qb; q++) cum += (gqa_ntiles(a, q) + a.split - 1) / a.split;
+  const int slot0 = pair * per_pair + cum;
+  const int b = pair / a.HK, h = (pair % a.HK) * 4 + hh;
+  gptr<float> po = gp<float>(a.part);
+  gptr<float> pml = gp<float>(a.part) + (size_t)a.part_slots * 4 * kRows * kHD;
+  const f4 g = ld4(gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)h * 2 * kHD + kHD + 4 * c4);
+  float mj[kMaxPieces], lj[kMaxPieces];
+  f4 oj[kMaxPieces];
+#pragma unroll
+  for (int j = 0; j < kMaxPieces; j++) {
+    if (j < np) {
+      const size_t r = ((size_t)(slot0 + j) * 4 + hh) * kRows + row;
+      mj[j] = pml[r * 2];
+      lj[j] = pml[r * 2 + 1];
+      oj[j] = *(gptr<f4>)(po + r * kHD + 4 * c4);
+    }
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kMaxPieces; j++)
+    if (j < np) M = fmaxf(M, mj[j]);
+  f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+  float l = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kMaxPieces; j++) {
+    if (j < np) {
+      const float w = mj[j] == M ? 1.0f : __builtin_amdgcn_exp2f(mj[j] - M);
+      o = o + w * oj[j];
+      l = l + w * lj[j];
+    }
+  }
+  const float linv = 1.0f / l;
+  f4 r;
+#pragma unroll
+  for (int c = 0; c < 4; c++) r[c] = (o[c] * linv) * sigmoid(g[c]);
+  store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + 4 * c4, r);
+}
+
 template <typename T>
 hipError_t launch_attn(const GqaArgs& a, hipStream_t s) {
   auto k = gqa_attn_kernel<T>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)kAttnLds);
   if (e != hipSuccess) return e;
-  dim3 grid(((a.L + kRows - 1) / kRows) * a.HK * a.B), block(64 * kWaves);
-  hipLaunchKernelGGL(k, grid, block, kAttnLds, s, a);
+  const int npair = a.B * a.HK, nqb = (a.L + kRows - 1) / kRows;
+  int per_pair = nqb;
+  bool any_split = false;
+  if (a.split > 0) {
+    per_pair = 0;
+    for (int q = 0; q < nqb; q++) {
+      const int np = (host_ntiles(a, q) + a.split - 1) / a.split;
+      per_pair += np;
+      any_split |= np > 1;
+    }
+    if (any_split && ((size_t)npair * per_pair > (size_t)a.part_slots || !a.part)) return hipErrorInvalidValue;
+    if ((a.LT / kBK + a.split - 1) / a.split > kMaxPieces) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(k, dim3(npair * per_pair), dim3(64 * kWaves), kAttnLds, s, a);
+  if ((e = hipGetLastError()) != hipSuccess || !any_split) return e;
+  hipLaunchKernelGGL(gqa_combine_kernel<T>, dim3(npair * nqb * 4, kRows / 4), dim3(256), 0, s, a, per_pair);
   return hipGetLastError();
 }
 
 }  // namespace
+
+size_t gqa_part_slot_bytes() { return (size_t)4 * kRows * (kHD + 2) * sizeof(float); }
+
+// Per pair, a call with P + L <= max_ctx has at most sum_{k=2}^{N+1} ceil(k / split) pieces (N = max_ctx / 64):
+// block qb reads at most P/64 + qb + 2 tiles and there are at most N - P/64 blocks.
+size_t gqa_part_slots(int pairs, int max_ctx, int split) {
+  if (split <= 0) return 0;
+  const int N = (max_ctx + kBK - 1) / kBK;
+  size_t per = 0;
+  for (int k = 2; k <= N + 1; k++) per += (size_t)((k + split - 1) / split);
+  return per * (size_t)pairs;
+}
 
 hipError_t launch_gqa(const GqaArgs& a, hipStream_t s) {
   // RD = 64 puts both halves of every rotated q pair in one lane of the fused q preparation

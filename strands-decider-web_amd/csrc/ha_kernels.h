@@ -40,7 +40,17 @@ struct GqaArgs {
   const float* rope;         // [LT][RD] cos/sin pairs
   _Float16* K;               // [B][HK][LT][HD] cache, row-major
   _Float16* V;               // [B][HK][HD][LT] cache, transposed (positions contiguous)
+  // Split key ranges: with split > 0, the keys of a query block are processed in pieces of `split` 64-key tiles
+  // at absolute tile boundaries, by separate workgroups; a block with more than one piece writes per-piece partial
+  // results to `part` (part_slots slots) and gqa_combine_kernel merges them. 0: one workgroup per block.
+  int split;
+  int part_slots;
+  float* part;               // [slots][4][64][HD] unnormalised O, then [slots][4][64][2] (reference max, sum)
 };
+
+// Slots of partial results the split GQA path needs for any call on a context of at most max_ctx positions.
+size_t gqa_part_slots(int pairs, int max_ctx, int split);
+size_t gqa_part_slot_bytes();
 
 // Copy the raw rows [dst_first, P + L) (dst_first >= s0 - (KC-1)) of every sequence from (tail, in) into
 // `tail_out` ([B][tail_cap][stride]); only the conv channels [0, C) and the a/b columns are kept.

@@ -63,3 +63,38 @@ def test_prefix_suffix_bit_exact(P, L):
     (suf,), _ = r.forward([x[:, P:]], cache=snap)
     np.testing.assert_array_equal(pre, full[:, :P])
     np.testing.assert_array_equal(suf, full[:, P:])
+
+
+@pytest.mark.parametrize("P,L", [(1000, 700), (1536, 64), (640, 1), (700, 1300), (1, 1998)])
+def test_split_key_ranges_prefix_suffix_bit_exact(P, L):
+    # one sequence: few (sequence, KV head) pairs, so the engine splits the key range of long query blocks over
+    # workgroups (pieces of 8 tiles at absolute boundaries) and merges the partial results; a resumed suffix must
+    # still equal the same rows of one forward bit for bit, whatever the blocks and pieces of the two calls
+    x = synth.gqa_rows(P + L, 1, seed=6)
+    p = synth.gqa_params(seed=6, noise=0.1)
+    r = Runner(["full_attention"], batch=1, max_ctx=2048)
+    r.set_params(0, p)
+    (full,), _ = r.forward([x])
+    (pre,), snap = r.forward([x[:, :P]], keep=True)
+    (suf,), _ = r.forward([x[:, P:]], cache=snap)
+    np.testing.assert_array_equal(pre, full[:, :P])
+    np.testing.assert_array_equal(suf, full[:, P:])
+
+
+def test_split_key_ranges_match_oracle_and_unsplit():
+    # the same sequence through a one-sequence engine (split key ranges) and as sequence 0 of a two-sequence
+    # engine (one workgroup per query block), both against the oracle
+    T = 1500
+    x1 = synth.gqa_rows(T, 1, seed=7)
+    x5 = np.concatenate([x1, synth.gqa_rows(T, 1, seed=8)], 0)
+    p = synth.gqa_params(seed=7, noise=0.1)
+    r1 = Runner(["full_attention"], batch=1, max_ctx=2048)
+    r5 = Runner(["full_attention"], batch=2, max_ctx=2048)
+    r1.set_params(0, p)
+    r5.set_params(0, p)
+    (o1,), _ = r1.forward([x1])
+    (o5,), _ = r5.forward([x5])
+    ref, _ = oracle_gqa(x1, p, 2048)
+    e1, e5, e15 = rel_err(o1, ref), rel_err(o5[:1], ref), rel_err(o1, o5[:1])
+    print("split vs oracle %.2e, unsplit vs oracle %.2e, split vs unsplit %.2e" % (e1, e5, e15))
+    assert e1 < TOL and e5 < TOL and e15 < TOL
