@@ -155,13 +155,13 @@ struct Width {
 
 // Block column J of T below the diagonal: T_iJ = -T_ii sum_{k=J}^{i-1} A_ik T_kJ for block rows i = J+1..3, in
 // order. The column's blocks stay in registers (D layout: rows 4 grp + e, column c16), so A is never overwritten
-// and the three column waves need no barrier between block rows; only the f16 copies T diag(beta) and
-// T diag(beta e^gc) are stored. The D layout is used directly as the B operand of v_mfma_f32_16x16x4f32 by giving
+// and the three column waves need no barrier between block rows; only the f16 copies T diag(beta) and (with
+// kWithTw) T diag(beta e^gc) are stored. The D layout is used directly as the B operand of v_mfma_f32_16x16x4f32 by giving
 // step e the K index 4 grp + e, and the A operand is read in the same order.
-template <int J, typename LdsT>
+template <int J, bool kWithTw = true, typename LdsT>
 __device__ __forceinline__ void t_column(LdsT& sm, int grp, int c16) {
   const int cj = 16 * J + c16;
-  const float fb = sm.bt[cj], fw = fb * sm.eg[cj];
+  const float fb = sm.bt[cj], fw = kWithTw ? fb * sm.eg[cj] : 0.0f;
   f4 Tc[4];
 #pragma unroll
   for (int e = 0; e < 4; e++) Tc[J][e] = sm.Tm[(16 * J + 4 * grp + e) * kAP + cj];
@@ -200,7 +200,7 @@ __device__ __forceinline__ void t_column(LdsT& sm, int grp, int c16) {
     for (int e = 0; e < 4; e++) {
       const int t = 16 * bi + 4 * grp + e;
       sm.Tb[t * kTP + cj] = (_Float16)(Tc[bi][e] * fb);
-      sm.Tw[t * kTP + cj] = (_Float16)(Tc[bi][e] * fw);
+      if constexpr (kWithTw) sm.Tw[t * kTP + cj] = (_Float16)(Tc[bi][e] * fw);
     }
   }
 }

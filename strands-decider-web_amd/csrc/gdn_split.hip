@@ -2,20 +2,22 @@
 //
 // Same semantics and chunk geometry as gdn_chunk.hip (the sequential rule of reference
 // web/public/engine/wgsl.js:124-187 + 252-268 in the chunked WY/UT form, chunk 64, chunk boundaries at s0 + 64 k),
-// split along the one dependency that is sequential: everything derived from a chunk's own rows (the q/k conv,
+// split along the one dependency that is sequential: everything derived from a chunk's own rows (the q/k/v conv,
 // l2 norms, gates, A = strictly_lower(beta k k^T decay) and T = (I + A)^-1) does not depend on the state, so
 //   gdn_prep_kernel  runs one workgroup per (chunk, sequence, head), all chunks at once over the whole chip, and
-//                    writes each chunk's "image" (q^, k^, T diag(beta), T diag(beta e^gc) in f16 and the gate
-//                    vectors) to a scratch buffer, in the exact layout the recurrence keeps in LDS;
+//                    writes each chunk's "image" (q^, k^, T diag(beta), v^T in f16 and the gate vectors) to a
+//                    scratch buffer, in the exact layout the recurrence keeps in LDS;
 //   gdn_recur_kernel runs one workgroup per (sequence, head) through the chunks in order, holding the fp32 state in
 //                    MFMA accumulators (8 waves x 16 value columns). Per chunk it DMAs the next image into LDS while
-//                    it does the state work of the current one, and builds k^T, the decay-masked scores q^ k^T and
-//                    the v conv itself (cheap, and their images would cost more HBM traffic than they save).
+//                    it does the state work of the current one, and builds k^T and the decay-masked scores q^ k^T
+//                    itself (cheap, and their images would cost more HBM traffic than they save). V_new is formed as
+//                    T diag(beta) (v - diag(e^gc) k^ S), one product instead of two.
 // The state-independent work is then off the per-chunk critical path, which is what bounds the fused kernel when
 // there are fewer (sequence, head) pairs than CUs (B = 1: 16 of 256 CUs).
 //
 // Both kernels share the fused kernel's helpers and MFMA operand conventions (gdn_common.h); the per-column state
-// arithmetic is the fused kernel's, the gated norm's row sums are formed in a different order (16-column partials).
+// arithmetic follows the fused kernel's except for the V_new bracket, and the gated norm's row sums are formed in
+// a different order (16-column partials).
 #include <stddef.h>
 
 #include "gdn_common.h"
@@ -27,8 +29,8 @@ namespace {
 struct Img {
   _Float16 Qs[kCH * kQP];  // q^ / sqrt(DK), [t][i]
   _Float16 Ks[kCH * kQP];  // k^, [t][i]
-  _Float16 Tb[kCH * kTP];  // T diag(beta), [t][t']
-  _Float16 Tw[kCH * kTP];  // T diag(beta e^gc)
+  _Float16 Tb[kCH * kTP];  // T diag(beta), [t][t'] (blocks above the diagonal zero)
+  _Float16 VT[kDV * kTP];  // v^ = SiLU(conv(v)) transposed, [j][t], 8-row groups swizzled by vt16
   float eg[kCH];           // e^gc
   float ed[kCH];           // e^(gc_63 - gc)
   float gc[kCH];           // cumulative log decay inside the chunk
@@ -36,30 +38,33 @@ struct Img {
   float colf[3][kCH];      // colf[i-1][t'] = e^(gc_16i - gc_t') for t' < 16 i, in (0, 1]
 };
 static_assert(sizeof(Img) % 16 == 0, "image is copied in 16-byte words");
-constexpr int kImg = (int)((sizeof(Img) + 1023) / 1024 * 1024);  // image stride: whole 1 KiB DMA instructions
+constexpr int kImg = (int)((sizeof(Img) + 1023) / 1024 * 1024);  // image size: whole 1 KiB DMA instructions
+// Per chunk, the image is followed by the gated norm's gate factors gnorm_w[j] * SiLU(z[t][j]) in fp32, [j][t]:
+// the recurrence reads them straight into the D layout of its output rows (4 consecutive rows per load).
+constexpr int kGate = (int)sizeof(float) * kDV * kCH;
+constexpr int kChunkScratch = kImg + kGate;
 
 // ------------------------------------------------------------------------------------------------------------------
-// gdn_prep_kernel: 4 waves. Conv lanes as the fused kernel's producers (8 rows x 8 channels of q or k per lane),
-// wave 3 also the gates, the diagonal blocks of A and their forward substitution; waves 0..2 the six
-// below-diagonal blocks of A and then one block column of T each.
+// gdn_prep_kernel: 4 waves. Conv lane pt: rows 8 (pt / 32) .. + 7 of the chunk, channels 4 (pt % 32) .. + 3 of each
+// of q, k and v. q^ and v^ go straight from registers to the image; k^ (the operand of A = k^ k^T) and T diag(beta)
+// are built in LDS and copied out with the gate vectors. Wave 3 also forms the gates, the diagonal blocks of A and
+// their forward substitution; waves 0..2 the six below-diagonal blocks of A and then one block column of T each.
 constexpr int kPW = 4, kPT = 64 * kPW;
 constexpr int kPRG = 8;  // rows per conv lane
 constexpr int kPG = kPW - 1;
 
 struct PrepLds {
-  // the image, built in place; these members are copied out as one block
-  _Float16 Qs[kCH * kQP];
   _Float16 Ks[kCH * kQP];
   _Float16 Tb[kCH * kTP];
-  _Float16 Tw[kCH * kTP];
-  float eg[kCH], ed[kCH], gc[kCH], rowf[kCH], colf[3][kCH];
-  // working tiles
-  float Tm[kCH * kAP];    // A, then T (fp32)
-  float cwq[8][32][kKC];  // q/k conv taps: channel 8 g + c (g < 32: q then k) at cwq[c][g]
-  float bt[kCH];          // beta
-  float brow[kCH];        // beta_t rowf_t
+  float eg[kCH], ed[kCH], gc[kCH], rowf[kCH], colf[3][kCH];  // as in Img, in the same order
+  float Tm[kCH * kAP];     // A, then T (fp32)
+  float cw[12][32][kKC];   // conv taps: channel 4 g + c of q (c < 4), k (4 <= c < 8), v (c >= 8) at cw[c][g]
+  float bt[kCH];           // beta
+  float brow[kCH];         // beta_t rowf_t
 };
-static_assert(offsetof(PrepLds, Tm) == sizeof(Img), "the image members lead the prep LDS");
+static_assert(offsetof(PrepLds, colf) + sizeof(float) * 3 * kCH - offsetof(PrepLds, eg) ==
+                  offsetof(Img, colf) + sizeof(float) * 3 * kCH - offsetof(Img, eg),
+              "gate vectors are copied as one block");
 
 template <typename T>
 __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
@@ -74,30 +79,29 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
   const unsigned rowb = (unsigned)a.stride * sizeof(T);
   const char* const seq_in = (const char*)a.in + (size_t)b * a.L * rowb;
+  char* const dst = (char*)a.img + ((size_t)bh * a.img_chunks + c) * kChunkScratch;
 
-  for (int i = tid0; i < 2 * 128 * kKC; i += kPT) {
-    const int lc = i / kKC, j = i % kKC;
-    const int ch = lc < 128 ? h * kDK + lc : a.H * kDK + h * kDK + (lc - 128);
-    sm.cwq[lc & 7][lc >> 3][j] = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
-  }
   const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
   const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
 
-  // raw rows cs-3 .. cs+63: lane pt rows 8 (pt / 32) - 3 .. 8 (pt / 32) + 7, channels 8 (pt % 16) of q (pt % 32 < 16)
-  // or k. Rows past the end repeat the last row (they only feed conv outputs past the end, which are masked);
-  // rows before P come from the tail buffer.
-  const int pt = tid0, rg = pt >> 5, cgi = pt & 31, qk = cgi >> 4, cg = cgi & 15;
-  float xq[kPRG + kKC - 1][8];
+  // raw rows cs-3 .. cs+63 of this lane's q, k and v channels (x[i][0..3] q, [4..7] k, [8..11] v): every load
+  // instruction reads whole 512-byte row segments. Rows past the end repeat the last row (they only feed conv
+  // outputs past the end, which are masked); rows before P come from the tail buffer.
+  const int pt = tid0, rg = pt >> 5, cl = pt & 31;
+  float x[kPRG + kKC - 1][12];
   const RowSrc src = row_src(a);
   {
-    const int col = (qk ? a.H * kDK : 0) + h * kDK + 8 * cg;
+    const int col = h * kDK + 4 * cl;
     const bool fast = cs - (kKC - 1) >= a.P && cs + kCH <= end;
     const char* base = seq_in + (ptrdiff_t)(cs - (kKC - 1) - a.P) * rowb;
     const unsigned off = (unsigned)(kPRG * rg) * rowb + (unsigned)col * (unsigned)sizeof(T);
 #pragma unroll
     for (int i = 0; i < kPRG + kKC - 1; i++) {
       const int r = min(cs + kPRG * rg - (kKC - 1) + i, end - 1);
-      load8(fast ? gp<T>(base + (size_t)i * rowb + off) : row_of<T>(a, src, b, r) + col, xq[i]);
+      const gptr<T> q = fast ? gp<T>(base + (size_t)i * rowb + off) : row_of<T>(a, src, b, r) + col;
+      load4(q, x[i]);
+      load4(q + a.H * kDK, x[i] + 4);
+      load4(q + 2 * a.H * kDK, x[i] + 8);
     }
   }
   // the gate wave: a and b of row `lane` of the chunk (rows past the end are masked where the gates are formed)
@@ -108,33 +112,71 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
     ga = (float)grow[aoff];
     gb = (float)grow[boff];
   }
+  // conv taps to LDS, behind the row loads
+  for (int i = tid0; i < 3 * 128 * kKC; i += kPT) {
+    const int lc = i / kKC, j = i % kKC, part = lc >> 7;
+    const int ch = part * a.H * kDK + h * kDK + (lc & 127);
+    sm.cw[(lc & 3) + 4 * part][(lc & 127) >> 2][j] = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
+  }
+  // blocks above the diagonal of T diag(beta) are read by full 32-wide K blocks and never written otherwise:
+  // row block rb (< 3) has 6 - 2 rb such 8-column groups per row, from column 16 (rb + 1)
+  if (tid0 < 192) {
+    const int k = tid0, rb = k < 96 ? 0 : k < 160 ? 1 : 2, k2 = k - (rb == 0 ? 0 : rb == 1 ? 96 : 160);
+    const int ng = 6 - 2 * rb, t = 16 * rb + k2 / ng, g = k2 % ng + 2 * (rb + 1);
+    *reinterpret_cast<h8*>(sm.Tb + t * kTP + 8 * g) = h8{};
+  }
   __syncthreads();  // conv taps visible
 
-  // conv + SiLU + l2 norm (q also scaled by 1/sqrt(DK)) -> q^ / k^ rows
+  // conv + SiLU; q and k rows l2-normalised (q also scaled by 1/sqrt(DK); a row's 128 channels of q, of k, sit in
+  // the 32 lanes of a half wave): q^ to the image, k^ to LDS; v^ columns (8 rows each) to the image's v^T
   {
-    float uq[kPRG][8], ss[kPRG];
+    float u[kPRG][12], ssq[kPRG], ssk[kPRG];
 #pragma unroll
-    for (int r = 0; r < kPRG; r++) ss[r] = 0.0f;
+    for (int r = 0; r < kPRG; r++) ssq[r] = ssk[r] = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const f4 wc = lds4(sm.cwq[k][cgi]);
+    for (int k = 0; k < 12; k++) {
+      const f4 wc = lds4(sm.cw[k][cl]);
 #pragma unroll
       for (int r = 0; r < kPRG; r++) {
-        float sv = wc[0] * xq[r][k];
-        sv = fmaf(wc[1], xq[r + 1][k], sv);
-        sv = fmaf(wc[2], xq[r + 2][k], sv);
-        sv = fmaf(wc[3], xq[r + 3][k], sv);
-        uq[r][k] = kPRG * rg + r < m ? silu(sv) : 0.0f;
-        ss[r] = fmaf(uq[r][k], uq[r][k], ss[r]);
+        float sv = wc[0] * x[r][k];
+        sv = fmaf(wc[1], x[r + 1][k], sv);
+        sv = fmaf(wc[2], x[r + 2][k], sv);
+        sv = fmaf(wc[3], x[r + 3][k], sv);
+        u[r][k] = kPRG * rg + r < m ? silu(sv) : 0.0f;
+        if (k < 4)
+          ssq[r] = fmaf(u[r][k], u[r][k], ssq[r]);
+        else if (k < 8)
+          ssk[r] = fmaf(u[r][k], u[r][k], ssk[r]);
       }
     }
 #pragma unroll
     for (int r = 0; r < kPRG; r++) {
-      const float rs = rsqrtf(row_sum16(ss[r]) + 1e-6f) * (qk ? 1.0f : qscale);
-      h8 hv;
+      float sq = row_sum16(ssq[r]), sk = row_sum16(ssk[r]);
+      sq += __shfl_xor(sq, 16);
+      sk += __shfl_xor(sk, 16);
+      const float rq = rsqrtf(sq + 1e-6f) * qscale, rk = rsqrtf(sk + 1e-6f);
+      const int t = kPRG * rg + r;
+      *(__attribute__((address_space(1))) h4*)(dst + offsetof(Img, Qs) + 2 * (size_t)(t * kQP + 4 * cl)) =
+          h4{(_Float16)(u[r][0] * rq), (_Float16)(u[r][1] * rq), (_Float16)(u[r][2] * rq), (_Float16)(u[r][3] * rq)};
+      *reinterpret_cast<h4*>(sm.Ks + t * kQP + 4 * cl) =
+          h4{(_Float16)(u[r][4] * rk), (_Float16)(u[r][5] * rk), (_Float16)(u[r][6] * rk), (_Float16)(u[r][7] * rk)};
+    }
 #pragma unroll
-      for (int k = 0; k < 8; k++) hv[k] = (_Float16)(uq[r][k] * rs);
-      *reinterpret_cast<h8*>((qk ? sm.Ks : sm.Qs) + (kPRG * rg + r) * kQP + 8 * cg) = hv;
+    for (int cc = 0; cc < 4; cc++) {
+      h8 vt;
+#pragma unroll
+      for (int r = 0; r < kPRG; r++) vt[r] = (_Float16)u[r][8 + cc];
+      *(__attribute__((address_space(1))) h8*)(dst + offsetof(Img, VT) + 2 * (size_t)vt16(4 * cl + cc, rg)) = vt;
+    }
+  }
+  // z of rows 8 rg .. + 7 (this lane's 4 channels) for the gate factors, in flight behind the work below; rows
+  // outside [P, P + L) are clamped (their outputs are never stored)
+  float zr[kPRG][4];
+  if (a.gnorm) {
+#pragma unroll
+    for (int r = 0; r < kPRG; r++) {
+      const int rr = min(max(cs + kPRG * rg + r - a.P, 0), a.L - 1);
+      load4(gp<T>(seq_in) + (size_t)rr * a.stride + a.C + h * kDV + 4 * cl, zr[r]);
     }
   }
   // gates: beta, the cumulative log decay (lane = row) and the vectors derived from it
@@ -163,14 +205,6 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
     for (int i = 1; i < 4; i++) {
       const float gi = __shfl(gcr, 16 * i);
       sm.colf[i - 1][lane] = lane < 16 * i ? __expf(gi - gcr) : 0.0f;
-    }
-  }
-  // blocks above the diagonal of the f16 T tiles are read by full 32-wide K blocks and never written otherwise
-  for (int idx = tid0; idx < kCH * kCH; idx += kPT) {
-    const int t = idx >> 6, tp = idx & 63;
-    if ((tp >> 4) > (t >> 4)) {
-      sm.Tb[t * kTP + tp] = (_Float16)0.0f;
-      sm.Tw[t * kTP + tp] = (_Float16)0.0f;
     }
   }
   __syncthreads();
@@ -213,12 +247,11 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
       for (int j = 0; j < r; j++) acc = fmaf(-ar[j], pc[j], acc);
       pc[r] = acc;
     }
-    const float cb = sm.bt[base + c16], cbw = cb * sm.eg[base + c16];
+    const float cb = sm.bt[base + c16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       sm.Tm[(base + r) * kAP + base + c16] = pc[r];
       sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cb);
-      sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cbw);
     }
   } else {
     // below-diagonal blocks of A: tiles 1,3,4,6,7,8 of the 10 on or below the diagonal, two per wave
@@ -242,25 +275,45 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
   }
   __syncthreads();
   if (w == 0)
-    t_column<0>(sm, grp, c16);
+    t_column<0, false>(sm, grp, c16);
   else if (w == 1)
-    t_column<1>(sm, grp, c16);
+    t_column<1, false>(sm, grp, c16);
   else if (w == 2)
-    t_column<2>(sm, grp, c16);
+    t_column<2, false>(sm, grp, c16);
   __syncthreads();
 
-  // the image out, 16 bytes per lane per step
-  char* dst = (char*)a.img + ((size_t)bh * a.img_chunks + c) * kImg;
-  for (int i = tid0; i < (int)(sizeof(Img) / 16); i += kPT)
-    *(__attribute__((address_space(1))) f4*)(dst + 16 * (size_t)i) = *reinterpret_cast<const f4*>(lds_raw + 16 * i);
+  if (a.gnorm) {
+    const f4 gw = ld4(gp<float>(a.gnorm) + 4 * cl);
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+      float* g = (float*)(dst + kImg) + (size_t)(4 * cl + cc) * kCH + kPRG * rg;
+      f4 lo, hi;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        lo[r] = gw[cc] * silu(zr[r][cc]);
+        hi[r] = gw[cc] * silu(zr[r + 4][cc]);
+      }
+      store4(gpw<float>(g), lo);
+      store4(gpw<float>(g + 4), hi);
+    }
+  }
+  // k^, T diag(beta) and the gate vectors out, 16 bytes per lane per step
+  auto copy_out = [&](size_t img_off, const void* from, int bytes) {
+    for (int i = tid0; i < bytes / 16; i += kPT)
+      *(__attribute__((address_space(1))) f4*)(dst + img_off + 16 * (size_t)i) =
+          *reinterpret_cast<const f4*>((const char*)from + 16 * i);
+  };
+  copy_out(offsetof(Img, Ks), sm.Ks, (int)sizeof(sm.Ks));
+  copy_out(offsetof(Img, Tb), sm.Tb, (int)sizeof(sm.Tb));
+  copy_out(offsetof(Img, eg), sm.eg, (int)(sizeof(Img) - offsetof(Img, eg)));
 }
 
 // ------------------------------------------------------------------------------------------------------------------
 // gdn_recur_kernel: 8 waves; wave w owns value columns 16 w .. 16 w + 15 of the fp32 state (MFMA D layout:
 // S[it][e] = S[16 it + 4 grp + e][16 w + c16]) and all of every chunk's work for them. Per period p, two segments:
 //   A: chunk p's state work (k^ S, V_new, q^ S, o, the state update, the gated-norm row partials); the DMA of image
-//      p+1 into the other image buffer and the raw v rows of p+1 are issued at its start
-//   B: chunk p's gated norm and output store; k^T, the masked scores and the v conv of chunk p+1; z of p+1
+//      p+1 into the other image buffer is issued at its start
+//   B: chunk p's gated norm and output store; k^T and the masked scores of chunk p+1; z of p+1
 constexpr int kRW = 8, kRT = 64 * kRW;
 
 // One halving step of a transposed 16-lane reduction over v[0 .. 2N): a lane whose selection bit is clear keeps the
@@ -273,14 +326,11 @@ __device__ __forceinline__ void halve(float* v, int hi) {
     v[i] = keep + DPP_F(send, CTRL);
   }
 }
-constexpr int kRRG = 4;  // rows per v-conv lane
 
 struct RecLds {
   unsigned char img[2][kImg];  // chunk images; chunk p in img[p & 1]
   _Float16 KT[kDK * kTP];      // k^ transposed, [i][t], 8-column groups swizzled by kt16
   _Float16 Att[kCH * kTP];     // decay-masked causal q^ k^T, [t][t']
-  _Float16 VT[kDV * kTP];      // v transposed, [j][t], swizzled by vt16
-  float cwv[4][32][kKC];       // v conv taps: channel 4 g + c at cwv[c][g]
   float red[kCH * kRW];        // gated-norm partial sums, [t][wave]
   float inv[kRW][kCH];         // per wave: 1 / rms of each row
 };
@@ -296,13 +346,9 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
   const unsigned rowb = (unsigned)a.stride * sizeof(T);
   const unsigned orowb = (unsigned)(a.H * kDV) * sizeof(T);
   const char* const seq_in = (const char*)a.in + (size_t)b * a.L * rowb;
-  const char* const imgs = (const char*)a.img + (size_t)bh * a.img_chunks * kImg;
+  const char* const imgs = (const char*)a.img + (size_t)bh * a.img_chunks * kChunkScratch;
   const size_t sbase = ((size_t)b * a.H + h) * kDK * kDV;
 
-  for (int i = tid0; i < 128 * kKC; i += kRT) {
-    const int lc = i / kKC, j = i % kKC;
-    sm.cwv[lc & 3][lc >> 2][j] = gp<float>(a.conv_w)[(size_t)(2 * a.H * kDK + h * kDV + lc) * kKC + j];
-  }
   for (int idx = tid0; idx < kCH * kCH; idx += kRT) {
     const int t = idx >> 6, tp = idx & 63;
     if ((tp >> 4) > (t >> 4)) sm.Att[t * kTP + tp] = (_Float16)0.0f;
@@ -310,41 +356,20 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
 
   // this wave's share of one chunk image: 1 KiB DMA instructions w, w + 8, ...
   auto issue_img = [&](int p) {
-    const char* src = imgs + (size_t)p * kImg;
+    const char* src = imgs + (size_t)p * kChunkScratch;
     unsigned char* dst = sm.img[p & 1];
     const int ln = opaque(tid0) & 63;
     for (int i = w; i < kImg / 1024; i += kRW)
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + 1024 * (size_t)i + 16 * ln),
                                        (__attribute__((address_space(3))) void*)(dst + 1024 * i), 16, 0, 0);
   };
-  // raw v rows of the chunk at cs: lane rows 4 (tid / 32) - 3 .. 4 (tid / 32) + 3, channels 4 (tid % 32) .. + 3;
-  // rows past the end repeat the last row (they only feed masked conv outputs)
-  float xv[kRRG + kKC - 1][4];
-  const RowSrc src = row_src(a);
-  auto fetch_v = [&](int cs) {
-    const int ct = opaque(tid0), rg = ct >> 5, cvg = ct & 31;
-    const int col = 2 * a.H * kDK + h * kDV + 4 * cvg;
-    const bool fast = cs - (kKC - 1) >= a.P && cs + kCH <= end;
-    const char* base = seq_in + (ptrdiff_t)(cs - (kKC - 1) - a.P) * rowb;
-    const unsigned off = (unsigned)(kRRG * rg) * rowb + (unsigned)col * (unsigned)sizeof(T);
-#pragma unroll
-    for (int i = 0; i < kRRG + kKC - 1; i++) {
-      const int r = min(cs + kRRG * rg - (kKC - 1) + i, end - 1);
-      load4(fast ? gp<T>(base + (size_t)i * rowb + off) : row_of<T>(a, src, b, r) + col, xv[i]);
-    }
-  };
-  // z of the chunk at cs in the MFMA D layout of this lane's output: rows 16 ti + 4 grp + e, column 16 w + c16
-  float zq[4][4];
-  auto fetch_z = [&](int cs) {
+  // gate factors of chunk q in the MFMA D layout of this lane's output: rows 16 ti + 4 grp .. +3, column 16 w + c16
+  f4 zq[4];
+  auto fetch_z = [&](int q) {
     const int lane = opaque(tid0) & 63, grp = lane >> 4, c16 = lane & 15;
-    const gptr<T> zb = gp<T>(seq_in) + a.C + h * kDV + 16 * w + c16;
+    gptr<float> g = gp<float>(imgs + (size_t)q * kChunkScratch + kImg) + (size_t)(16 * w + c16) * kCH + 4 * grp;
 #pragma unroll
-    for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int rr = min(max(cs + 16 * ti + 4 * grp + e - a.P, 0), a.L - 1);
-        zq[ti][e] = (float)zb[(size_t)rr * a.stride];
-      }
+    for (int ti = 0; ti < 4; ti++) zq[ti] = ld4(g + 16 * ti);
   };
 
   f4 S[8];
@@ -356,17 +381,15 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
       for (int e = 0; e < 4; e++)
         S[it][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 16 * w + l16] : 0.0f;
   }
-  const float gwc = a.gnorm ? gp<float>(a.gnorm)[16 * w + (tid0 & 15)] : 1.0f;
   // Drain these loads here: the compiler's wait counting merges the loop's entry state into every iteration, so a
   // state load still outstanding at the loop head would make each period's first use of S wait for the image DMA
   // issued just before it.
   __builtin_amdgcn_s_waitcnt(0);
 
-  // chunk q's k^T, decay-masked scores and v conv (image q in LDS, its raw v rows in xv)
+  // chunk q's k^T and decay-masked scores (image q in LDS)
   auto prep_chunk = [&](int q) {
     const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
     const Img& nx = *reinterpret_cast<const Img*>(sm.img[q & 1]);
-    const int cs = a.s0 + kCH * q;
     // k^T from k^: items (channel i, 8-row group g8), two per lane
 #pragma unroll
     for (int k = 0; k < 2; k++) {
@@ -406,39 +429,18 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
         }
       }
     }
-    // v conv + SiLU -> v^T (rows 4 rg .. 4 rg + 3, channels 4 cvg .. + 3)
-    {
-      const int rg = tid >> 5, cvg = tid & 31;
-      const int m1 = min(kCH, end - cs);
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const f4 wc = lds4(sm.cwv[k][cvg]);
-        h4 vt;
-#pragma unroll
-        for (int r = 0; r < kRRG; r++) {
-          float sv = wc[0] * xv[r][k];
-          sv = fmaf(wc[1], xv[r + 1][k], sv);
-          sv = fmaf(wc[2], xv[r + 2][k], sv);
-          sv = fmaf(wc[3], xv[r + 3][k], sv);
-          vt[r] = (_Float16)(kRRG * rg + r < m1 ? silu(sv) : 0.0f);
-        }
-        *reinterpret_cast<h4*>(sm.VT + vt16(4 * cvg + k, rg >> 1) + 4 * (rg & 1)) = vt;
-      }
-    }
   };
 
-  // prologue: chunk 0's image and v rows, then its scores and v conv. The loop is entered with only z loads in
-  // flight, which nothing in segment A overwrites, so no wait in A depends on the DMA issued at its start.
-  const int last_cs = a.s0 + kCH * (nchunks - 1);
+  // prologue: chunk 0's image, then its k^T and scores. The loop is entered with only z loads in flight, which
+  // nothing in segment A overwrites, so no wait in A depends on the DMA issued at its start.
   issue_img(0);
-  fetch_v(a.s0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   prep_chunk(0);
-  if (a.gnorm) fetch_z(a.s0);
+  if (a.gnorm) fetch_z(0);
   __syncthreads();
   for (int p = 0; p < nchunks; p++) {
-    const int c0 = a.s0 + kCH * p, c1 = c0 + kCH;
+    const int c0 = a.s0 + kCH * p;
     f4 O[4];
     const int m = min(kCH, end - c0);
     const bool full = m == kCH;
@@ -463,24 +465,28 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
         }
       };
       read_kq(Aq[0], 0);
-      fetch_v(min(c1, last_cs));  // the next chunk's v rows, in flight behind this chunk's work (see below)
       f4 KS[4];
-      h8 tb[4][2], tw[4][2], vb[2];
+      h8 tb[4][2];
+      h4 vlo[2], vhi[2];
+      f4 eg4[4];
 #pragma unroll
       for (int kb = 0; kb < 4; kb++) {
         if (kb < 3) {
           read_kq(Aq[(kb + 1) & 1], kb + 1);
         } else {
-          // V_new operands: T diag(beta) and T diag(beta e^gc) rows, v^T columns
+          // V_new operands: rows of T diag(beta) in the permuted K order, this column's v^ rows in the same order
+          // (rows 32 k2 + 4 grp .. +3 and 32 k2 + 16 + 4 grp .. +3), e^gc of this lane's D-layout rows
 #pragma unroll
-          for (int ti = 0; ti < 4; ti++)
+          for (int ti = 0; ti < 4; ti++) {
 #pragma unroll
-            for (int k2 = 0; k2 <= (ti >> 1); k2++) {
-              tb[ti][k2] = *reinterpret_cast<const h8*>(im.Tb + (16 * ti + c16) * kTP + 32 * k2 + 8 * grp);
-              tw[ti][k2] = perm_a(im.Tw, kTP, 16 * ti + c16, k2, grp);
-            }
+            for (int k2 = 0; k2 <= (ti >> 1); k2++) tb[ti][k2] = perm_a(im.Tb, kTP, 16 * ti + c16, k2, grp);
+            eg4[ti] = lds4(&im.eg[16 * ti + 4 * grp]);
+          }
 #pragma unroll
-          for (int k2 = 0; k2 < 2; k2++) vb[k2] = *reinterpret_cast<const h8*>(sm.VT + vt16(col, 4 * k2 + grp));
+          for (int k2 = 0; k2 < 2; k2++) {
+            vlo[k2] = *reinterpret_cast<const h4*>(im.VT + vt16(col, 4 * k2 + (grp >> 1)) + 4 * (grp & 1));
+            vhi[k2] = *reinterpret_cast<const h4*>(im.VT + vt16(col, 4 * k2 + 2 + (grp >> 1)) + 4 * (grp & 1));
+          }
         }
         h8 S16 = pack_b(S[2 * kb], S[2 * kb + 1]);
         asm volatile("" : "+v"(S16)::"memory");
@@ -492,29 +498,31 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      // V_new = T diag(beta) v - T diag(beta e^gc) (k^ S)
-      const h8 KSb[2] = {pack_b(-KS[0], -KS[1]), pack_b(-KS[2], -KS[3])};
+      // V_new = T diag(beta) (v - diag(e^gc) k^ S): the bracket is formed in fp32 in the D layout of k^ S and
+      // rounded once to f16 as the B operand
+      h8 Bv[2];
+#pragma unroll
+      for (int k2 = 0; k2 < 2; k2++) {
+        const f4 lo = f4{(float)vlo[k2][0], (float)vlo[k2][1], (float)vlo[k2][2], (float)vlo[k2][3]} - eg4[2 * k2] * KS[2 * k2];
+        const f4 hi = f4{(float)vhi[k2][0], (float)vhi[k2][1], (float)vhi[k2][2], (float)vhi[k2][3]} - eg4[2 * k2 + 1] * KS[2 * k2 + 1];
+        Bv[k2] = pack_b(lo, hi);
+      }
       f4 Vn[4];
 #pragma unroll
       for (int ti = 0; ti < 4; ti++) {
         f4 u = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int k2 = 0; k2 <= (ti >> 1); k2++) {
-          u = mfma16(tb[ti][k2], vb[k2], u);
-          u = mfma16(tw[ti][k2], KSb[k2], u);
-        }
+        for (int k2 = 0; k2 <= (ti >> 1); k2++) u = mfma16(tb[ti][k2], Bv[k2], u);
         Vn[ti] = u;
       }
       __builtin_amdgcn_sched_barrier(0);
       // o = e^gc (q^ S) + scores V_new
       {
         h8 att[4][2];
-        f4 eg4[4];
 #pragma unroll
         for (int ti = 0; ti < 4; ti++) {
           att[ti][0] = perm_a(sm.Att, kTP, 16 * ti + c16, 0, grp);
           if (ti >= 2) att[ti][1] = perm_a(sm.Att, kTP, 16 * ti + c16, 1, grp);
-          eg4[ti] = lds4(&im.eg[16 * ti + 4 * grp]);
         }
         const h8 Vb0 = pack_b(Vn[0], Vn[1]), Vb1 = pack_b(Vn[2], Vn[3]);
 #pragma unroll
@@ -590,7 +598,7 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
         for (int ti = 0; ti < 4; ti++) {
           const f4 iv = lds4(&sm.inv[w][16 * ti + 4 * grp]);
 #pragma unroll
-          for (int e = 0; e < 4; e++) Y[ti][e] = Y[ti][e] * iv[e] * (gwc * silu(zq[ti][e]));
+          for (int e = 0; e < 4; e++) Y[ti][e] = Y[ti][e] * iv[e] * zq[ti][e];
         }
       }
       __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + col;
@@ -613,7 +621,7 @@ __global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
     // The v and z loads run every period (past the last chunk on the last chunk's rows, never used): conditional
     // loads would make the loop-carried registers a merge of old and new values, resolved with copies that wait
     // for the loads right after they are issued.
-    if (a.gnorm) fetch_z(min(c1, last_cs));
+    if (a.gnorm) fetch_z(min(p + 1, nchunks - 1));
     __syncthreads();  // A
   }
   const int g0 = (tid0 & 63) >> 4, l16 = tid0 & 15;
@@ -644,7 +652,7 @@ hipError_t launch(const GdnArgs& a, hipStream_t s) {
 
 }  // namespace
 
-size_t gdn_split_image_bytes() { return (size_t)kImg; }
+size_t gdn_split_image_bytes() { return (size_t)kChunkScratch; }
 
 hipError_t launch_gdn_split(const GdnArgs& a, hipStream_t s) {
   if (a.DK != kDK || a.DV != kDV || a.KC != kKC || !a.img) return hipErrorInvalidValue;
