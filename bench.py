@@ -148,9 +148,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the T / B sweep")
     ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy"],
-                    help="run only one layer kind (B=8, T=2048) --steps times, for rocprofv3; 'copy' runs a plain "
+                    help="run only one layer kind (T=2048, B=--profile-batch) --steps times, for rocprofv3; 'copy' runs a plain "
                          "512 MiB device-to-device copy kernel, the reference point that scales FETCH_SIZE / "
                          "WRITE_SIZE to bytes")
+    ap.add_argument("--profile-batch", type=int, default=8, help="batch size for --profile-kernel gdn / gqa")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the hybrid-attention path is benchmarked on a single GPU in this build "
@@ -180,6 +181,7 @@ def main():
     if args.profile_kernel:
         kind = "full_attention" if args.profile_kernel == "gqa" else "linear_attention"
         rec = ha.SEQUENTIAL if args.profile_kernel == "gdn-seq" else ha.CHUNKED
+        B = args.profile_batch
         with torch.cuda.stream(stream):
             e = make_engine(ha, [kind], B, 4096, stream.cuda_stream)
             i, o = make_buffers(torch, [kind], B, T)
@@ -254,7 +256,7 @@ def main():
                      "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": gdn_bytes, "bytes_per_token": gdn_bytes_per_token(),
                      "launch_ms": round(gdn_launch_ms, 5)},
-        "roofline_gqa": {"bound": "mfma", "kernel": "gqa_prep_kernel + gqa_attn_kernel",
+        "roofline_gqa": {"bound": "mfma", "kernel": "gqa_kv_kernel + gqa_attn_kernel",
                          "achieved": round(gqa_tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": round(gqa_tf / 2500.0, 4), "flops_per_launch": B * gqa_flops(T),
                          "launch_ms": round(gqa_launch_ms, 5)},
