@@ -140,6 +140,35 @@ int ha_copy_to_device(ha_engine* e, void* dst, const void* host, size_t bytes);
 int ha_copy_to_host(ha_engine* e, void* host, const void* src, size_t bytes);
 int ha_synchronize(ha_engine* e);
 
+/* ---- MatMulNBits projections: the matmuls either side of the path ----
+   Weight formats of web/public/gemmbench/kernels.js:1-14: blocks of 32 consecutive k of one output row n, `bits`
+   u32 words each ([N][K/32][bits]); 4 bits = MatMulNBits (element 2i in the low nibble of byte i, zero point 8),
+   2 bits = element e at bits 2(e%16) of word e/16, 3 bits = 2-bit low words plus a word of high bits. One f16 scale
+   per `group` (32 or 64) values of a row ([N][K/group]); symmetric w = (q - 2^(bits-1)) * scale, asymmetric
+   w = q * scale + bias with an f16 bias of the same shape. convert/export_engine.py:17-26 writes int4, group 32,
+   symmetric. */
+typedef struct ha_mnb ha_mnb;
+typedef struct ha_mnb_format {
+  int bits;  /* 2, 3 or 4 */
+  int group; /* 32 or 64 */
+  int asym;  /* 0 symmetric, 1 per-group bias */
+} ha_mnb_format;
+
+/* A quantised weight matrix on HIP device `device`: q, s and (asymmetric) b are device pointers the caller keeps
+   alive (the reference's weight storage buffers, engine.js:236-246). N must be a multiple of 16 (the export pads to
+   64), K of 32 and of the group. */
+int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const void* s, const void* b, int device,
+                  ha_mnb** out);
+/* y[M][N] = a[M][K] x W^T (f16 in and out, fp32 accumulation) on `stream` (hipStream_t as void*, NULL: the null
+   stream): the matmul dispatch of engine.js:236-246, kernel chosen by M as engine.js:17-33 does. a and y are device
+   pointers. The first call with M > 64 also builds the handle's dequantised f16 copy of W (N*K*2 bytes). */
+int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream);
+int ha_mnb_destroy(ha_mnb* w);
+/* In-place orthonormal Walsh-Hadamard transform of every contiguous n-block of the f16 array x (elems values, a
+   multiple of n; n a power of two up to 8192): the online input rotation of a tensor exported with `had: n`
+   (FWHT, web/public/engine/wgsl.js:91-108; applied before the matmul at engine.js:240). */
+int ha_fwht(void* x, long elems, int n, int device, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libha.so")
 NAPI_OUT = os.path.join(HERE, "js", "ha_napi.node")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["engine.cpp", "gdn_seq.hip", "gdn_chunk.hip", "gdn_split.hip", "gqa.hip", "tail.hip"]
+SOURCES = ["engine.cpp", "gdn_seq.hip", "gdn_chunk.hip", "gdn_split.hip", "gqa.hip", "tail.hip", "mnb.hip"]
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
@@ -46,7 +46,8 @@ def build_lib(verbose=False):
     with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
     tmp = LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs +
+         ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"], verbose)
     os.replace(tmp, LIB)
     return LIB
 

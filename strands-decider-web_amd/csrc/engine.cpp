@@ -197,6 +197,14 @@ void free_snapshot_buffers(ha_snapshot* s) {
 
 }  // namespace
 
+constexpr uint32_t kMnbMagic = 0x48414d4eu;
+struct ha_mnb {
+  uint32_t magic = kMnbMagic;
+  ha::MnbArgs args{};
+  int device = 0;
+  _Float16* w16 = nullptr;  // dequantised copy for the M > 64 product, built on first use
+};
+
 extern "C" {
 
 const char* ha_last_error(void) { return g_err.c_str(); }
@@ -571,6 +579,71 @@ int ha_synchronize(ha_engine* e) {
   if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
   HA_HIP(hipSetDevice(e->device));
   HA_HIP(hipStreamSynchronize(e->stream));
+  return HA_OK;
+}
+
+// ---- MatMulNBits projections ----
+
+int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const void* s, const void* b, int device,
+                  ha_mnb** out) {
+  if (!fmt || !out) return fail(HA_ERR_ARG, "fmt and out must be non-NULL");
+  *out = nullptr;
+  ha::MnbArgs a{};
+  a.N = N; a.K = K; a.bits = fmt->bits; a.group = fmt->group; a.asym = fmt->asym ? 1 : 0;
+  a.q = q; a.s = s; a.b = b;
+  if (ha::mnb_check(a) != hipSuccess)
+    return fail(HA_ERR_ARG, "unsupported MatMulNBits shape or format (N % 16, K % 32, K % group, bits 2/3/4, group "
+                            "32/64, q/s (and b when asymmetric) non-NULL)");
+  int ndev = 0;
+  HA_HIP(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) return fail(HA_ERR_ARG, "no HIP device " + std::to_string(device));
+  ha_mnb* w = new ha_mnb();
+  w->args = a;
+  w->device = device;
+  *out = w;
+  return HA_OK;
+}
+
+int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
+  if (!w || w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
+  if (M < 1 || !a || !y) return fail(HA_ERR_ARG, "M must be >= 1 and a, y non-NULL");
+  HA_HIP(hipSetDevice(w->device));
+  hipStream_t st = (hipStream_t)stream;
+  ha::MnbArgs g = w->args;
+  g.M = M; g.a = a; g.y = y;
+  if (M <= 64) {
+    HA_HIP(ha::launch_mnb_gemv(g, st));
+    return HA_OK;
+  }
+  if (!w->w16) {
+    int rc = dalloc(&w->w16, sizeof(_Float16) * (size_t)g.N * g.K);
+    if (rc) return rc;
+    HA_HIP(ha::launch_mnb_dequant(g, w->w16, st));
+  }
+  hipError_t he = ha::lt_gemm_f16(w->device, M, g.N, g.K, w->w16, a, y, st);
+  if (he != hipSuccess) return fail(HA_ERR_DEVICE, std::string("hipBLASLt f16 GEMM: ") + hipGetErrorString(he));
+  return HA_OK;
+}
+
+int ha_mnb_destroy(ha_mnb* w) {
+  if (!w) return HA_OK;
+  if (w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
+  if (w->w16) {
+    HA_HIP(hipSetDevice(w->device));
+    HA_HIP(hipDeviceSynchronize());
+    (void)hipFree(w->w16);
+  }
+  w->magic = kDeadMagic;
+  delete w;
+  return HA_OK;
+}
+
+int ha_fwht(void* x, long elems, int n, int device, void* stream) {
+  if (!x || elems <= 0) return fail(HA_ERR_ARG, "x must be non-NULL and elems > 0");
+  HA_HIP(hipSetDevice(device));
+  hipError_t he = ha::launch_fwht(x, elems, n, (hipStream_t)stream);
+  if (he == hipErrorInvalidValue) return fail(HA_ERR_ARG, "n must be a power of two in [2, 8192] dividing elems");
+  HA_HIP(he);
   return HA_OK;
 }
 

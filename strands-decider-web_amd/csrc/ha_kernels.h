@@ -67,6 +67,22 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t s);
 hipError_t launch_gdn_split(const GdnArgs& a, hipStream_t s);  // chunk-parallel preparation + recurrence
 size_t gdn_split_image_bytes();                                // bytes of one chunk image
 hipError_t launch_gqa(const GqaArgs& a, hipStream_t s);
+
+// MatMulNBits projection: y[M][N] (f16) = a[M][K] (f16) x W^T, W in packed blocks of 32 (`bits` u32 words each) with
+// one f16 scale (and, asymmetric, one f16 bias) per `group` values of a row.
+struct MnbArgs {
+  int M, N, K, bits, group, asym;
+  const void* a;  // [M][K] f16
+  void* y;        // [M][N] f16
+  const void* q;  // [N][K/32][bits] u32
+  const void* s;  // [N][K/group] f16
+  const void* b;  // [N][K/group] f16 (asymmetric only)
+};
+hipError_t mnb_check(const MnbArgs& a);
+hipError_t launch_mnb_gemv(const MnbArgs& a, hipStream_t s);  // M <= 64
+hipError_t launch_mnb_dequant(const MnbArgs& a, _Float16* w16, hipStream_t s);
+hipError_t lt_gemm_f16(int device, int M, int N, int K, const void* w16, const void* a, void* y, hipStream_t s);
+hipError_t launch_fwht(void* x, long elems, int n, hipStream_t s);
 hipError_t launch_tail_update(const TailArgs& a, hipStream_t s);
 
 constexpr int kChunk = 64;  // gated-delta chunk length; chunk boundaries sit at s0 + 64k

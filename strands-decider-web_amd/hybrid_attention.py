@@ -38,6 +38,10 @@ class HaConfig(ctypes.Structure):
                 ("rope_theta", ctypes.c_float), ("eps", ctypes.c_float)]
 
 
+class HaMnbFormat(ctypes.Structure):
+    _fields_ = [("bits", ctypes.c_int), ("group", ctypes.c_int), ("asym", ctypes.c_int)]
+
+
 class HaForwardOpts(ctypes.Structure):
     _fields_ = [("recurrence", ctypes.c_int), ("timestamps", ctypes.c_int), ("sync", ctypes.c_int),
                 ("gpu_ms", ctypes.c_float), ("layer_ms", ctypes.POINTER(ctypes.c_float))]
@@ -74,6 +78,10 @@ def load_library(path=LIB_PATH):
         "ha_copy_to_device": ([vp, vp, vp, sz], i),
         "ha_copy_to_host": ([vp, vp, vp, sz], i),
         "ha_synchronize": ([vp], i),
+        "ha_mnb_create": ([i, i, ctypes.POINTER(HaMnbFormat), vp, vp, vp, i, ctypes.POINTER(vp)], i),
+        "ha_mnb_forward": ([vp, i, vp, vp, vp], i),
+        "ha_mnb_destroy": ([vp], i),
+        "ha_fwht": ([vp, ctypes.c_long, i, i, vp], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -203,3 +211,37 @@ class Engine:
                 self._h = None
         except Exception:
             pass
+
+
+class MnbWeight:
+    """A MatMulNBits weight matrix on the GPU (formats of web/public/gemmbench/kernels.js:1-14): ``q`` packed blocks
+    [N][K/32][bits] u32, ``s`` f16 scales [N][K/group], ``b`` f16 biases (asymmetric). The device buffers are the
+    caller's and must stay alive. ``forward(M, a, y)`` computes y[M][N] = a[M][K] x W^T in f16 (engine.js:236-246)."""
+
+    def __init__(self, N, K, q, s, b=None, bits=4, group=32, asym=False, device=0):
+        load_library()
+        self.N, self.K, self.bits, self.group, self.asym = N, K, bits, group, bool(asym)
+        fmt = HaMnbFormat(bits, group, int(bool(asym)))
+        h = ctypes.c_void_p()
+        _check(_lib.ha_mnb_create(N, K, ctypes.byref(fmt), _ptr(q), _ptr(s), _ptr(b), device, ctypes.byref(h)))
+        self._h = h
+
+    def forward(self, M, a, y, stream=None):
+        _check(_lib.ha_mnb_forward(self._h, M, _ptr(a), _ptr(y), _ptr(stream) if stream is not None else None))
+
+    def close(self):
+        if self._h:
+            _check(_lib.ha_mnb_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def fwht(x, elems, n, device=0, stream=None):
+    """In-place orthonormal Walsh-Hadamard transform of each n-block of the f16 device array x (wgsl.js:91-108)."""
+    load_library()
+    _check(_lib.ha_fwht(_ptr(x), elems, n, device, _ptr(stream) if stream is not None else None))
