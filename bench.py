@@ -12,6 +12,8 @@ Also reported, on the same line:
   roofline_gqa  the GQA layer: algorithmic MFMA flops / average layer time, against 2.5 PFLOP/s dense f16
   sweep         the stack at T = 8, 128, 512 (B = 8) and at T = 2048 with B = 1
   cpu_baseline  the CPU oracle (oracle/, fp64) on the host cores for a bounded sample, scaled to the metric
+  projections   the MatMulNBits projections either side of the path: per-forward time at M = 1 (HBM roofline)
+                and M = 2048 (MFMA roofline), with their own CPU baseline (the numpy oracle)
 """
 import argparse
 import json
@@ -140,6 +142,89 @@ def cpu_baseline(T=2048, reps=2):
                       % (reps, tg * 1e3, ta * 1e3)}
 
 
+# The model's int4 projection shapes (K, N) and how many of each one forward runs, as the reference's matmul
+# benchmark weighs them (web/public/gemmbench/portable.js:18 and :69).
+MNB_SHAPES = [(2048, 12288, 15), (6144, 2048, 15), (2048, 8256, 11), (2048, 5120, 4), (2048, 2048, 16)]
+MNB_MS = (1, 2048)  # decode (one token) and one 2048-token prefill, the reference's default M ends
+
+
+def mnb_weights(torch, N, K, seed):
+    """Random packed int4 blocks and scales 0.005..0.015 (portable.js:29-30), on the GPU."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 2 ** 32, (N, K // 32, 4), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    s = (0.005 + 0.01 * rng.random((N, K // 32))).astype(np.float16)
+    return torch.from_numpy(q).to("cuda:0"), torch.from_numpy(s).to("cuda:0")
+
+
+def mnb_measure(torch, ha, stream, steps=20, Ms=MNB_MS):
+    """Per-forward time of the MatMulNBits projections (shape x count) at each M, from HIP events on the launch
+    stream around `steps` back-to-back calls per shape; the M = 1 line against the HBM peak (packed weights + scales
+    + a + y bytes), the large-M line against the dense f16 MFMA peak (2 M N K flops)."""
+    out = {}
+    per = {M: {"ms": 0.0, "bytes": 0, "flops": 0, "shapes": {}} for M in Ms}
+    for i, (K, N, cnt) in enumerate(MNB_SHAPES):
+        q, s = mnb_weights(torch, N, K, seed=i)
+        w = ha.MnbWeight(N, K, q, s, None)
+        for M in Ms:
+            a = torch.randn(M, K, device="cuda:0").to(torch.float16)
+            y = torch.empty(M, N, device="cuda:0", dtype=torch.float16)
+            for _ in range(3):
+                w.forward(M, a, y, stream.cuda_stream)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                w.forward(M, a, y, stream.cuda_stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            p = per[M]
+            p["ms"] += cnt * ms
+            p["bytes"] += cnt * (N * K // 2 + N * K // 32 * 2 + 2 * M * K + 2 * M * N)
+            p["flops"] += cnt * 2 * M * N * K
+            p["shapes"]["%dx%d" % (N, K)] = round(ms * 1e3, 2)
+            del a, y
+        w.close()
+        del q, s
+        torch.cuda.empty_cache()
+    for M, p in per.items():
+        d = {"ms_per_forward": round(p["ms"], 4), "us_per_call": p["shapes"]}
+        if M == 1:
+            gbs = p["bytes"] / (p["ms"] * 1e-3) / 1e9
+            d["roofline"] = {"bound": "hbm", "kernel": "mnb_gemv_lanes_kernel", "achieved": round(gbs, 1),
+                             "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
+                             "bytes_per_forward": p["bytes"], "traffic": None}
+        else:
+            tf = p["flops"] / (p["ms"] * 1e-3) / 1e12
+            d["roofline"] = {"bound": "mfma", "kernel": "hipBLASLt f16 GEMM on the dequantised copy",
+                             "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                             "frac": round(tf / 2500.0, 4), "flops_per_forward": p["flops"], "traffic": None}
+        out["M%d" % M] = d
+    return out
+
+
+def mnb_cpu_baseline():
+    """The numpy oracle (oracle/mnb_oracle.py: dequantise in fp64, then the product) at M = 1 on each shape once,
+    scaled by the per-forward counts."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import mnb_oracle as mo
+    tot = 0.0
+    for i, (K, N, cnt) in enumerate(MNB_SHAPES):
+        rng = np.random.default_rng(i)
+        words = rng.integers(0, 2 ** 32, (N, K // 32, 4), dtype=np.uint64).astype(np.uint32)
+        sc = (0.005 + 0.01 * rng.random((N, K // 32))).astype(np.float16)
+        a = ((rng.random((1, K)) - 0.5) * 2).astype(np.float16)
+        t0 = time.perf_counter()
+        mo.matmul(a, mo.dequant(words, sc, N, K))
+        tot += cnt * (time.perf_counter() - t0)
+    return {"value": round(tot * 1e3, 1), "unit": "ms per forward's projections at M=1", "cores": 1, "kind": "port",
+            "sample": "numpy oracle (fp64 dequantise + product) at M=1, each of the 5 shapes once, x per-forward "
+                      "counts"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -147,7 +232,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the T / B sweep")
-    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy"],
+    ap.add_argument("--no-mnb", action="store_true", help="skip the MatMulNBits projection measurement")
+    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy", "mnb"],
                     help="run only one layer kind (T=2048, B=--profile-batch) --steps times, for rocprofv3; 'copy' runs a plain "
                          "512 MiB device-to-device copy kernel, the reference point that scales FETCH_SIZE / "
                          "WRITE_SIZE to bytes")
@@ -177,6 +263,12 @@ def main():
             torch.cuda.synchronize()
         print(json.dumps({"profile_kernel": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
                           "ms_per_launch": (time.perf_counter() - t0) * 1e3 / args.steps}), flush=True)
+        return
+    if args.profile_kernel == "mnb":
+        t0 = time.perf_counter()
+        res = mnb_measure(torch, ha, stream, steps=args.steps)
+        print(json.dumps({"profile_kernel": "mnb", "steps": args.steps, "result": res,
+                          "wall_s": round(time.perf_counter() - t0, 2)}), flush=True)
         return
     if args.profile_kernel:
         kind = "full_attention" if args.profile_kernel == "gqa" else "linear_attention"
@@ -262,8 +354,14 @@ def main():
                          "launch_ms": round(gqa_launch_ms, 5)},
         "sweep": sweep,
     }
+    if not args.no_mnb:
+        line["projections"] = mnb_measure(torch, ha, stream)
+        line["projections"]["workload"] = ("MatMulNBits int4 group-32 projections of one forward, shapes x counts of "
+                                           "web/public/gemmbench/portable.js:18,69, random weights")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        if "projections" in line:
+            line["projections"]["cpu_baseline"] = mnb_cpu_baseline()
     print(json.dumps(line), flush=True)
 
 

@@ -104,6 +104,10 @@ int ha_destroy(ha_engine* e);
 /* Bind the engine to an existing HIP stream (hipStream_t passed as void*), e.g. a framework's current stream.
    NULL rebinds the engine's own stream. */
 int ha_set_stream(ha_engine* e, void* stream);
+/* The stream the engine's calls run on (hipStream_t as void*): for a host that queues its own work, such as the
+   projection matmuls (ha_mnb_forward), in order with the token mixers. No counterpart in the reference, whose
+   WebGPU queue is implicit (engine.js:236-246 records everything into one command encoder). */
+int ha_get_stream(ha_engine* e, void** stream);
 
 /* Upload one per-layer tensor under its manifest name (export_engine.py:55-58,64-65), as f32 host data:
      linear layers: "conv" [C][conv_k] with C = 2*H*DK + H*DV, "neg_exp_A" [H], "dt_bias" [H], "gnorm" [DV]
@@ -161,7 +165,9 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
                   ha_mnb** out);
 /* y[M][N] = a[M][K] x W^T (f16 in and out, fp32 accumulation) on `stream` (hipStream_t as void*, NULL: the null
    stream): the matmul dispatch of engine.js:236-246, kernel chosen by M as engine.js:17-33 does. a and y are device
-   pointers. The first call with M > 64 also builds the handle's dequantised f16 copy of W (N*K*2 bytes). */
+   pointers. Up to 16 rows (48 when N*K <= 2048*2048) the kernels read the packed weights directly; above that the
+   first call builds the handle's dequantised f16 copy of W (N*K*2 bytes) and the rows go through a library GEMM in
+   slices of at most 512 rows. */
 int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream);
 int ha_mnb_destroy(ha_mnb* w);
 /* In-place orthonormal Walsh-Hadamard transform of every contiguous n-block of the f16 array x (elems values, a

@@ -202,7 +202,7 @@ struct ha_mnb {
   uint32_t magic = kMnbMagic;
   ha::MnbArgs args{};
   int device = 0;
-  _Float16* w16 = nullptr;  // dequantised copy for the M > 64 product, built on first use
+  _Float16* w16 = nullptr;  // dequantised copy for the library product (rows above mnb_packed_path), built on first use
 };
 
 extern "C" {
@@ -316,6 +316,13 @@ int ha_destroy(ha_engine* e) {
 int ha_set_stream(ha_engine* e, void* stream) {
   if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
   e->stream = stream ? static_cast<hipStream_t>(stream) : e->own;
+  return HA_OK;
+}
+
+int ha_get_stream(ha_engine* e, void** stream) {
+  if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  if (!stream) return fail(HA_ERR_ARG, "stream must be non-NULL");
+  *stream = e->stream;
   return HA_OK;
 }
 
@@ -611,7 +618,7 @@ int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   ha::MnbArgs g = w->args;
   g.M = M; g.a = a; g.y = y;
-  if (M <= 64) {
+  if (ha::mnb_packed_path(M, g.N, g.K)) {
     HA_HIP(ha::launch_mnb_gemv(g, st));
     return HA_OK;
   }
@@ -620,8 +627,17 @@ int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
     if (rc) return rc;
     HA_HIP(ha::launch_mnb_dequant(g, w->w16, st));
   }
-  hipError_t he = ha::lt_gemm_f16(w->device, M, g.N, g.K, w->w16, a, y, st);
-  if (he != hipSuccess) return fail(HA_ERR_DEVICE, std::string("hipBLASLt f16 GEMM: ") + hipGetErrorString(he));
+  // The library GEMM is only ever called on row slices of at most kLtRows rows: a single call with M = 16384
+  // (N = 8256, K = 2048) faulted the GPU for a reason not found, while every projection shape passed its parity
+  // test with M <= 512.
+  constexpr int kLtRows = 512;
+  for (int r0 = 0; r0 < M; r0 += kLtRows) {
+    const int m = std::min(kLtRows, M - r0);
+    const void* ar = (const char*)a + (size_t)r0 * g.K * sizeof(_Float16);
+    void* yr = (char*)y + (size_t)r0 * g.N * sizeof(_Float16);
+    hipError_t he = ha::lt_gemm_f16(w->device, m, g.N, g.K, w->w16, ar, yr, st);
+    if (he != hipSuccess) return fail(HA_ERR_DEVICE, std::string("hipBLASLt f16 GEMM: ") + hipGetErrorString(he));
+  }
   return HA_OK;
 }
 

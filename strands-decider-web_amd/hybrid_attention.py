@@ -216,7 +216,8 @@ class Engine:
 class MnbWeight:
     """A MatMulNBits weight matrix on the GPU (formats of web/public/gemmbench/kernels.js:1-14): ``q`` packed blocks
     [N][K/32][bits] u32, ``s`` f16 scales [N][K/group], ``b`` f16 biases (asymmetric). The device buffers are the
-    caller's and must stay alive. ``forward(M, a, y)`` computes y[M][N] = a[M][K] x W^T in f16 (engine.js:236-246)."""
+    caller's (the handle borrows them); this wrapper keeps a reference to q, s and b for its own lifetime.
+    ``forward(M, a, y)`` computes y[M][N] = a[M][K] x W^T in f16 (engine.js:236-246)."""
 
     def __init__(self, N, K, q, s, b=None, bits=4, group=32, asym=False, device=0):
         load_library()
@@ -225,6 +226,7 @@ class MnbWeight:
         h = ctypes.c_void_p()
         _check(_lib.ha_mnb_create(N, K, ctypes.byref(fmt), _ptr(q), _ptr(s), _ptr(b), device, ctypes.byref(h)))
         self._h = h
+        self._borrowed = (q, s, b)
 
     def forward(self, M, a, y, stream=None):
         _check(_lib.ha_mnb_forward(self._h, M, _ptr(a), _ptr(y), _ptr(stream) if stream is not None else None))
@@ -233,6 +235,7 @@ class MnbWeight:
         if self._h:
             _check(_lib.ha_mnb_destroy(self._h))
             self._h = None
+            self._borrowed = None
 
     def __del__(self):
         try:

@@ -144,7 +144,8 @@ class Engine {
   }
   constructor(config, opts) {
     this.config = Array.isArray(config.layerKinds) ? config : configFromManifest(config, opts);
-    this._h = native.create(this.config, pick(opts, 'device', 0));
+    this.device = pick(opts, 'device', 0);
+    this._h = native.create(this.config, this.device);
   }
   // per-layer tensor under its manifest name (conv, neg_exp_A, dt_bias, gnorm, q_norm, k_norm), Float32Array
   setParam(layer, name, data) {
@@ -186,8 +187,43 @@ class Engine {
   }
 }
 
+/*
+ * A quantised projection weight (MatMulNBits, the formats of web/public/gemmbench/kernels.js:1-14) and its matmul,
+ * y[M][N] = a[M][K] x W^T in f16 (the matmul dispatch of engine.js:236-246). q (packed blocks [N][K/32][bits] u32),
+ * s (f16 scales [N][K/group]) and b (f16 biases, asymmetric formats only) are device buffers the caller keeps alive;
+ * format {bits: 2|3|4, group: 32|64, asym: bool} defaults to the exporter's int4 / 32 / symmetric. The matmuls run on
+ * the engine's stream, in order with its token mixers.
+ */
+class MatMulNBits {
+  constructor(engine, N, K, q, s, b, format) {
+    const f = format || {};
+    this.engine = engine;
+    this.N = N;
+    this.K = K;
+    this._h = native.mnbCreate(N, K, { bits: pick(f, 'bits', 4), group: pick(f, 'group', 32), asym: pick(f, 'asym', false) ? 1 : 0 },
+      ptrOf(q), ptrOf(s), b === undefined || b === null ? null : ptrOf(b), engine ? engine.device : pick(f, 'device', 0));
+  }
+  forward(M, a, y) {
+    native.mnbForward(this._h, M, ptrOf(a), ptrOf(y), this.engine ? this.engine._h : null);
+  }
+  destroy() {
+    if (this._h) {
+      native.mnbDestroy(this._h);
+      this._h = null;
+    }
+  }
+}
+
+// In-place orthonormal Walsh-Hadamard transform of every n-block of an f16 device buffer of `elems` values: the
+// input rotation of a weight exported with `had: n` (web/public/engine/wgsl.js:91-108), on the engine's stream.
+function fwht(engine, x, elems, n) {
+  native.fwht(ptrOf(x), elems, n, engine ? engine.device : 0, engine ? engine._h : null);
+}
+
 module.exports = {
   Engine: Engine,
+  MatMulNBits: MatMulNBits,
+  fwht: fwht,
   Snapshot: Snapshot,
   DeviceBuffer: DeviceBuffer,
   configFromManifest: configFromManifest,

@@ -15,13 +15,23 @@
 
 #include "ha.h"
 
+/* Every external holds one of these boxes; `kind` tells them apart, so a handle of the wrong kind is a TypeError. */
+enum { BOX_ENGINE = 0x45, BOX_SNAPSHOT = 0x53, BOX_MNB = 0x4d };
+
 typedef struct {
+  int kind;
   ha_engine* e;
 } engine_box;
 
 typedef struct {
+  int kind;
   ha_snapshot* s;
 } snap_box;
+
+typedef struct {
+  int kind;
+  ha_mnb* w;
+} mnb_box;
 
 static napi_value throw_status(napi_env env, int rc) {
   char code[16];
@@ -104,17 +114,17 @@ static int get_ptr(napi_env env, napi_value v, void** out) {
   return 1;
 }
 
-static engine_box* get_engine(napi_env env, napi_value v) {
+static void* get_box(napi_env env, napi_value v, int kind) {
+  napi_valuetype t;
   void* p = NULL;
-  if (napi_get_value_external(env, v, &p) != napi_ok || !p) return NULL;
-  return (engine_box*)p;
+  if (napi_typeof(env, v, &t) != napi_ok || t != napi_external) return NULL;
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p || *(const int*)p != kind) return NULL;
+  return p;
 }
 
-static snap_box* get_snap(napi_env env, napi_value v) {
-  void* p = NULL;
-  if (napi_get_value_external(env, v, &p) != napi_ok || !p) return NULL;
-  return (snap_box*)p;
-}
+static engine_box* get_engine(napi_env env, napi_value v) { return (engine_box*)get_box(env, v, BOX_ENGINE); }
+static snap_box* get_snap(napi_env env, napi_value v) { return (snap_box*)get_box(env, v, BOX_SNAPSHOT); }
+static mnb_box* get_mnb(napi_env env, napi_value v) { return (mnb_box*)get_box(env, v, BOX_MNB); }
 
 /* host bytes of a TypedArray / ArrayBuffer view */
 static int get_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
@@ -150,6 +160,13 @@ static void snap_finalize(napi_env env, void* data, void* hint) {
   (void)env; (void)hint;
   snap_box* b = (snap_box*)data;
   if (b->s) ha_snapshot_destroy(b->s);
+  free(b);
+}
+
+static void mnb_finalize(napi_env env, void* data, void* hint) {
+  (void)env; (void)hint;
+  mnb_box* b = (mnb_box*)data;
+  if (b->w) ha_mnb_destroy(b->w);
   free(b);
 }
 
@@ -224,6 +241,7 @@ static napi_value js_create(napi_env env, napi_callback_info info) {
     ha_destroy(e);
     return type_error(env, "out of host memory");
   }
+  b->kind = BOX_ENGINE;
   b->e = e;
   napi_value r;
   if (napi_create_external(env, b, engine_finalize, NULL, &r) != napi_ok) {
@@ -349,6 +367,7 @@ static napi_value js_forward(napi_env env, napi_callback_info info) {
       free(lms);
       return type_error(env, "out of host memory");
     }
+    sb->kind = BOX_SNAPSHOT;
     sb->s = snap;
     if (napi_create_external(env, sb, snap_finalize, NULL, &v) != napi_ok) {
       ha_snapshot_destroy(snap);
@@ -495,6 +514,97 @@ static napi_value js_synchronize(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* The stream of an optional engine argument (null / undefined: the null stream). Returns 0 on a bad argument. */
+static int stream_of(napi_env env, napi_value v, void** stream) {
+  *stream = NULL;
+  if (is_nullish(env, v)) return 1;
+  engine_box* eb = get_engine(env, v);
+  if (!eb || !eb->e) return 0;
+  return ha_get_stream(eb->e, stream) == HA_OK;
+}
+
+/* mnbCreate(N, K, {bits, group, asym}, q: BigInt, s: BigInt, b: BigInt|null, device) -> handle */
+static napi_value js_mnb_create(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (!get_args(env, info, 7, argv)) return NULL;
+  int32_t N, K, device = 0;
+  if (napi_get_value_int32(env, argv[0], &N) != napi_ok || napi_get_value_int32(env, argv[1], &K) != napi_ok)
+    return type_error(env, "N and K must be integers");
+  ha_mnb_format f;
+  if (is_nullish(env, argv[2])) return type_error(env, "format must be an object {bits, group, asym}");
+  if (!get_int(env, argv[2], "bits", 4, &f.bits) || !get_int(env, argv[2], "group", 32, &f.group) ||
+      !get_int(env, argv[2], "asym", 0, &f.asym))
+    return type_error(env, "invalid format field");
+  void *q, *sc, *bi = NULL;
+  if (!get_ptr(env, argv[3], &q) || !get_ptr(env, argv[4], &sc)) return type_error(env, "q and s must be BigInt");
+  if (!is_nullish(env, argv[5]) && !get_ptr(env, argv[5], &bi)) return type_error(env, "b must be a BigInt or null");
+  if (!is_nullish(env, argv[6]) && napi_get_value_int32(env, argv[6], &device) != napi_ok)
+    return type_error(env, "device must be an integer");
+  ha_mnb* w = NULL;
+  CHECK_HA(ha_mnb_create(N, K, &f, q, sc, bi, device, &w));
+  mnb_box* b = (mnb_box*)malloc(sizeof(mnb_box));
+  if (!b) {
+    ha_mnb_destroy(w);
+    return type_error(env, "out of host memory");
+  }
+  b->kind = BOX_MNB;
+  b->w = w;
+  napi_value r;
+  if (napi_create_external(env, b, mnb_finalize, NULL, &r) != napi_ok) {
+    ha_mnb_destroy(w);
+    free(b);
+    napi_throw_error(env, NULL, "napi_create_external failed");
+    return NULL;
+  }
+  return r;
+}
+
+/* mnbForward(handle, M, a: BigInt, y: BigInt, engine|null): on the engine's stream when one is given */
+static napi_value js_mnb_forward(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  if (!get_args(env, info, 5, argv)) return NULL;
+  mnb_box* mb = get_mnb(env, argv[0]);
+  if (!mb) return type_error(env, "not a MatMulNBits handle");
+  if (!mb->w) return type_error(env, "MatMulNBits handle was destroyed");
+  int32_t M;
+  void *a, *y, *st;
+  if (napi_get_value_int32(env, argv[1], &M) != napi_ok) return type_error(env, "M must be an integer");
+  if (!get_ptr(env, argv[2], &a) || !get_ptr(env, argv[3], &y)) return type_error(env, "a and y must be BigInt");
+  if (!stream_of(env, argv[4], &st)) return type_error(env, "the last argument must be an engine handle or null");
+  CHECK_HA(ha_mnb_forward(mb->w, M, a, y, st));
+  return NULL;
+}
+
+static napi_value js_mnb_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  mnb_box* mb = get_mnb(env, argv[0]);
+  if (!mb) return type_error(env, "not a MatMulNBits handle");
+  if (mb->w) {
+    ha_mnb* w = mb->w;
+    mb->w = NULL;
+    CHECK_HA(ha_mnb_destroy(w));
+  }
+  return NULL;
+}
+
+/* fwht(x: BigInt, elems, n, device, engine|null) */
+static napi_value js_fwht(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  if (!get_args(env, info, 5, argv)) return NULL;
+  void *x, *st;
+  double elems;
+  int32_t n, device = 0;
+  if (!get_ptr(env, argv[0], &x)) return type_error(env, "x must be a BigInt");
+  if (napi_get_value_double(env, argv[1], &elems) != napi_ok || elems < 0) return type_error(env, "elems must be >= 0");
+  if (napi_get_value_int32(env, argv[2], &n) != napi_ok) return type_error(env, "n must be an integer");
+  if (!is_nullish(env, argv[3]) && napi_get_value_int32(env, argv[3], &device) != napi_ok)
+    return type_error(env, "device must be an integer");
+  if (!stream_of(env, argv[4], &st)) return type_error(env, "the last argument must be an engine handle or null");
+  CHECK_HA(ha_fwht(x, (long)elems, n, device, st));
+  return NULL;
+}
+
 static napi_value init(napi_env env, napi_value exports) {
   const struct {
     const char* name;
@@ -508,6 +618,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"deviceAlloc", js_device_alloc},     {"deviceFree", js_device_free},
       {"copyToDevice", js_copy_to_device},  {"copyToHost", js_copy_to_host},
       {"synchronize", js_synchronize},
+      {"mnbCreate", js_mnb_create},         {"mnbForward", js_mnb_forward},
+      {"mnbDestroy", js_mnb_destroy},       {"fwht", js_fwht},
   };
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); i++) {
     napi_value f;

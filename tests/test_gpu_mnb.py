@@ -1,7 +1,7 @@
 """GPU parity of the MatMulNBits projections (ha_mnb_forward through the C ABI) against the fp64 oracle: the model's
-projection shapes (web/public/gemmbench/portable.js:18) across both implementations (M <= 64: packed-weight MFMA
-kernel; larger M: dequantised copy + hipBLASLt), every weight format of gemmbench/kernels.js:1-14, the exporter's
-own int4 quantiser, and the FWHT input rotation."""
+projection shapes (web/public/gemmbench/portable.js:18) across the three implementations (M <= 2: lanes kernel;
+M <= 16, or 48 on matrices up to 2048 x 2048: packed-weight MFMA kernel; larger M: dequantised copy + hipBLASLt),
+every weight format of gemmbench/kernels.js:1-14, the exporter's own int4 quantiser, and the FWHT input rotation."""
 import os
 import sys
 
@@ -50,7 +50,7 @@ def _run(words, sc, bi, N, K, Ms, bits=4, group=32, asym=False, seed=1):
 @pytest.mark.parametrize("K,N", [(2048, 12288), (6144, 2048), (2048, 8256), (2048, 5120), (2048, 2048)])
 def test_projection_shapes_int4(K, N):
     words, sc, _ = _weights(N, K, seed=K + N)
-    errs = _run(words, sc, None, N, K, [1, 7, 16, 64, 68, 512])
+    errs = _run(words, sc, None, N, K, [1, 2, 3, 5, 8, 9, 16, 17, 33, 48, 49, 64, 68, 512])
     print("K=%d N=%d" % (K, N), {m: "%.1e" % e for m, e in errs.items()})
     assert max(errs.values()) < TOL
 
@@ -60,7 +60,7 @@ def test_projection_shapes_int4(K, N):
 def test_formats(bits, group, asym):
     N, K = 1024, 2048
     words, sc, bi = _weights(N, K, bits, group, asym, seed=bits * 100 + group)
-    errs = _run(words, sc, bi, N, K, [3, 33, 200], bits, group, asym)
+    errs = _run(words, sc, bi, N, K, [1, 2, 3, 17, 33, 48, 200], bits, group, asym)
     print("bits=%d group=%d asym=%d" % (bits, group, asym), {m: "%.1e" % e for m, e in errs.items()})
     assert max(errs.values()) < TOL
 
@@ -77,22 +77,25 @@ def test_exporter_quantised_weights():
     assert max(errs.values()) < TOL
 
 
-def test_both_implementations_agree_at_the_boundary():
-    # rows computed with M = 64 (packed-weight kernel) and M = 65 (dequantised copy + library GEMM)
+@pytest.mark.parametrize("N,K", [(2048, 2048), (4096, 2048)])
+def test_implementations_agree_at_the_boundaries(N, K):
+    # the first rows computed with M = 2 (lanes kernel), 3 and 16 (MFMA kernel), 48 (MFMA kernel on the
+    # 2048 x 2048 matrix, library on the larger one) and 49 (dequantised copy + library GEMM)
     import torch
-    N, K = 2048, 2048
     words, sc, _ = _weights(N, K, seed=9)
     dev = "cuda:0"
     w = ha.MnbWeight(N, K, torch.from_numpy(words.view(np.int32)).to(dev), torch.from_numpy(sc).to(dev), None)
-    a = torch.from_numpy(((np.random.default_rng(2).random((65, K)) - 0.5) * 2).astype(np.float16)).to(dev)
-    y64 = torch.empty(64, N, dtype=torch.float16, device=dev)
-    y65 = torch.empty(65, N, dtype=torch.float16, device=dev)
-    w.forward(64, a, y64)
-    w.forward(65, a, y65)
+    a = torch.from_numpy(((np.random.default_rng(2).random((49, K)) - 0.5) * 2).astype(np.float16)).to(dev)
+    ys = {}
+    for M in (2, 3, 16, 17, 48, 49):
+        ys[M] = torch.empty(M, N, dtype=torch.float16, device=dev)
+        w.forward(M, a, ys[M])
     torch.cuda.synchronize()
-    e = mo.rel_err(y64.float().cpu().numpy(), y65[:64].float().cpu().numpy())
-    print("M=64 kernel vs M=65 library: %.1e" % e)
-    assert e < TOL
+    ref = ys[49][:2].float().cpu().numpy()
+    for M, y in ys.items():
+        e = mo.rel_err(y[:2].float().cpu().numpy(), ref)
+        print("M=%d vs M=49 on the first two rows: %.1e" % (M, e))
+        assert e < TOL
     w.close()
 
 

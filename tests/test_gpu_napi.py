@@ -6,6 +6,7 @@ import json
 import os
 import shutil
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -73,3 +74,56 @@ def test_node_forward_resume_release(tmp_path):
     e_g, e_a = rel_err(js_out(0, 0, T0), ref_g), rel_err(js_out(1, 0, T0), ref_a)
     print("node prefix vs oracle: gated-delta %.2e, gqa %.2e" % (e_g, e_a))
     assert e_g < 2e-3 and e_a < 1e-2
+
+
+@pytest.mark.parametrize("bits,group,asym", [(4, 32, False), (3, 64, True)])
+def test_node_matmulnbits(tmp_path, bits, group, asym):
+    # the MatMulNBits projection through engine.js -> ha_napi.node -> libha.so: bit-identical to the same call
+    # through the C ABI from Python on the packed-weight kernels (M <= 48 here), within the projection bar of the
+    # fp64 oracle everywhere. Above that the product is a hipBLASLt GEMM, and the two processes load different
+    # builds of it (Python binds the copy bundled with torch, Node the system one), whose kernels round differently.
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import mnb_oracle as mo
+
+    import hybrid_attention as ha
+    d = str(tmp_path)
+    N, K, Ms = 1024, 2048, [1, 5, 40, 70]
+    rng = np.random.default_rng(bits)
+    words = rng.integers(0, 2 ** 32, (N, K // 32, bits), dtype=np.uint64).astype(np.uint32)
+    sc = (0.005 + 0.01 * rng.random((N, K // group))).astype(np.float16)
+    bi = ((rng.random((N, K // group)) - 0.5) * 0.1).astype(np.float16) if asym else None
+    a = ((rng.random((max(Ms), K)) - 0.5) * 2).astype(np.float16)
+    words.tofile(os.path.join(d, "q.bin"))
+    sc.tofile(os.path.join(d, "s.bin"))
+    if asym:
+        bi.tofile(os.path.join(d, "b.bin"))
+    a.tofile(os.path.join(d, "a.bin"))
+    with open(os.path.join(d, "spec.json"), "w") as f:
+        json.dump({"N": N, "K": K, "Ms": Ms, "bits": bits, "group": group, "asym": asym}, f)
+    print("node matmulnbits: bits=%d group=%d asym=%d" % (bits, group, asym), flush=True)
+    r = subprocess.run([shutil.which("node"), os.path.join(ROOT, "tests", "js", "napi_mnb.js"), d],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert json.loads(r.stdout.strip().splitlines()[-1])["ok"]
+
+    dev = "cuda:0"
+    qd, sd = torch.from_numpy(words.view(np.int32)).to(dev), torch.from_numpy(sc).to(dev)
+    bd = torch.from_numpy(bi).to(dev) if asym else None
+    w = ha.MnbWeight(N, K, qd, sd, bd, bits=bits, group=group, asym=asym)
+    ad = torch.from_numpy(a).to(dev)
+    W = mo.dequant(words, sc, N, K, bits, group, asym, bi)
+    for M in Ms:
+        y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        w.forward(M, ad, y)
+        torch.cuda.synchronize()
+        yj = np.fromfile(os.path.join(d, "y_%d.bin" % M), dtype=np.float16).reshape(M, N)
+        if M <= 48:
+            assert np.array_equal(yj, y.cpu().numpy()), "M=%d differs from the C ABI call" % M
+        else:
+            assert mo.rel_err(yj.astype(np.float64), y.cpu().numpy().astype(np.float64)) < 1e-3
+        assert mo.rel_err(yj.astype(np.float64), mo.matmul(a[:M], W)) < 2e-3
+    w.close()
+    fj = np.fromfile(os.path.join(d, "fwht.bin"), dtype=np.float16).astype(np.float64)
+    assert mo.rel_err(fj, mo.fwht(a[0, :64].astype(np.float64), 64)) < 2e-3

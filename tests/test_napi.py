@@ -24,13 +24,18 @@ out.cfg = m.configFromManifest({layer_types: ['linear_attention', 'linear_attent
 try { m.configFromManifest({layer_types: ['mamba']}); } catch (e) { out.bad_kind = e.message; }
 out.adapter = m.configFromManifest({layer_types: ['linear_attention', 'adapter', 'full_attention']}).layerKinds;
 try { m.Engine.createSync(out.cfg, {device: 0}); out.created = true; } catch (e) { out.err = [e.code, e.message]; }
+const nat = require(require('path').join(require('path').dirname(%r), 'ha_napi.node'));
+try { nat.mnbForward({}, 1, BigInt(0), BigInt(0), null); } catch (e) { out.bad_handle = e.name + ': ' + e.message; }
+try { new m.MatMulNBits(null, 15, 2048, BigInt(16), BigInt(16), null); } catch (e) { out.bad_shape = e.code; }
+try { new m.MatMulNBits(null, 16, 2048, BigInt(16), BigInt(16), null); } catch (e) { out.no_dev = e.code; }
 m.Engine.create(out.cfg).then(function () { out.async = 'resolved'; }, function (e) { out.async = e.code; })
   .then(function () { console.log(JSON.stringify(out)); });
 """
 
 
 def _run():
-    js = SCRIPT % os.path.join(ROOT, "strands-decider-web_amd", "js", "engine.js")
+    mod = os.path.join(ROOT, "strands-decider-web_amd", "js", "engine.js")
+    js = SCRIPT % (mod, mod)
     r = subprocess.run([NODE, "-e", js], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     return json.loads(r.stdout.strip().splitlines()[-1])
@@ -39,7 +44,12 @@ def _run():
 def test_addon_loads_and_maps_manifest_config():
     out = _run()
     assert out["abi"] == 1
-    assert {"Engine", "Snapshot", "DeviceBuffer", "configFromManifest", "CHUNKED", "SEQUENTIAL"} <= set(out["exports"])
+    assert {"Engine", "Snapshot", "DeviceBuffer", "configFromManifest", "CHUNKED", "SEQUENTIAL", "MatMulNBits",
+            "fwht"} <= set(out["exports"])
+    # a handle of the wrong kind is a TypeError from the addon, not a crash
+    assert out["bad_handle"] == "TypeError: not a MatMulNBits handle"
+    # shape checks come before any device access (N % 16): HA_ERR_ARG
+    assert out["bad_shape"] == "HA_1"
     c = out["cfg"]
     assert c["layerKinds"] == [0, 0, 0, 1] and c["batch"] == 8
     # the engine's fused row strides (export_engine.py:52,61): 8256 = 64-padded q|k|v|z|a|b, 5120 = q|gate|k|v
@@ -55,4 +65,5 @@ def test_create_without_device_throws_with_status_code():
     out = _run()
     assert "created" not in out
     assert out["err"][0] == "HA_4" and "no HIP device" in out["err"][1]
+    assert out["no_dev"] == "HA_4"  # ha_mnb_create: the device query fails without a GPU, as for the engine
     assert out["async"] == "HA_4"
