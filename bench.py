@@ -197,7 +197,7 @@ def mnb_measure(torch, ha, stream, steps=20, Ms=MNB_MS):
                              "bytes_per_forward": p["bytes"], "traffic": None}
         else:
             tf = p["flops"] / (p["ms"] * 1e-3) / 1e12
-            d["roofline"] = {"bound": "mfma", "kernel": "hipBLASLt f16 GEMM on the dequantised copy",
+            d["roofline"] = {"bound": "mfma", "kernel": "mnb_gemm_kernel",
                              "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
                              "frac": round(tf / 2500.0, 4), "flops_per_forward": p["flops"], "traffic": None}
         out["M%d" % M] = d

@@ -202,7 +202,6 @@ struct ha_mnb {
   uint32_t magic = kMnbMagic;
   ha::MnbArgs args{};
   int device = 0;
-  _Float16* w16 = nullptr;  // dequantised copy for the library product (rows above mnb_packed_path), built on first use
 };
 
 extern "C" {
@@ -622,34 +621,14 @@ int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
     HA_HIP(ha::launch_mnb_gemv(g, st));
     return HA_OK;
   }
-  if (!w->w16) {
-    int rc = dalloc(&w->w16, sizeof(_Float16) * (size_t)g.N * g.K);
-    if (rc) return rc;
-    HA_HIP(ha::launch_mnb_dequant(g, w->w16, st));
-  }
-  // The library GEMM is only ever called on row slices of at most kLtRows rows: a single call with M = 16384
-  // (N = 8256, K = 2048) faulted the GPU for a reason not found, while every projection shape passed its parity
-  // test with M <= 512.
-  constexpr int kLtRows = 512;
-  for (int r0 = 0; r0 < M; r0 += kLtRows) {
-    const int m = std::min(kLtRows, M - r0);
-    const void* ar = (const char*)a + (size_t)r0 * g.K * sizeof(_Float16);
-    void* yr = (char*)y + (size_t)r0 * g.N * sizeof(_Float16);
-    hipError_t he = ha::lt_gemm_f16(w->device, m, g.N, g.K, w->w16, ar, yr, st);
-    if (he != hipSuccess) return fail(HA_ERR_DEVICE, std::string("hipBLASLt f16 GEMM: ") + hipGetErrorString(he));
-  }
+  HA_HIP(ha::launch_mnb_gemm(g, st));
   return HA_OK;
 }
 
 int ha_mnb_destroy(ha_mnb* w) {
   if (!w) return HA_OK;
   if (w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
-  if (w->w16) {
-    HA_HIP(hipSetDevice(w->device));
-    HA_HIP(hipDeviceSynchronize());
-    (void)hipFree(w->w16);
-  }
-  w->magic = kDeadMagic;
+  w->magic = kDeadMagic;  // the handle owns no device memory; kernels in flight took its arguments by value
   delete w;
   return HA_OK;
 }

@@ -81,8 +81,7 @@ struct MnbArgs {
 hipError_t mnb_check(const MnbArgs& a);
 bool mnb_packed_path(int M, int N, int K);  // whether launch_mnb_gemv (packed weights) serves M rows
 hipError_t launch_mnb_gemv(const MnbArgs& a, hipStream_t s);  // M <= 64 (mnb_packed_path picks up to 48)
-hipError_t launch_mnb_dequant(const MnbArgs& a, _Float16* w16, hipStream_t s);
-hipError_t lt_gemm_f16(int device, int M, int N, int K, const void* w16, const void* a, void* y, hipStream_t s);
+hipError_t launch_mnb_gemm(const MnbArgs& a, hipStream_t s);  // any M: tiled GEMM, weights dequantised into LDS
 hipError_t launch_fwht(void* x, long elems, int n, hipStream_t s);
 hipError_t launch_tail_update(const TailArgs& a, hipStream_t s);
 

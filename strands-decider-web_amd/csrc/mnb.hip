@@ -17,18 +17,13 @@
 //            K blocks; each lane dequantises a whole packed block into the f16 B operands of
 //            v_mfma_f32_16x16x32_f16 (no LDS), the a rows are the A operand (16 rows per tile, up to 4 tiles share
 //            each dequantised operand), and the waves' partial sums meet in LDS.
-//   above    compute bound: the weights are dequantised once (mnb_dequant_kernel) into an f16 copy the handle
-//            keeps, and the product is a plain f16 GEMM with fp32 accumulation through hipBLASLt, on row slices of
-//            at most 512 rows (the host side slices).
+//   above    mnb_gemm_kernel: compute bound. A tiled MFMA GEMM (128 x 128 workgroup tiles) whose weight tiles are
+//            dequantised on their way into LDS, so the weights stay packed in HBM.
 // All three dequantise with the same f16 arithmetic (dequant8_pk: each weight rounded to f16 once), accumulate in
-// fp32 and round the output to f16.
+// fp32 and round the output to f16. None splits K across workgroups, so results are deterministic.
 #include <hip/hip_runtime.h>
-#include <hipblaslt/hipblaslt.h>
 
 #include <cmath>
-#include <map>
-#include <mutex>
-#include <tuple>
 
 #include "ha_kernels.h"
 
@@ -89,29 +84,6 @@ __device__ __forceinline__ h8 perm8(h8 x) {
 }
 
 __device__ __forceinline__ h2 splat2(_Float16 v) { return h2{v, v}; }
-
-// W16[n][k] = dequantised W, one 32-element block per thread.
-template <int BITS, int GROUP, bool ASYM>
-__global__ __launch_bounds__(256) void mnb_dequant_kernel(MnbArgs a, _Float16* w16) {
-  const int nblk = a.K / kBlk;
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (long)a.N * nblk) return;
-  const long n = i / nblk;
-  const int b = (int)(i % nblk);
-  const long gi = n * (a.K / GROUP) + (long)b * kBlk / GROUP;
-  const h2 sc = splat2(gp<_Float16>(a.s)[gi]);
-  const h2 bi = splat2(ASYM ? gp<_Float16>(a.b)[gi] : (_Float16)0.0f);
-  gptr<unsigned> wp = gp<unsigned>(a.q) + i * BITS;
-  unsigned wd[BITS];
-#pragma unroll
-  for (int j = 0; j < BITS; j++) wd[j] = wp[j];
-  __attribute__((address_space(1))) h8* dst = (__attribute__((address_space(1))) h8*)(w16 + n * a.K + (long)b * kBlk);
-#pragma unroll
-  for (int g = 0; g < 4; g++) {
-    const h8 v = dequant8_pk<BITS, ASYM>(wd, g, sc, bi);
-    dst[g] = h8{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]};
-  }
-}
 
 // y for M <= 16 MT rows. Workgroup: kGW waves, output columns 16 blockIdx.x .. +15; the K blocks go in groups of
 // four, wave w taking groups w, w + kGW, ... Lane (g = lane / 16, c = lane % 16) loads the whole packed block b0 + g
@@ -248,6 +220,128 @@ __global__ __launch_bounds__(256) void mnb_gemv_lanes_kernel(MnbArgs a) {
     }
 }
 
+// y for larger M: a tiled f16 GEMM whose weight tiles are dequantised on the way into LDS, so the weights are read
+// packed (0.5 byte per weight for 4 bits) and no f16 copy exists. Workgroup tile 128 or 256 rows (the larger when
+// there are enough tiles: each dequantised weight then serves twice the rows) x 128 columns, k tiles of
+// 64 (two packed blocks); 4 waves (8 for 256-row tiles), wave (wm, wn) = (w / 2, w % 2) owns rows 64 wm .. + 63 and
+// columns 64 wn .. + 63
+// as 2 x 2 tiles of v_mfma_f32_32x32x16_f16 (A operand lane l: row l % 32 of a, k 8 (l / 32) .. + 7 of the
+// 16-step; B operand: column l % 32, the same k; D: column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4).
+// The a tile and the dequantised weight tile are double-buffered in LDS (row pitch 72 halves). Each thread keeps
+// the global loads of the next kDepth tiles in flight in a register ring (per tile 64 bytes of one a row, one packed
+// block of one column and its scale); after multiplying tile kt it writes tile kt + 1, dequantised, into the other
+// buffer and issues the loads of tile kt + 1 + kDepth; one barrier per k tile. Rows past M and columns past N load clamped rows and are not stored; a k tile past the last
+// block (K % 64 == 32) is zero in both operands. Tiles are numbered so that each XCD (workgroup id % 8) takes a
+// contiguous range of them, n fastest, sharing a rows in its L2.
+constexpr int kTN = 128, kTK = 64, kPitch = kTK + 8, kDepth = 4;
+typedef float f16v __attribute__((ext_vector_type(16)));
+template <int BITS, int GROUP, bool ASYM, int WMW>
+__global__ __launch_bounds__(128 * WMW) void mnb_gemm_kernel(MnbArgs a) {
+  constexpr int kTM = 64 * WMW;                 // WMW wave rows of 64 a rows, 2 wave columns of 64 weight columns
+  constexpr int kSPT = 8 / WMW;                 // dequantised 8-element slices per thread and k tile
+  constexpr int kTPB = 4 / kSPT;                // threads per packed block
+  __shared__ _Float16 As[2][kTM * kPitch];
+  __shared__ _Float16 Bs[2][kTN * kPitch];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, wm = w >> 1, wn = w & 1;
+  const int ntn = (a.N + kTN - 1) / kTN, ntm = (a.M + kTM - 1) / kTM, ntiles = ntn * ntm;
+  int id = blockIdx.x;
+  if (ntiles % 8 == 0) id = (id % 8) * (ntiles / 8) + id / 8;
+  const int tn = id % ntn, tm = id / ntn;
+  const int nblk = a.K / kBlk, nkt = (nblk + 1) / 2, ng = a.K / GROUP;
+  // this thread's loads: a row tm * kTM + tid / 2, k half tid % 2; weight column tn * 128 + bc, block half bh,
+  // slices s0 .. s0 + kSPT - 1 of the block
+  const int lr = tid >> 1, lh = tid & 1;
+  const int bc = tid / (2 * kTPB), bh = (tid / kTPB) & 1, s0 = (tid % kTPB) * kSPT;
+  const int arow = min(tm * kTM + lr, a.M - 1), wcol = min(tn * kTN + bc, a.N - 1);
+  gptr<h8> ap = (gptr<h8>)(gp<_Float16>(a.a) + (size_t)arow * a.K);  // 4 h8 per block
+  gptr<unsigned> wp = gp<unsigned>(a.q) + (size_t)wcol * nblk * BITS;
+  gptr<unsigned short> sp = gp<unsigned short>(a.s) + (size_t)wcol * ng;
+  gptr<unsigned short> bp = ASYM ? gp<unsigned short>(a.b) + (size_t)wcol * ng : sp;
+  // ring of kDepth tiles in flight: tile t's loads live in slot t % kDepth
+  h8 ar[kDepth][4];
+  unsigned wr[kDepth][BITS];
+  unsigned short sr[kDepth], br[kDepth];  // f16 bits, loaded zero-extended into whole registers
+  auto load = [&](int kt, int r) {
+    const int b = min(2 * kt + lh, nblk - 1), bb = min(2 * kt + bh, nblk - 1);
+#pragma unroll
+    for (int j = 0; j < 4; j++) ar[r][j] = ap[4 * b + j];
+#pragma unroll
+    for (int j = 0; j < BITS; j++) wr[r][j] = wp[bb * BITS + j];
+    sr[r] = sp[bb * kBlk / GROUP];
+    br[r] = ASYM ? bp[bb * kBlk / GROUP] : (unsigned short)0;
+  };
+  auto store = [&](int kt, int r, int buf) {
+    const bool oka = 2 * kt + lh < nblk, okb = 2 * kt + bh < nblk;
+    _Float16* ad = &As[buf][lr * kPitch + 32 * lh];
+    _Float16* bd = &Bs[buf][bc * kPitch + 32 * bh];
+    const h2 sc = splat2(__builtin_bit_cast(_Float16, sr[r])), bi = splat2(__builtin_bit_cast(_Float16, br[r]));
+#pragma unroll
+    for (int j = 0; j < 4; j++) *reinterpret_cast<h8*>(ad + 8 * j) = oka ? ar[r][j] : h8{};
+#pragma unroll
+    for (int j = s0; j < s0 + kSPT; j++) {
+      const h8 v = dequant8_pk<BITS, ASYM>(wr[r], j, sc, bi);
+      *reinterpret_cast<h8*>(bd + 8 * j) = okb ? h8{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]} : h8{};
+    }
+  };
+  f16v acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = f16v{};
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
+  auto compute = [&](int buf) {
+    const _Float16* A0 = &As[buf][(64 * wm + fr) * kPitch + fk];
+    const _Float16* B0 = &Bs[buf][(64 * wn + fr) * kPitch + fk];
+#pragma unroll
+    for (int ks = 0; ks < kTK / 16; ks++) {
+      h8 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        af[i] = *reinterpret_cast<const h8*>(A0 + 32 * i * kPitch + 16 * ks);
+        bf[i] = *reinterpret_cast<const h8*>(B0 + 32 * i * kPitch + 16 * ks);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  // prologue: tile 0 into LDS buffer 0, tiles 1 .. kDepth in flight (loads past the last tile read clamped blocks)
+  load(0, 0);
+  store(0, 0, 0);
+#pragma unroll
+  for (int t = 1; t <= kDepth; t++) load(t, t % kDepth);
+  __syncthreads();
+  // iteration kt: multiply tile kt; write tile kt + 1 (slot (kt + 1) % kDepth) into the other buffer; refill that
+  // slot with tile kt + 1 + kDepth. Unrolled by kDepth so every slot index is a constant, and run to a multiple of
+  // kDepth tiles with no branch inside (tiles past the last block are zero in LDS and add nothing), so the compiler
+  // waits for one tile's loads at a time and never for the whole ring.
+  const int nkt_pad = (nkt + kDepth - 1) / kDepth * kDepth;
+  for (int k0 = 0; k0 < nkt_pad; k0 += kDepth) {
+#pragma unroll
+    for (int r = 0; r < kDepth; r++) {
+      const int kt = k0 + r;
+      compute(kt & 1);
+      const int slot = (r + 1) % kDepth;
+      store(kt + 1, slot, (kt + 1) & 1);
+      load(kt + 1 + kDepth, slot);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int n = tn * kTN + 64 * wn + 32 * j + fr;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = tm * kTM + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (m < a.M) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)acc[i][j][v];
+      }
+    }
+}
+
 // In-place orthonormal Walsh-Hadamard transform (Sylvester order) of each contiguous n-block of an f16 row, one
 // workgroup per block (wgsl.js:91-108): the online input rotation of a tensor exported with `had: n`.
 __global__ __launch_bounds__(256) void fwht_kernel(_Float16* x, int n, float scale) {
@@ -288,9 +382,14 @@ hipError_t launch_gemv(const MnbArgs& a, hipStream_t s) {
 }
 
 template <int BITS, int GROUP, bool ASYM>
-hipError_t launch_dequant(const MnbArgs& a, _Float16* w16, hipStream_t s) {
-  const long n = (long)a.N * (a.K / kBlk);
-  hipLaunchKernelGGL((mnb_dequant_kernel<BITS, GROUP, ASYM>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, w16);
+hipError_t launch_gemm(const MnbArgs& a, hipStream_t s) {
+  // 256-row tiles (8 waves) when they still give every CU a workgroup, else 128-row tiles (4 waves)
+  const long ntn = (a.N + kTN - 1) / kTN, tiles256 = ntn * ((a.M + 255) / 256);
+  if (tiles256 >= 256)
+    hipLaunchKernelGGL((mnb_gemm_kernel<BITS, GROUP, ASYM, 4>), dim3((unsigned)tiles256), dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((mnb_gemm_kernel<BITS, GROUP, ASYM, 2>), dim3((unsigned)(ntn * ((a.M + 127) / 128))),
+                       dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -314,10 +413,9 @@ struct GemvF {
   static hipError_t run(const MnbArgs& a, hipStream_t s) { return launch_gemv<B, G, S>(a, s); }
 };
 template <int B, int G, bool S>
-struct DequantF {
-  static hipError_t run(const MnbArgs& a, _Float16* w16, hipStream_t s) { return launch_dequant<B, G, S>(a, w16, s); }
+struct GemmF {
+  static hipError_t run(const MnbArgs& a, hipStream_t s) { return launch_gemm<B, G, S>(a, s); }
 };
-
 }  // namespace
 
 hipError_t mnb_check(const MnbArgs& a) {
@@ -340,7 +438,10 @@ hipError_t launch_mnb_gemv(const MnbArgs& a, hipStream_t s) {
   return a.M <= kLanesRows ? dispatch_fmt<GemvLanesF>(a, s) : dispatch_fmt<GemvF>(a, s);
 }
 
-hipError_t launch_mnb_dequant(const MnbArgs& a, _Float16* w16, hipStream_t s) { return dispatch_fmt<DequantF>(a, w16, s); }
+hipError_t launch_mnb_gemm(const MnbArgs& a, hipStream_t s) {
+  if (a.M < 1 || !a.a || !a.y) return hipErrorInvalidValue;
+  return dispatch_fmt<GemmF>(a, s);
+}
 
 hipError_t launch_fwht(void* x, long rows_times_k, int n, hipStream_t s) {
   if (n < 2 || (n & (n - 1)) || n > 8192 || rows_times_k % n) return hipErrorInvalidValue;
@@ -348,83 +449,6 @@ hipError_t launch_fwht(void* x, long rows_times_k, int n, hipStream_t s) {
   hipLaunchKernelGGL(fwht_kernel, dim3((unsigned)(rows_times_k / n)), dim3(256), sizeof(float) * n, s, (_Float16*)x, n,
                      scale);
   return hipGetLastError();
-}
-
-// ---- the hipBLASLt product above mnb_packed_path: y (col-major N x M, ld N) = W16^T (W16 col-major K x N, ld K, transposed)
-// x a (col-major K x M, ld K) ----
-struct LtPlan {
-  hipblasLtMatmulDesc_t desc = nullptr;
-  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
-  hipblasLtMatmulAlgo_t algo{};
-};
-struct LtGemm {
-  hipblasLtHandle_t h = nullptr;
-  void* ws = nullptr;
-  size_t ws_bytes = 32u << 20;
-  std::mutex mu;
-  std::map<std::tuple<int, int, int>, LtPlan> plans;  // descriptors and algorithm per (M, N, K), kept for reuse
-};
-
-static LtGemm& lt_for_device(int dev) {
-  static std::mutex m;
-  static std::map<int, LtGemm*> per;
-  std::lock_guard<std::mutex> g(m);
-  LtGemm*& p = per[dev];
-  if (!p) p = new LtGemm();  // one per device for the process lifetime
-  return *p;
-}
-
-static bool make_plan(LtGemm& L, int M, int N, int K, LtPlan& p) {
-  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-  if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return false;
-  if (hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) != HIPBLAS_STATUS_SUCCESS)
-    return false;
-  if (hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16F, K, N, K) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16F, K, M, K) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16F, N, M, N) != HIPBLAS_STATUS_SUCCESS)
-    return false;
-  hipblasLtMatmulPreference_t pref = nullptr;
-  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
-  const uint64_t wsb = L.ws_bytes;
-  bool ok = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)) ==
-            HIPBLAS_STATUS_SUCCESS;
-  hipblasLtMatmulHeuristicResult_t res[1];
-  int got = 0;
-  ok = ok && hipblasLtMatmulAlgoGetHeuristic(L.h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &got) ==
-                 HIPBLAS_STATUS_SUCCESS &&
-       got >= 1 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= L.ws_bytes;
-  hipblasLtMatmulPreferenceDestroy(pref);
-  if (ok) p.algo = res[0].algo;
-  return ok;
-}
-
-hipError_t lt_gemm_f16(int device, int M, int N, int K, const void* w16, const void* a, void* y, hipStream_t s) {
-  LtGemm& L = lt_for_device(device);
-  std::lock_guard<std::mutex> g(L.mu);
-  if (!L.h) {
-    if (hipblasLtCreate(&L.h) != HIPBLAS_STATUS_SUCCESS) return hipErrorUnknown;
-    if (hipMalloc(&L.ws, L.ws_bytes) != hipSuccess) return hipErrorOutOfMemory;
-  }
-  auto key = std::make_tuple(M, N, K);
-  auto it = L.plans.find(key);
-  if (it == L.plans.end()) {
-    LtPlan p;
-    if (!make_plan(L, M, N, K, p)) {
-      if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
-      if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
-      if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
-      if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
-      return hipErrorNotSupported;
-    }
-    it = L.plans.emplace(key, p).first;
-  }
-  const LtPlan& p = it->second;
-  const float alpha = 1.0f, beta = 0.0f;
-  if (hipblasLtMatmul(L.h, p.desc, &alpha, w16, p.la, a, p.lb, &beta, y, p.lc, y, p.lc, &p.algo, L.ws, L.ws_bytes, s) !=
-      HIPBLAS_STATUS_SUCCESS)
-    return hipErrorUnknown;
-  return hipSuccess;
 }
 
 }  // namespace ha

@@ -1,7 +1,8 @@
 """GPU parity of the MatMulNBits projections (ha_mnb_forward through the C ABI) against the fp64 oracle: the model's
 projection shapes (web/public/gemmbench/portable.js:18) across the three implementations (M <= 2: lanes kernel;
-M <= 16, or 48 on matrices up to 2048 x 2048: packed-weight MFMA kernel; larger M: dequantised copy + hipBLASLt),
-every weight format of gemmbench/kernels.js:1-14, the exporter's own int4 quantiser, and the FWHT input rotation."""
+M <= 16, or 48 on matrices up to 2048 x 2048: packed-weight MFMA GEMV; larger M: the tiled GEMM that dequantises
+weight tiles into LDS), every weight format of gemmbench/kernels.js:1-14, ragged tile edges, the exporter's own
+int4 quantiser, and the FWHT input rotation."""
 import os
 import sys
 
@@ -79,8 +80,8 @@ def test_exporter_quantised_weights():
 
 @pytest.mark.parametrize("N,K", [(2048, 2048), (4096, 2048)])
 def test_implementations_agree_at_the_boundaries(N, K):
-    # the first rows computed with M = 2 (lanes kernel), 3 and 16 (MFMA kernel), 48 (MFMA kernel on the
-    # 2048 x 2048 matrix, library on the larger one) and 49 (dequantised copy + library GEMM)
+    # the first rows computed with M = 2 (lanes kernel), 3 and 16 (MFMA GEMV), 48 (MFMA GEMV on the 2048 x 2048
+    # matrix, tiled GEMM on the larger one) and 17 / 49 (tiled GEMM on the larger / smaller one)
     import torch
     words, sc, _ = _weights(N, K, seed=9)
     dev = "cuda:0"
@@ -96,6 +97,43 @@ def test_implementations_agree_at_the_boundaries(N, K):
         e = mo.rel_err(y[:2].float().cpu().numpy(), ref)
         print("M=%d vs M=49 on the first two rows: %.1e" % (M, e))
         assert e < TOL
+    w.close()
+
+
+@pytest.mark.parametrize("N,K,Ms,bits,group,asym", [
+    (1040, 2080, [49, 130, 257], 4, 32, False),   # N % 128 = 16, K % 64 = 32, M % 128 != 0
+    (2064, 2048, [200], 3, 64, True),
+    (16, 64, [1, 3, 50, 129], 2, 32, True),       # one 16-column tile, two blocks
+])
+def test_gemm_edges(N, K, Ms, bits, group, asym):
+    words, sc, bi = _weights(N, K, bits, group, asym, seed=N + K)
+    errs = _run(words, sc, bi, N, K, Ms, bits, group, asym)
+    print("N=%d K=%d bits=%d group=%d asym=%d" % (N, K, bits, group, asym), {m: "%.1e" % e for m, e in errs.items()})
+    assert max(errs.values()) < TOL
+
+
+def test_gemm_large_m_sampled_rows():
+    # one call with every row of a B = 8, T = 2048 prefill (M = 16384) on the largest input projection; a sample of
+    # rows against the oracle (the full fp64 product is too slow on the CPU), and rows 0..63 against an M = 64 call
+    import torch
+    N, K, M = 8256, 2048, 16384
+    words, sc, _ = _weights(N, K, seed=77)
+    dev = "cuda:0"
+    w = ha.MnbWeight(N, K, torch.from_numpy(words.view(np.int32)).to(dev), torch.from_numpy(sc).to(dev), None)
+    a = torch.from_numpy(((np.random.default_rng(3).random((M, K)) - 0.5) * 2).astype(np.float16)).to(dev)
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    y64 = torch.empty(64, N, dtype=torch.float16, device=dev)
+    print("gemm M=%d N=%d K=%d" % (M, N, K), flush=True)
+    w.forward(M, a, y)
+    w.forward(64, a, y64)
+    torch.cuda.synchronize()
+    assert torch.equal(y[:64], y64), "rows differ between M = 16384 and M = 64"
+    assert not torch.isnan(y).any()
+    rows = [0, 1, 127, 128, 5000, 8191, 12345, M - 1]
+    W = mo.dequant(words, sc, N, K)
+    e = mo.rel_err(y[rows].float().cpu().numpy(), mo.matmul(a[rows].cpu().numpy(), W))
+    print("sampled rows rel_err %.1e" % e)
+    assert e < TOL
     w.close()
 
 
