@@ -165,9 +165,9 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
                   ha_mnb** out);
 /* y[M][N] = a[M][K] x W^T (f16 in and out, fp32 accumulation) on `stream` (hipStream_t as void*, NULL: the null
    stream): the matmul dispatch of engine.js:236-246, kernel chosen by M as engine.js:17-33 does. a and y are device
-   pointers. Up to 16 rows (48 when N*K <= 2048*2048) the kernels read the packed weights directly; above that the
-   first call builds the handle's dequantised f16 copy of W (N*K*2 bytes) and the rows go through a library GEMM in
-   slices of at most 512 rows. */
+   pointers (16-byte aligned). Up to 64 rows a GEMV kernel reads the packed weights; above that a tiled MFMA GEMM
+   dequantises weight tiles into LDS. With few output tiles it splits K over workgroups, using a workspace the
+   handle owns (grown on demand, at most 64 MiB), so calls on one handle must be ordered. */
 int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream);
 int ha_mnb_destroy(ha_mnb* w);
 /* In-place orthonormal Walsh-Hadamard transform of every contiguous n-block of the f16 array x (elems values, a

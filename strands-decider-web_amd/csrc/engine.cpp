@@ -202,6 +202,8 @@ struct ha_mnb {
   uint32_t magic = kMnbMagic;
   ha::MnbArgs args{};
   int device = 0;
+  float* ws = nullptr;  // fp32 partial products of a split GEMM, grown on demand
+  size_t ws_bytes = 0;
 };
 
 extern "C" {
@@ -621,6 +623,22 @@ int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
     HA_HIP(ha::launch_mnb_gemv(g, st));
     return HA_OK;
   }
+  g.split = ha::mnb_gemm_split(M, g.N, g.K);
+  if (g.split > 1) {
+    const size_t need = sizeof(float) * (size_t)g.split * M * g.N;
+    if (need > w->ws_bytes) {
+      if (w->ws) {
+        HA_HIP(hipDeviceSynchronize());  // earlier calls on this handle may still read the old area
+        (void)hipFree(w->ws);
+        w->ws = nullptr;
+        w->ws_bytes = 0;
+      }
+      int rc = dalloc(&w->ws, need);
+      if (rc) return rc;
+      w->ws_bytes = need;
+    }
+    g.ws = w->ws;
+  }
   HA_HIP(ha::launch_mnb_gemm(g, st));
   return HA_OK;
 }
@@ -628,7 +646,12 @@ int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
 int ha_mnb_destroy(ha_mnb* w) {
   if (!w) return HA_OK;
   if (w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
-  w->magic = kDeadMagic;  // the handle owns no device memory; kernels in flight took its arguments by value
+  if (w->ws) {
+    HA_HIP(hipSetDevice(w->device));
+    HA_HIP(hipDeviceSynchronize());  // a split product in flight may still use the workspace
+    (void)hipFree(w->ws);
+  }
+  w->magic = kDeadMagic;
   delete w;
   return HA_OK;
 }

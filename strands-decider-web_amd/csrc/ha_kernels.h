@@ -77,10 +77,13 @@ struct MnbArgs {
   const void* q;  // [N][K/32][bits] u32
   const void* s;  // [N][K/group] f16
   const void* b;  // [N][K/group] f16 (asymmetric only)
+  int split = 1;     // GEMM only: K ranges, each on its own workgroups, summed in order by a second kernel
+  float* ws = nullptr;  // [split][M][N] fp32 partial products when split > 1
 };
 hipError_t mnb_check(const MnbArgs& a);
 bool mnb_packed_path(int M, int N, int K);  // whether launch_mnb_gemv (packed weights) serves M rows
 hipError_t launch_mnb_gemv(const MnbArgs& a, hipStream_t s);  // M <= 64 (mnb_packed_path picks up to 48)
+int mnb_gemm_split(int M, int N, int K);  // K ranges the GEMM uses for this shape (1: none, no workspace)
 hipError_t launch_mnb_gemm(const MnbArgs& a, hipStream_t s);  // any M: tiled GEMM, weights dequantised into LDS
 hipError_t launch_fwht(void* x, long elems, int n, hipStream_t s);
 hipError_t launch_tail_update(const TailArgs& a, hipStream_t s);

@@ -13,17 +13,21 @@
 // Three implementations, chosen by M (mnb_packed_path) as the reference chooses its kernels by M:
 //   M <= 2   mnb_gemv_lanes_kernel: weight-bandwidth bound. A wave owns 4 output columns, its lanes run along K
 //            over whole packed blocks, v_dot2_f32_f16 products, a cross-lane reduction.
-//   M <= 16 (48 on small matrices)  mnb_gemv_kernel: a workgroup owns 16 output columns and its 8 waves split the
-//            K blocks; each lane dequantises a whole packed block into the f16 B operands of
-//            v_mfma_f32_16x16x32_f16 (no LDS), the a rows are the A operand (16 rows per tile, up to 4 tiles share
-//            each dequantised operand), and the waves' partial sums meet in LDS.
-//   above    mnb_gemm_kernel: compute bound. A tiled MFMA GEMM (128 x 128 workgroup tiles) whose weight tiles are
-//            dequantised on their way into LDS, so the weights stay packed in HBM.
+//   M <= 64  mnb_gemv_kernel: a workgroup owns 16 output columns and its 8 waves split the K blocks; each lane
+//            dequantises a whole packed block into the f16 B operands of v_mfma_f32_16x16x32_f16 (no LDS), the a
+//            rows are the A operand (16 rows per tile, up to 4 tiles share each dequantised operand), and the
+//            waves' partial sums meet in LDS.
+//   above    mnb_gemm_kernel: compute bound. A tiled MFMA GEMM (128 or 256 x 128 workgroup tiles) whose weight
+//            tiles are dequantised on their way into LDS, so the weights stay packed in HBM. With few output tiles
+//            the K range is split over workgroups and mnb_split_sum_kernel adds the fp32 partials in order.
 // All three dequantise with the same f16 arithmetic (dequant8_pk: each weight rounded to f16 once), accumulate in
-// fp32 and round the output to f16. None splits K across workgroups, so results are deterministic.
+// fp32 and round the output to f16. Results are deterministic: a split K range is summed in a fixed order that
+// depends only on the shape.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "ha_kernels.h"
 
@@ -227,60 +231,88 @@ __global__ __launch_bounds__(256) void mnb_gemv_lanes_kernel(MnbArgs a) {
 // columns 64 wn .. + 63
 // as 2 x 2 tiles of v_mfma_f32_32x32x16_f16 (A operand lane l: row l % 32 of a, k 8 (l / 32) .. + 7 of the
 // 16-step; B operand: column l % 32, the same k; D: column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4).
-// The a tile and the dequantised weight tile are double-buffered in LDS (row pitch 72 halves). Each thread keeps
-// the global loads of the next kDepth tiles in flight in a register ring (per tile 64 bytes of one a row, one packed
-// block of one column and its scale); after multiplying tile kt it writes tile kt + 1, dequantised, into the other
-// buffer and issues the loads of tile kt + 1 + kDepth; one barrier per k tile. Rows past M and columns past N load clamped rows and are not stored; a k tile past the last
+// The a tile and the dequantised weight tile are double-buffered in LDS, 16-byte chunks XOR-swizzled by row. The a
+// tiles arrive by DMA (global_load_lds_dwordx4), issued one tile ahead; the packed weights of the next two tiles
+// sit in a register ring and are dequantised into the other stage while the current one is multiplied; one barrier
+// per k tile. Rows past M and columns past N load clamped rows and are not stored; a k tile past the last
 // block (K % 64 == 32) is zero in both operands. Tiles are numbered so that each XCD (workgroup id % 8) takes a
 // contiguous range of them, n fastest, sharing a rows in its L2.
-constexpr int kTN = 128, kTK = 64, kPitch = kTK + 8, kDepth = 4;
+constexpr int kTN = 128, kTK = 64;
 typedef float f16v __attribute__((ext_vector_type(16)));
+// 16-byte chunk c (k 8 c .. 8 c + 7 of the tile) of row r sits in slot 8 r + (c ^ (r & 7)): the MFMA operand reads
+// of 32 rows at one chunk then fall in distinct banks without padding
+__device__ __forceinline__ int swz(int r, int c) { return 8 * r + (c ^ (r & 7)); }
 template <int BITS, int GROUP, bool ASYM, int WMW>
 __global__ __launch_bounds__(128 * WMW) void mnb_gemm_kernel(MnbArgs a) {
   constexpr int kTM = 64 * WMW;                 // WMW wave rows of 64 a rows, 2 wave columns of 64 weight columns
   constexpr int kSPT = 8 / WMW;                 // dequantised 8-element slices per thread and k tile
   constexpr int kTPB = 4 / kSPT;                // threads per packed block
-  __shared__ _Float16 As[2][kTM * kPitch];
-  __shared__ _Float16 Bs[2][kTN * kPitch];
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, wm = w >> 1, wn = w & 1;
+  constexpr int kNB = ASYM ? 3 : 2;             // load instructions per thread for one tile's weights
+  // two stages of each tile as separate objects, so that the compiler can tell the stage being read from the one
+  // the DMA is filling and does not wait for the DMA before every read
+  __shared__ h8 As0[kTM * 8], As1[kTM * 8];
+  __shared__ h8 Bs0[kTN * 8], Bs1[kTN * 8];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wm = w >> 1, wn = w & 1;
   const int ntn = (a.N + kTN - 1) / kTN, ntm = (a.M + kTM - 1) / kTM, ntiles = ntn * ntm;
   int id = blockIdx.x;
   if (ntiles % 8 == 0) id = (id % 8) * (ntiles / 8) + id / 8;
   const int tn = id % ntn, tm = id / ntn;
   const int nblk = a.K / kBlk, nkt = (nblk + 1) / 2, ng = a.K / GROUP;
-  // this thread's loads: a row tm * kTM + tid / 2, k half tid % 2; weight column tn * 128 + bc, block half bh,
-  // slices s0 .. s0 + kSPT - 1 of the block
-  const int lr = tid >> 1, lh = tid & 1;
+  // this workgroup's K range: tiles kt0 .. kt1 - 1 (all of them unless the product is split)
+  const int sp_idx = blockIdx.y, kt0 = sp_idx * nkt / a.split, kt1 = (sp_idx + 1) * nkt / a.split;
+  // a tiles go global -> LDS directly: wave w's instruction i fills slots 64 (4 w + i) .. + 63 (rows 8 (4 w + i) ..
+  // + 7); lane l takes slot 64 (4 w + i) + l, i.e. row 8 (4 w + i) + l / 8 and the chunk swizzled into slot l % 8
+  const _Float16* arow_p[4];
+  int achunk[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 8 * (4 * w + i) + (lane >> 3);
+    arow_p[i] = (const _Float16*)a.a + (size_t)min(tm * kTM + r, a.M - 1) * a.K;
+    achunk[i] = (lane & 7) ^ (r & 7);
+  }
+  auto issue_a = [&](int kt, h8* stage) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      // past the last block (K % 64 == 32, or a tile past the end) read the row's last real block: the weights
+      // there are zero, so finite activations add nothing
+      int blk = 2 * kt + (achunk[i] >> 2);
+      const int c = blk < nblk ? achunk[i] : (achunk[i] & 3);
+      blk = min(blk, nblk - 1);
+      const _Float16* src = arow_p[i] + (size_t)blk * kBlk + 8 * (c & 3);
+      // global_load_lds_dwordx4 written out: the compiler would otherwise wait for every DMA in flight before any
+      // LDS read; the k-loop's explicit waits order the DMAs instead
+      const unsigned lds = __builtin_amdgcn_readfirstlane(
+          (unsigned)(size_t)(__attribute__((address_space(3))) h8*)&stage[64 * (4 * w + i)]);
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+    }
+  };
+  // weights: column tn * 128 + bc, block half bh, slices s0 .. s0 + kSPT - 1, loaded into a 2-deep register ring
   const int bc = tid / (2 * kTPB), bh = (tid / kTPB) & 1, s0 = (tid % kTPB) * kSPT;
-  const int arow = min(tm * kTM + lr, a.M - 1), wcol = min(tn * kTN + bc, a.N - 1);
-  gptr<h8> ap = (gptr<h8>)(gp<_Float16>(a.a) + (size_t)arow * a.K);  // 4 h8 per block
+  const int wcol = min(tn * kTN + bc, a.N - 1);
   gptr<unsigned> wp = gp<unsigned>(a.q) + (size_t)wcol * nblk * BITS;
   gptr<unsigned short> sp = gp<unsigned short>(a.s) + (size_t)wcol * ng;
   gptr<unsigned short> bp = ASYM ? gp<unsigned short>(a.b) + (size_t)wcol * ng : sp;
-  // ring of kDepth tiles in flight: tile t's loads live in slot t % kDepth
-  h8 ar[kDepth][4];
-  unsigned wr[kDepth][BITS];
-  unsigned short sr[kDepth], br[kDepth];  // f16 bits, loaded zero-extended into whole registers
-  auto load = [&](int kt, int r) {
-    const int b = min(2 * kt + lh, nblk - 1), bb = min(2 * kt + bh, nblk - 1);
-#pragma unroll
-    for (int j = 0; j < 4; j++) ar[r][j] = ap[4 * b + j];
-#pragma unroll
-    for (int j = 0; j < BITS; j++) wr[r][j] = wp[bb * BITS + j];
+  typedef unsigned uw __attribute__((ext_vector_type(BITS)));
+  uw wr[2];
+  unsigned short sr[2], br[2];  // f16 bits, loaded zero-extended into whole registers
+  auto load_b = [&](int kt, int r) {
+    const int bb = min(2 * kt + bh, nblk - 1);
+    wr[r] = *(const __attribute__((address_space(1))) uw*)(wp + bb * BITS);
     sr[r] = sp[bb * kBlk / GROUP];
-    br[r] = ASYM ? bp[bb * kBlk / GROUP] : (unsigned short)0;
+    if constexpr (ASYM) br[r] = bp[bb * kBlk / GROUP];
   };
-  auto store = [&](int kt, int r, int buf) {
-    const bool oka = 2 * kt + lh < nblk, okb = 2 * kt + bh < nblk;
-    _Float16* ad = &As[buf][lr * kPitch + 32 * lh];
-    _Float16* bd = &Bs[buf][bc * kPitch + 32 * bh];
-    const h2 sc = splat2(__builtin_bit_cast(_Float16, sr[r])), bi = splat2(__builtin_bit_cast(_Float16, br[r]));
+  auto store_b = [&](int kt, int r, h8* buf) {
+    const bool okb = kt < kt1 && 2 * kt + bh < nblk;
+    const h2 sc = splat2(__builtin_bit_cast(_Float16, sr[r]));
+    const h2 bi = splat2(ASYM ? __builtin_bit_cast(_Float16, br[r]) : (_Float16)0.0f);
+    unsigned wd[BITS];
 #pragma unroll
-    for (int j = 0; j < 4; j++) *reinterpret_cast<h8*>(ad + 8 * j) = oka ? ar[r][j] : h8{};
+    for (int j = 0; j < BITS; j++) wd[j] = wr[r][j];
 #pragma unroll
     for (int j = s0; j < s0 + kSPT; j++) {
-      const h8 v = dequant8_pk<BITS, ASYM>(wr[r], j, sc, bi);
-      *reinterpret_cast<h8*>(bd + 8 * j) = okb ? h8{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]} : h8{};
+      const h8 v = dequant8_pk<BITS, ASYM>(wd, j, sc, bi);
+      buf[swz(bc, 4 * bh + j)] = okb ? h8{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]} : h8{};
     }
   };
   f16v acc[2][2];
@@ -288,17 +320,15 @@ __global__ __launch_bounds__(128 * WMW) void mnb_gemm_kernel(MnbArgs a) {
   for (int i = 0; i < 2; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = f16v{};
-  const int fr = lane & 31, fk = 8 * (lane >> 5);
-  auto compute = [&](int buf) {
-    const _Float16* A0 = &As[buf][(64 * wm + fr) * kPitch + fk];
-    const _Float16* B0 = &Bs[buf][(64 * wn + fr) * kPitch + fk];
+  const int fr = lane & 31, fh = lane >> 5;
+  auto compute = [&](const h8* stage, const h8* buf) {
 #pragma unroll
     for (int ks = 0; ks < kTK / 16; ks++) {
       h8 af[2], bf[2];
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        af[i] = *reinterpret_cast<const h8*>(A0 + 32 * i * kPitch + 16 * ks);
-        bf[i] = *reinterpret_cast<const h8*>(B0 + 32 * i * kPitch + 16 * ks);
+        af[i] = stage[swz(64 * wm + 32 * i + fr, 2 * ks + fh)];
+        bf[i] = buf[swz(64 * wn + 32 * i + fr, 2 * ks + fh)];
       }
 #pragma unroll
       for (int i = 0; i < 2; i++)
@@ -306,28 +336,51 @@ __global__ __launch_bounds__(128 * WMW) void mnb_gemm_kernel(MnbArgs a) {
         for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
   };
-  // prologue: tile 0 into LDS buffer 0, tiles 1 .. kDepth in flight (loads past the last tile read clamped blocks)
-  load(0, 0);
-  store(0, 0, 0);
+  // s_waitcnt on vmcnt <= n (expcnt untouched) and, with lgkm, on this wave's LDS writes
+  auto wait_vm = [](auto n, bool lgkm = false) {
+    constexpr int v = decltype(n)::value;
+    if (lgkm)
+      __builtin_amdgcn_s_waitcnt((v & 15) | ((v >> 4) << 14) | (7 << 4));
+    else
+      __builtin_amdgcn_s_waitcnt((v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8));
+  };
+  // The k-loop's barrier: every wave's weight stores and its a tile kt + 1 have landed, then s_barrier. Written
+  // out because __syncthreads() carries a release fence, which waits for every load in flight (the a tiles arrive
+  // by DMA into LDS) and so would empty the pipeline; the empty asm statements keep the compiler from moving LDS
+  // accesses across.
+  auto barrier_after = [&](auto n) {
+    asm volatile("" ::: "memory");
+    wait_vm(n, true);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // prologue: a tile kt0 and its weights in LDS stage 0, the weights of tile kt0 + 1 in the ring
+  issue_a(kt0, As0);
+  load_b(kt0, 0);
+  load_b(kt0 + 1, 1);
+  store_b(kt0, 0, Bs0);
+  wait_vm(std::integral_constant<int, kNB>{}, true);  // all but the weights of tile 1
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  // iteration kt (stage r = kt % 2): issue a tile kt + 1 into the other stage; multiply tile kt; load tile kt + 2's
+  // weights into the ring slot tile kt's left, dequantise tile kt + 1's into the other stage; wait for a tile kt + 1
+  // (tile kt + 2's weights may stay in flight); one barrier. Run to an even tile count with no branch inside, so
+  // every stage and ring index is a constant; tiles past the last block are zero in the weight operand.
+  const int kt_end = kt0 + ((kt1 - kt0 + 1) & ~1);
+  for (int k0 = kt0; k0 < kt_end; k0 += 2) {
 #pragma unroll
-  for (int t = 1; t <= kDepth; t++) load(t, t % kDepth);
-  __syncthreads();
-  // iteration kt: multiply tile kt; write tile kt + 1 (slot (kt + 1) % kDepth) into the other buffer; refill that
-  // slot with tile kt + 1 + kDepth. Unrolled by kDepth so every slot index is a constant, and run to a multiple of
-  // kDepth tiles with no branch inside (tiles past the last block are zero in LDS and add nothing), so the compiler
-  // waits for one tile's loads at a time and never for the whole ring.
-  const int nkt_pad = (nkt + kDepth - 1) / kDepth * kDepth;
-  for (int k0 = 0; k0 < nkt_pad; k0 += kDepth) {
-#pragma unroll
-    for (int r = 0; r < kDepth; r++) {
+    for (int r = 0; r < 2; r++) {
       const int kt = k0 + r;
-      compute(kt & 1);
-      const int slot = (r + 1) % kDepth;
-      store(kt + 1, slot, (kt + 1) & 1);
-      load(kt + 1 + kDepth, slot);
-      __syncthreads();
+      issue_a(kt + 1, r ? As0 : As1);
+      compute(r ? As1 : As0, r ? Bs1 : Bs0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(kt + 2, r);
+      store_b(kt + 1, r ^ 1, r ? Bs0 : Bs1);
+      barrier_after(std::integral_constant<int, kNB>{});
     }
   }
+  // the last iterations issued a tiles past the end: let them land before the workgroup's LDS can be reused
+  wait_vm(std::integral_constant<int, 0>{});
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -336,11 +389,27 @@ __global__ __launch_bounds__(128 * WMW) void mnb_gemm_kernel(MnbArgs a) {
       if (n >= a.N) continue;
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const int m = tm * kTM + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (m < a.M) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)acc[i][j][v];
+        const int m = tm * kTM + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * fh + (v & 3);
+        if (m >= a.M) continue;
+        if (a.split > 1)
+          a.ws[((size_t)sp_idx * a.M + m) * a.N + n] = acc[i][j][v];
+        else
+          ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)acc[i][j][v];
       }
     }
 }
+
+// y = the sum of the split GEMM's partial products, in split order (so the result depends only on the shape)
+__global__ __launch_bounds__(256) void mnb_split_sum_kernel(const float* ws, _Float16* y, long mn4, int split) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= mn4) return;
+  f4 t = reinterpret_cast<const f4*>(ws)[i];
+  for (int s = 1; s < split; s++) t += reinterpret_cast<const f4*>(ws)[(size_t)s * mn4 + i];
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  reinterpret_cast<h4*>(y)[i] = h4{(_Float16)t[0], (_Float16)t[1], (_Float16)t[2], (_Float16)t[3]};
+}
+
+
 
 // In-place orthonormal Walsh-Hadamard transform (Sylvester order) of each contiguous n-block of an f16 row, one
 // workgroup per block (wgsl.js:91-108): the online input rotation of a tensor exported with `had: n`.
@@ -386,10 +455,15 @@ hipError_t launch_gemm(const MnbArgs& a, hipStream_t s) {
   // 256-row tiles (8 waves) when they still give every CU a workgroup, else 128-row tiles (4 waves)
   const long ntn = (a.N + kTN - 1) / kTN, tiles256 = ntn * ((a.M + 255) / 256);
   if (tiles256 >= 256)
-    hipLaunchKernelGGL((mnb_gemm_kernel<BITS, GROUP, ASYM, 4>), dim3((unsigned)tiles256), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((mnb_gemm_kernel<BITS, GROUP, ASYM, 4>), dim3((unsigned)tiles256, a.split), dim3(512), 0, s, a);
   else
-    hipLaunchKernelGGL((mnb_gemm_kernel<BITS, GROUP, ASYM, 2>), dim3((unsigned)(ntn * ((a.M + 127) / 128))),
+    hipLaunchKernelGGL((mnb_gemm_kernel<BITS, GROUP, ASYM, 2>), dim3((unsigned)(ntn * ((a.M + 127) / 128)), a.split),
                        dim3(256), 0, s, a);
+  if (a.split > 1) {
+    const long mn4 = (long)a.M * a.N / 4;
+    hipLaunchKernelGGL(mnb_split_sum_kernel, dim3((unsigned)((mn4 + 255) / 256)), dim3(256), 0, s, a.ws,
+                       (_Float16*)a.y, mn4, a.split);
+  }
   return hipGetLastError();
 }
 
@@ -428,9 +502,9 @@ hipError_t mnb_check(const MnbArgs& a) {
 
 bool mnb_packed_path(int M, int N, int K) {
   // Measured on MI355X, back-to-back calls on the model's projection shapes (N x K from 2048 x 2048 to
-  // 12288 x 2048): the library GEMM costs about 10 us at any M <= 64, the MFMA kernel 4-11 us up to 16 rows and
-  // up to 48 rows on matrices of at most 2048 x 2048, more beyond.
-  return M <= 16 || (M <= 48 && (long)N * K <= 2048L * 2048L);
+  // 12288 x 2048): up to 64 rows the packed-weight kernels are at least as fast as the tiled GEMM on every shape
+  // (at 64 rows 10-28 us against 27-71 us).
+  return M <= 64;
 }
 
 hipError_t launch_mnb_gemv(const MnbArgs& a, hipStream_t s) {
@@ -438,8 +512,20 @@ hipError_t launch_mnb_gemv(const MnbArgs& a, hipStream_t s) {
   return a.M <= kLanesRows ? dispatch_fmt<GemvLanesF>(a, s) : dispatch_fmt<GemvF>(a, s);
 }
 
+int mnb_gemm_split(int M, int N, int K) {
+  // Fewer output tiles than CUs leave CUs idle behind one long K loop each (about 0.85 us per 64-deep k tile):
+  // split K so that about 384 workgroups run, each over at least 4 k tiles, with at most 64 MiB of fp32 partials.
+  const long ntn = (N + kTN - 1) / kTN, tiles256 = ntn * ((M + 255) / 256);
+  const long tiles = tiles256 >= 256 ? tiles256 : ntn * ((M + 127) / 128);
+  const int nkt = (K / kBlk + 1) / 2;
+  if (tiles >= 256) return 1;
+  long sp = std::min<long>((384 + tiles - 1) / tiles, nkt / 4);
+  while (sp > 1 && sp * M * (long)N * 4 > (64L << 20)) sp--;
+  return (int)std::max<long>(sp, 1);
+}
+
 hipError_t launch_mnb_gemm(const MnbArgs& a, hipStream_t s) {
-  if (a.M < 1 || !a.a || !a.y) return hipErrorInvalidValue;
+  if (a.M < 1 || !a.a || !a.y || a.split < 1 || (a.split > 1 && !a.ws)) return hipErrorInvalidValue;
   return dispatch_fmt<GemmF>(a, s);
 }
 
