@@ -159,8 +159,9 @@ typedef struct ha_mnb_format {
 } ha_mnb_format;
 
 /* A quantised weight matrix on HIP device `device`: q, s and (asymmetric) b are device pointers the caller keeps
-   alive (the reference's weight storage buffers, engine.js:236-246). N must be a multiple of 16 (the export pads to
-   64), K of 32 and of the group. */
+   alive (the reference's weight storage buffers, engine.js:236-246). K must be a multiple of 32 and of the group;
+   a matmul (ha_mnb_forward) also needs N % 16 == 0 (the export pads N to 64), an embedding table (ha_embed) does
+   not. */
 int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const void* s, const void* b, int device,
                   ha_mnb** out);
 /* y[M][N] = a[M][K] x W^T (f16 in and out, fp32 accumulation) on `stream` (hipStream_t as void*, NULL: the null
@@ -174,6 +175,28 @@ int ha_mnb_destroy(ha_mnb* w);
    multiple of n; n a power of two up to 8192): the online input rotation of a tensor exported with `had: n`
    (FWHT, web/public/engine/wgsl.js:91-108; applied before the matmul at engine.js:240). */
 int ha_fwht(void* x, long elems, int n, int device, void* stream);
+
+/* ---- The rest of the torso forward (web/public/engine/engine.js:248-291): all device pointers, all on `stream`
+   (hipStream_t as void*, NULL: the null stream), on HIP device `device`. */
+
+/* x[t][0..K) = f32 row ids[t] of the quantised embedding table held by `table` (a MatMulNBits handle with N = table
+   rows, K = hidden size; EMBED, web/public/engine/wgsl.js:42-61): (q - 2^(bits-1)) * scale, or q * scale + bias, in
+   f32. ids: L u32 on the device; an id >= N gives a row of NaN. */
+int ha_embed(const ha_mnb* table, int L, const void* ids, void* x, void* stream);
+
+/* Residual add + RMSNorm (ADD_NORM, wgsl.js:64-87): for output row r with source row s = rows[r] (rows NULL: s = r),
+   if y != NULL first x[s] += y[s] (f32 += f16, written back), then
+   h[r] = x[s] * (mean(x[s]^2) + eps)^-1/2 * w   (w: D f32, already 1 + w where the model says so),
+   h f16, or f32 when out_f32 (the final norm, engine.js:290-291). x has nx rows of D (D % 8 == 0, D <= 8192);
+   a source row >= nx gives a NaN output row. */
+int ha_add_norm(int R, int D, int nx, void* x, const void* y, const float* w, void* h, int out_f32,
+                const void* rows, float eps, int device, void* stream);
+
+/* mid[t][j] = silu(big[t][j]) * big[t][I + j] for t < L, j < I (SILU_MUL, wgsl.js:90-99); f16, I % 8 == 0. */
+int ha_silu_mul(int L, int I, const void* big, void* mid, int device, void* stream);
+
+/* y[t][j] += c[j] for t < L, j < N (ADD_BIAS, wgsl.js:119-121): y f16, c f32 on the device, N % 8 == 0. */
+int ha_add_bias(int L, int N, void* y, const float* c, int device, void* stream);
 
 #ifdef __cplusplus
 }

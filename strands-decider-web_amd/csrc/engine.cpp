@@ -600,7 +600,7 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
   a.N = N; a.K = K; a.bits = fmt->bits; a.group = fmt->group; a.asym = fmt->asym ? 1 : 0;
   a.q = q; a.s = s; a.b = b;
   if (ha::mnb_check(a) != hipSuccess)
-    return fail(HA_ERR_ARG, "unsupported MatMulNBits shape or format (N % 16, K % 32, K % group, bits 2/3/4, group "
+    return fail(HA_ERR_ARG, "unsupported MatMulNBits shape or format (K % 32, K % group, bits 2/3/4, group "
                             "32/64, q/s (and b when asymmetric) non-NULL)");
   int ndev = 0;
   HA_HIP(hipGetDeviceCount(&ndev));
@@ -615,6 +615,7 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
 int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
   if (!w || w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
   if (M < 1 || !a || !y) return fail(HA_ERR_ARG, "M must be >= 1 and a, y non-NULL");
+  if (w->args.N % 16) return fail(HA_ERR_ARG, "a matmul needs N % 16 == 0 (the exporter pads N to 64)");
   HA_HIP(hipSetDevice(w->device));
   hipStream_t st = (hipStream_t)stream;
   ha::MnbArgs g = w->args;
@@ -662,6 +663,48 @@ int ha_fwht(void* x, long elems, int n, int device, void* stream) {
   hipError_t he = ha::launch_fwht(x, elems, n, (hipStream_t)stream);
   if (he == hipErrorInvalidValue) return fail(HA_ERR_ARG, "n must be a power of two in [2, 8192] dividing elems");
   HA_HIP(he);
+  return HA_OK;
+}
+
+int ha_embed(const ha_mnb* table, int L, const void* ids, void* x, void* stream) {
+  if (!table || table->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
+  if (L < 1 || !ids || !x) return fail(HA_ERR_ARG, "L must be >= 1 and ids, x non-NULL");
+  HA_HIP(hipSetDevice(table->device));
+  const ha::MnbArgs& t = table->args;
+  ha::EmbedArgs a{};
+  a.L = L; a.D = t.K; a.rows = t.N; a.bits = t.bits; a.group = t.group; a.asym = t.asym;
+  a.ids = (const unsigned*)ids; a.q = (const unsigned*)t.q; a.s = (const _Float16*)t.s; a.b = (const _Float16*)t.b;
+  a.x = (float*)x;
+  hipError_t he = ha::launch_embed(a, (hipStream_t)stream);
+  if (he == hipErrorInvalidValue) return fail(HA_ERR_ARG, "unsupported embedding table shape or format");
+  HA_HIP(he);
+  return HA_OK;
+}
+
+int ha_add_norm(int R, int D, int nx, void* x, const void* y, const float* w, void* h, int out_f32,
+                const void* rows, float eps, int device, void* stream) {
+  if (!x || !w || !h) return fail(HA_ERR_ARG, "x, w and h must be non-NULL");
+  if (R < 1 || nx < 1 || D < 8 || D % 8 || D > 8192) return fail(HA_ERR_ARG, "need R, nx >= 1, D % 8 == 0, D <= 8192");
+  if (!rows && R > nx) return fail(HA_ERR_ARG, "R > nx without a row list");
+  HA_HIP(hipSetDevice(device));
+  ha::AddNormArgs a{};
+  a.R = R; a.D = D; a.nx = nx; a.x = (float*)x; a.y = (const _Float16*)y; a.w = w; a.h = h; a.out_f32 = out_f32 ? 1 : 0;
+  a.rows = (const unsigned*)rows; a.eps = eps;
+  HA_HIP(ha::launch_add_norm(a, (hipStream_t)stream));
+  return HA_OK;
+}
+
+int ha_silu_mul(int L, int I, const void* big, void* mid, int device, void* stream) {
+  if (!big || !mid || L < 1 || I < 8 || I % 8) return fail(HA_ERR_ARG, "need big, mid non-NULL, L >= 1, I % 8 == 0");
+  HA_HIP(hipSetDevice(device));
+  HA_HIP(ha::launch_silu_mul(big, mid, L, I, (hipStream_t)stream));
+  return HA_OK;
+}
+
+int ha_add_bias(int L, int N, void* y, const float* c, int device, void* stream) {
+  if (!y || !c || L < 1 || N < 8 || N % 8) return fail(HA_ERR_ARG, "need y, c non-NULL, L >= 1, N % 8 == 0");
+  HA_HIP(hipSetDevice(device));
+  HA_HIP(ha::launch_add_bias(y, c, L, N, (hipStream_t)stream));
   return HA_OK;
 }
 

@@ -88,6 +88,30 @@ hipError_t launch_mnb_gemm(const MnbArgs& a, hipStream_t s);  // any M: tiled GE
 hipError_t launch_fwht(void* x, long elems, int n, hipStream_t s);
 hipError_t launch_tail_update(const TailArgs& a, hipStream_t s);
 
+// Torso ops around the mixers and projections (torso.hip).
+struct EmbedArgs {
+  int L, D, rows, bits, group, asym;  // rows: rows of the quantised table (ids >= rows give a NaN row)
+  const unsigned* ids;                // [L] device
+  const unsigned* q;                  // [rows][D/32][bits]
+  const _Float16* s;                  // [rows][D/group]
+  const _Float16* b;                  // asymmetric only
+  float* x;                           // [L][D] f32
+};
+struct AddNormArgs {
+  int R, D, nx;           // output rows, width, rows of x (a gather index >= nx gives a NaN output row)
+  float* x;               // [nx][D] f32 residual stream (updated in place when y is given)
+  const _Float16* y;      // [nx][D] f16 or NULL (no residual add)
+  const float* w;         // [D] norm weight (already 1 + w where the model says so)
+  void* h;                // [R][D] f16, or f32 with out_f32
+  const unsigned* rows;   // [R] source rows, or NULL for the identity
+  int out_f32;
+  float eps;
+};
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
+hipError_t launch_add_norm(const AddNormArgs& a, hipStream_t s);
+hipError_t launch_silu_mul(const void* big, void* mid, int L, int I, hipStream_t s);
+hipError_t launch_add_bias(void* y, const float* c, int L, int N, hipStream_t s);
+
 constexpr int kChunk = 64;  // gated-delta chunk length; chunk boundaries sit at s0 + 64k
 
 }  // namespace ha

@@ -493,7 +493,7 @@ struct GemmF {
 }  // namespace
 
 hipError_t mnb_check(const MnbArgs& a) {
-  if (a.N <= 0 || a.K <= 0 || a.N % 16 || a.K % 32) return hipErrorInvalidValue;
+  if (a.N <= 0 || a.K <= 0 || a.K % 32) return hipErrorInvalidValue;  // N % 16 is checked per matmul
   if (!(a.bits == 2 || a.bits == 3 || a.bits == 4) || !(a.group == 32 || a.group == 64) || a.K % a.group)
     return hipErrorInvalidValue;
   if (!a.q || !a.s || (a.asym && !a.b)) return hipErrorInvalidValue;

@@ -82,6 +82,10 @@ def load_library(path=LIB_PATH):
         "ha_mnb_forward": ([vp, i, vp, vp, vp], i),
         "ha_mnb_destroy": ([vp], i),
         "ha_fwht": ([vp, ctypes.c_long, i, i, vp], i),
+        "ha_embed": ([vp, i, vp, vp, vp], i),
+        "ha_add_norm": ([i, i, i, vp, vp, vp, vp, i, vp, ctypes.c_float, i, vp], i),
+        "ha_silu_mul": ([i, i, vp, vp, i, vp], i),
+        "ha_add_bias": ([i, i, vp, vp, i, vp], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -248,3 +252,34 @@ def fwht(x, elems, n, device=0, stream=None):
     """In-place orthonormal Walsh-Hadamard transform of each n-block of the f16 device array x (wgsl.js:91-108)."""
     load_library()
     _check(_lib.ha_fwht(_ptr(x), elems, n, device, _ptr(stream) if stream is not None else None))
+
+
+def _st(stream):
+    return _ptr(stream) if stream is not None else None
+
+
+def embed(table, L, ids, x, stream=None):
+    """x[t] = f32 row ids[t] of the quantised embedding table `table` (an MnbWeight with N = table rows, K = hidden
+    size; wgsl.js:42-61). ids: L u32 on the device; an id outside the table gives a NaN row."""
+    load_library()
+    _check(_lib.ha_embed(table._h, L, _ptr(ids), _ptr(x), _st(stream)))
+
+
+def add_norm(R, D, nx, x, y, w, h, out_f32=False, rows=None, eps=1e-6, device=0, stream=None):
+    """Residual add (x[s] += y[s] when y is given) then RMSNorm h[r] = x[s] rsqrt(mean(x[s]^2) + eps) w, with
+    s = rows[r] (identity when rows is None); h f16, or f32 with out_f32 (wgsl.js:64-87)."""
+    load_library()
+    _check(_lib.ha_add_norm(R, D, nx, _ptr(x), _ptr(y), _ptr(w), _ptr(h), int(bool(out_f32)), _ptr(rows), eps,
+                            device, _st(stream)))
+
+
+def silu_mul(L, I, big, mid, device=0, stream=None):
+    """mid[t][j] = silu(big[t][j]) * big[t][I + j] (f16; wgsl.js:90-99)."""
+    load_library()
+    _check(_lib.ha_silu_mul(L, I, _ptr(big), _ptr(mid), device, _st(stream)))
+
+
+def add_bias(L, N, y, c, device=0, stream=None):
+    """y[t][j] += c[j] (y f16, c f32; wgsl.js:119-121)."""
+    load_library()
+    _check(_lib.ha_add_bias(L, N, _ptr(y), _ptr(c), device, _st(stream)))

@@ -158,8 +158,10 @@ def test_errors():
     import torch
     s = torch.zeros(16, 64, dtype=torch.float16, device="cuda:0")
     q = torch.zeros(16, 64, 4, dtype=torch.int32, device="cuda:0")
+    w = ha.MnbWeight(15, 2048, q, s, None)  # a table of any row count (an embedding) ...
     with pytest.raises(ha.HAError):
-        ha.MnbWeight(15, 2048, q, s, None)  # N not a multiple of 16
+        w.forward(1, s, s)  # ... but a matmul needs N % 16 == 0
+    w.close()
     with pytest.raises(ha.HAError):
         ha.MnbWeight(16, 2048, q, s, None, bits=5)
     with pytest.raises(ha.HAError):

@@ -26,7 +26,7 @@ out.adapter = m.configFromManifest({layer_types: ['linear_attention', 'adapter',
 try { m.Engine.createSync(out.cfg, {device: 0}); out.created = true; } catch (e) { out.err = [e.code, e.message]; }
 const nat = require(require('path').join(require('path').dirname(%r), 'ha_napi.node'));
 try { nat.mnbForward({}, 1, BigInt(0), BigInt(0), null); } catch (e) { out.bad_handle = e.name + ': ' + e.message; }
-try { new m.MatMulNBits(null, 15, 2048, BigInt(16), BigInt(16), null); } catch (e) { out.bad_shape = e.code; }
+try { new m.MatMulNBits(null, 16, 2048, BigInt(16), BigInt(16), null, {bits: 5}); } catch (e) { out.bad_shape = e.code; }
 try { new m.MatMulNBits(null, 16, 2048, BigInt(16), BigInt(16), null); } catch (e) { out.no_dev = e.code; }
 m.Engine.create(out.cfg).then(function () { out.async = 'resolved'; }, function (e) { out.async = e.code; })
   .then(function () { console.log(JSON.stringify(out)); });
@@ -48,7 +48,7 @@ def test_addon_loads_and_maps_manifest_config():
             "fwht"} <= set(out["exports"])
     # a handle of the wrong kind is a TypeError from the addon, not a crash
     assert out["bad_handle"] == "TypeError: not a MatMulNBits handle"
-    # shape checks come before any device access (N % 16): HA_ERR_ARG
+    # format checks come before any device access (bits 5): HA_ERR_ARG
     assert out["bad_shape"] == "HA_1"
     c = out["cfg"]
     assert c["layerKinds"] == [0, 0, 0, 1] and c["batch"] == 8
