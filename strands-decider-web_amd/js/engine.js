@@ -220,8 +220,167 @@ function fwht(engine, x, elems, n) {
   native.fwht(ptrOf(x), elems, n, engine ? engine.device : 0, engine ? engine._h : null);
 }
 
+// In-place orthonormal Walsh-Hadamard transform of each n-block of a host Float32Array row range (the CPU unrotate
+// of a rotated torso's output, engine.js:365-366).
+function fwhtHost(a, off, n) {
+  for (let h = 1; h < n; h *= 2) {
+    for (let i = 0; i < n; i += 2 * h) {
+      for (let j = i; j < i + h; j++) {
+        const x = a[off + j], y = a[off + j + h];
+        a[off + j] = x + y;
+        a[off + j + h] = x - y;
+      }
+    }
+  }
+  const s = 1 / Math.sqrt(n);
+  for (let j = 0; j < n; j++) a[off + j] *= s;
+}
+
+/*
+ * The whole torso forward of the reference engine (web/public/engine/engine.js:248-376), batch 1, on this GPU:
+ * EMBED; per layer the input norm (with the residual add from layer 1 on), the in_proj / qkv projection, the token
+ * mixer, out_proj / o_proj, the post norm, gate_up, SILU_MUL and down (an adapter layer: proj + bias); then the final
+ * norm of the requested rows, f32, and the CPU unrotate of a rotated torso. Every step runs on one stream.
+ *
+ * Tensors by manifest name (convert/export_engine.py): setWeight(name, {q, s, b, N, K, bits, group, asym, had}) for
+ * the quantised ones ("embed", "layers.<i>.in_proj" | "qkv" | "out_proj" | "o_proj" | "gate_up" | "down" | "proj");
+ * setParam(name, Float32Array) for "final_norm", "layers.<i>.in_norm" | "post_norm" | "bias" (uploaded here) and the
+ * token mixers' "conv" | "neg_exp_A" | "dt_bias" | "gnorm" | "q_norm" | "k_norm" (forwarded to the layer's mixer).
+ * A quantised tensor's device buffers are the caller's and must stay alive.
+ */
+class Torso {
+  constructor(manifest, opts) {
+    const o = opts || {};
+    this.manifest = manifest;
+    this.D = pick(manifest, 'hidden_size', 2048);
+    this.I = pick(manifest, 'intermediate_size', 6144);
+    this.device = pick(o, 'device', 0);
+    this.types = manifest.layer_types.slice();
+    this.unrotate = pick(o, 'unrotate', pick(manifest, 'unrotate', null));
+    this.mixers = this.types.map((t) => {
+      if (t === 'adapter') return null;
+      return new Engine(configFromManifest(Object.assign({}, manifest, { layer_types: [t] }),
+        { batch: 1, maxCtx: pick(o, 'maxCtx', 4096), linDtype: F16, fullDtype: F16 }), { device: this.device });
+    });
+    this.lead = this.mixers.find((m) => m !== null) || new Engine(configFromManifest({ layer_types: ['adapter'] },
+      { batch: 1 }), { device: this.device });
+    this.mixers.forEach((m) => { if (m && m !== this.lead) native.shareStream(m._h, this.lead._h); });
+    this.weights = {};
+    this.vectors = {};
+  }
+  setWeight(name, w) {
+    const h = new MatMulNBits(this.lead, w.N, w.K, w.q, w.s, pick(w, 'b', null),
+      { bits: pick(w, 'bits', 4), group: pick(w, 'group', 32), asym: pick(w, 'asym', false) });
+    if (this.weights[name]) this.weights[name].h.destroy();
+    this.weights[name] = { h: h, N: w.N, K: w.K, had: pick(w, 'had', 0) };
+  }
+  setParam(name, data) {
+    const m = /^layers\.(\d+)\.(conv|neg_exp_A|dt_bias|gnorm|q_norm|k_norm)$/.exec(name);
+    if (m) {
+      const e = this.mixers[+m[1]];
+      if (!e) throw new Error('layer ' + m[1] + ' has no token mixer');
+      e.setParam(0, m[2], data);
+      return;
+    }
+    if (this.vectors[name]) this.vectors[name].free();
+    this.vectors[name] = this.lead.alloc(data.byteLength).upload(data);
+  }
+  _w(name) {
+    const w = this.weights[name];
+    if (!w) throw new Error('no tensor ' + name);
+    return w;
+  }
+  _v(name) {
+    const v = this.vectors[name];
+    if (!v) throw new Error('no tensor ' + name);
+    return v;
+  }
+  _matmul(L, a, name, y) {
+    const w = this._w(name);
+    if (w.had) native.fwht(a.ptr, L * w.K, w.had, this.device, this.lead._h);  // a is not read again
+    w.h.forward(L, a, y);
+    return w.N;
+  }
+  _norm(R, nx, x, y, wname, h, outF32, rows) {
+    native.addNorm(R, this.D, nx, x.ptr, y ? y.ptr : null, this._v(wname).ptr, h.ptr, outF32 ? 1 : 0,
+      rows ? rows.ptr : null, pick(this.manifest, 'rms_norm_eps', 1e-6), this.device, this.lead._h);
+  }
+  /*
+   * ids: token rows of the embedding table; rows: indices into ids whose final-normed hidden states are returned
+   * (default all). options {cache, keepCache} as Engine.forward; the cache is {P, ids, layers, release()}.
+   * Returns {hidden: Float32Array(rows.length * D), d: D, cache}.
+   */
+  forward(ids, rows, options) {
+    const o = options || {};
+    const L = ids.length, D = this.D, I = this.I;
+    const cache = pick(o, 'cache', null), keep = !!pick(o, 'keepCache', false);
+    const R = rows ? rows : Array.from({ length: L }, (_, i) => i);
+    let maxN = 2 * I;
+    Object.keys(this.weights).forEach((k) => { maxN = Math.max(maxN, this.weights[k].N); });
+    const al = (bytes) => this.lead.alloc(bytes);
+    const bufs = {
+      ids: al(L * 4).upload(Uint32Array.from(ids)), x: al(L * D * 4), h: al(L * D * 2), big: al(L * maxN * 2),
+      o: al(L * D * 2), y: al(L * D * 2), mid: al(L * I * 2), rows: al(Math.max(R.length, 1) * 4),
+      out: al(Math.max(R.length, 1) * D * 4),
+    };
+    const snaps = [];
+    try {
+      native.embed(this._w('embed').h._h, L, bufs.ids.ptr, bufs.x.ptr, this.lead._h);
+      this.types.forEach((t, i) => {
+        const P = 'layers.' + i + '.';
+        this._norm(L, L, bufs.x, i > 0 ? bufs.y : null, P + 'in_norm', bufs.h, false, null);
+        if (t === 'adapter') {  // x += proj(rms_norm(x)) + bias, the add in the next norm (engine.js:256-261)
+          this._matmul(L, bufs.h, P + 'proj', bufs.y);
+          native.addBias(L, D, bufs.y.ptr, this._v(P + 'bias').ptr, this.device, this.lead._h);
+          snaps.push(null);
+          return;
+        }
+        const stride = t === 'linear_attention' ? this.mixers[i].config.linStride : this.mixers[i].config.fullStride;
+        const pname = P + (t === 'linear_attention' ? 'in_proj' : 'qkv');
+        if (this._w(pname).N !== stride) throw new Error(pname + ' has ' + this._w(pname).N + ' columns, the mixer reads rows of ' + stride);
+        this._matmul(L, bufs.h, pname, bufs.big);
+        const r = this.mixers[i].forward(L, [bufs.big], [bufs.o],
+          { cache: cache ? cache.layers[i] : null, keepCache: keep });
+        snaps.push(r.cache);
+        this._matmul(L, bufs.o, P + (t === 'linear_attention' ? 'out_proj' : 'o_proj'), bufs.y);
+        this._norm(L, L, bufs.x, bufs.y, P + 'post_norm', bufs.h, false, null);
+        this._matmul(L, bufs.h, P + 'gate_up', bufs.big);
+        native.siluMul(L, I, bufs.big.ptr, bufs.mid.ptr, this.device, this.lead._h);
+        this._matmul(L, bufs.mid, P + 'down', bufs.y);
+      });
+      const out = new Float32Array(R.length * D);
+      if (R.length) {
+        bufs.rows.upload(Uint32Array.from(R));
+        this._norm(R.length, L, bufs.x, bufs.y, 'final_norm', bufs.out, true, bufs.rows);
+        bufs.out.download(out);  // synchronous on the shared stream
+      }
+      const c = this.unrotate;  // rotated torso: the original basis is c * FWHT(row) (engine.js:365-366)
+      if (c) for (let r = 0; r < R.length; r++) { fwhtHost(out, r * D, D); for (let j = 0; j < D; j++) out[r * D + j] *= c[j]; }
+      let snap = null;
+      if (keep) {
+        snap = { P: (cache ? cache.P : 0) + L, ids: (cache ? cache.ids : []).concat(Array.from(ids)), layers: snaps,
+          release: function () { snaps.forEach((s) => { if (s) s.release(); }); } };
+      }
+      return { hidden: out, d: D, cache: snap };
+    } finally {
+      this.lead.synchronize();  // nothing queued may still use the buffers
+      Object.keys(bufs).forEach((k) => bufs[k].free());
+    }
+  }
+  destroy() {
+    Object.keys(this.weights).forEach((k) => this.weights[k].h.destroy());
+    Object.keys(this.vectors).forEach((k) => this.vectors[k].free());
+    this.weights = {};
+    this.vectors = {};
+    this.mixers.forEach((m) => { if (m && m !== this.lead) m.destroy(); });
+    if (this.lead) this.lead.destroy();
+    this.lead = null;
+  }
+}
+
 module.exports = {
   Engine: Engine,
+  Torso: Torso,
   MatMulNBits: MatMulNBits,
   fwht: fwht,
   Snapshot: Snapshot,

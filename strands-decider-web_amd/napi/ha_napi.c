@@ -605,6 +605,84 @@ static napi_value js_fwht(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* shareStream(engine, other): run `engine`'s calls on `other`'s stream, so that work on several engines stays in
+   one order (ha_get_stream + ha_set_stream) */
+static napi_value js_share_stream(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  engine_box* a = get_engine(env, argv[0]);
+  engine_box* b = get_engine(env, argv[1]);
+  if (!a || !a->e || !b || !b->e) return type_error(env, "both arguments must be live engine handles");
+  void* st = NULL;
+  CHECK_HA(ha_get_stream(b->e, &st));
+  CHECK_HA(ha_set_stream(a->e, st));
+  return NULL;
+}
+
+/* embed(table, L, ids: BigInt, x: BigInt, engine|null) */
+static napi_value js_embed(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  if (!get_args(env, info, 5, argv)) return NULL;
+  mnb_box* mb = get_mnb(env, argv[0]);
+  if (!mb || !mb->w) return type_error(env, "not a MatMulNBits handle");
+  int32_t L;
+  void *ids, *x, *st;
+  if (napi_get_value_int32(env, argv[1], &L) != napi_ok) return type_error(env, "L must be an integer");
+  if (!get_ptr(env, argv[2], &ids) || !get_ptr(env, argv[3], &x)) return type_error(env, "ids and x must be BigInt");
+  if (!stream_of(env, argv[4], &st)) return type_error(env, "the last argument must be an engine handle or null");
+  CHECK_HA(ha_embed(mb->w, L, ids, x, st));
+  return NULL;
+}
+
+/* addNorm(R, D, nx, x, y|null, w, h, outF32, rows|null, eps, device, engine|null) */
+static napi_value js_add_norm(napi_env env, napi_callback_info info) {
+  napi_value argv[12];
+  if (!get_args(env, info, 12, argv)) return NULL;
+  int32_t R, D, nx, of, dev;
+  double eps;
+  void *x, *y = NULL, *w, *h, *rows = NULL, *st;
+  if (napi_get_value_int32(env, argv[0], &R) != napi_ok || napi_get_value_int32(env, argv[1], &D) != napi_ok ||
+      napi_get_value_int32(env, argv[2], &nx) != napi_ok || napi_get_value_int32(env, argv[7], &of) != napi_ok ||
+      napi_get_value_double(env, argv[9], &eps) != napi_ok || napi_get_value_int32(env, argv[10], &dev) != napi_ok)
+    return type_error(env, "R, D, nx, outF32, eps and device must be numbers");
+  if (!get_ptr(env, argv[3], &x) || !get_ptr(env, argv[5], &w) || !get_ptr(env, argv[6], &h))
+    return type_error(env, "x, w and h must be BigInt");
+  if (!is_nullish(env, argv[4]) && !get_ptr(env, argv[4], &y)) return type_error(env, "y must be a BigInt or null");
+  if (!is_nullish(env, argv[8]) && !get_ptr(env, argv[8], &rows)) return type_error(env, "rows must be a BigInt or null");
+  if (!stream_of(env, argv[11], &st)) return type_error(env, "the last argument must be an engine handle or null");
+  CHECK_HA(ha_add_norm(R, D, nx, x, y, (const float*)w, h, of, rows, (float)eps, dev, st));
+  return NULL;
+}
+
+/* siluMul(L, I, big, mid, device, engine|null) and addBias(L, N, y, c, device, engine|null) */
+static napi_value js_silu_mul(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  if (!get_args(env, info, 6, argv)) return NULL;
+  int32_t L, I, dev;
+  void *big, *mid, *st;
+  if (napi_get_value_int32(env, argv[0], &L) != napi_ok || napi_get_value_int32(env, argv[1], &I) != napi_ok ||
+      napi_get_value_int32(env, argv[4], &dev) != napi_ok)
+    return type_error(env, "L, I and device must be integers");
+  if (!get_ptr(env, argv[2], &big) || !get_ptr(env, argv[3], &mid)) return type_error(env, "big and mid must be BigInt");
+  if (!stream_of(env, argv[5], &st)) return type_error(env, "the last argument must be an engine handle or null");
+  CHECK_HA(ha_silu_mul(L, I, big, mid, dev, st));
+  return NULL;
+}
+
+static napi_value js_add_bias(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  if (!get_args(env, info, 6, argv)) return NULL;
+  int32_t L, N, dev;
+  void *y, *c, *st;
+  if (napi_get_value_int32(env, argv[0], &L) != napi_ok || napi_get_value_int32(env, argv[1], &N) != napi_ok ||
+      napi_get_value_int32(env, argv[4], &dev) != napi_ok)
+    return type_error(env, "L, N and device must be integers");
+  if (!get_ptr(env, argv[2], &y) || !get_ptr(env, argv[3], &c)) return type_error(env, "y and c must be BigInt");
+  if (!stream_of(env, argv[5], &st)) return type_error(env, "the last argument must be an engine handle or null");
+  CHECK_HA(ha_add_bias(L, N, y, (const float*)c, dev, st));
+  return NULL;
+}
+
 static napi_value init(napi_env env, napi_value exports) {
   const struct {
     const char* name;
@@ -620,6 +698,9 @@ static napi_value init(napi_env env, napi_value exports) {
       {"synchronize", js_synchronize},
       {"mnbCreate", js_mnb_create},         {"mnbForward", js_mnb_forward},
       {"mnbDestroy", js_mnb_destroy},       {"fwht", js_fwht},
+      {"embed", js_embed},                  {"addNorm", js_add_norm},
+      {"siluMul", js_silu_mul},             {"addBias", js_add_bias},
+      {"shareStream", js_share_stream},
   };
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); i++) {
     napi_value f;

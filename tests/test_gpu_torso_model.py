@@ -1,0 +1,216 @@
+"""A whole torso forward (web/public/engine/engine.js:248-376) on the GPU: embedding, a linear-attention, a full-
+attention, an adapter and a second linear-attention layer, each with its projections, norms and MLP at the model's
+widths (D = 2048, I = 6144), random int4 weights, then the final norm of a few rows. Three checks:
+- the Node host API (Torso in js/engine.js over the N-API addon) gives, bit for bit, what the same C ABI calls made
+  from Python give, for a prefix forward that keeps its cache and a suffix forward resumed from it;
+- both against an fp64 composition of the oracles (oracle/ C restatement for the token mixers, mnb_oracle for the
+  projections, torso_oracle for the rest) that rounds to f16 where the reference stores f16
+  (wgsl.js: matmul inputs and outputs, the mixers' outputs);
+- the resumed suffix against the same rows of one forward over the whole sequence (bit-exact at these lengths)."""
+import json
+import os
+import shutil
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import hybrid_attention as ha
+import synth
+from harness import oracle_gdn, oracle_gqa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+import mnb_oracle as mo  # noqa: E402
+import torso_oracle as to  # noqa: E402
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")]
+TYPES = ["linear_attention", "full_attention", "adapter", "linear_attention"]
+D, I, VOCAB, L0, L1 = 2048, 6144, 1000, 40, 9
+ROWS0, ROWS1 = [0, 17, 39], [0, 8]
+
+
+def _model(seed=11):
+    rng = np.random.default_rng(seed)
+    W, V, M = {}, {}, []
+
+    def quant(name, N, K, scale=0.005):
+        words = rng.integers(0, 2 ** 32, (N, K // 32, 4), dtype=np.uint64).astype(np.uint32)
+        sc = (scale * (0.8 + 0.4 * rng.random((N, K // 32)))).astype(np.float16)
+        W[name] = (words, sc, N, K)
+
+    def vec(name, base=1.0, noise=0.1):
+        V[name] = (base + noise * rng.normal(size=D)).astype(np.float32)
+
+    quant("embed", VOCAB, D, scale=0.1)
+    vec("final_norm")
+    for i, t in enumerate(TYPES):
+        p = "layers.%d." % i
+        vec(p + "in_norm")
+        if t == "adapter":
+            quant(p + "proj", D, D)
+            vec(p + "bias", 0.0, 0.05)
+            continue
+        if t == "linear_attention":
+            quant(p + "in_proj", 8256, D)
+            quant(p + "out_proj", D, 2048)
+            for k, v in synth.gdn_params(seed=seed, layer=i).items():
+                M.append((i, k, np.ascontiguousarray(v, np.float32)))
+        else:
+            quant(p + "qkv", 5120, D)
+            quant(p + "o_proj", D, 2048)
+            for k, v in synth.gqa_params(seed=seed, layer=i, noise=0.1).items():
+                M.append((i, k, np.ascontiguousarray(v, np.float32)))
+        vec(p + "post_norm")
+        quant(p + "gate_up", 2 * I, D)
+        quant(p + "down", D, I)
+    return W, V, M
+
+
+class PyTorso:
+    """The same C ABI calls as js/engine.js Torso.forward, in the same order, on one stream."""
+
+    def __init__(self, W, V, M):
+        import torch
+        self.torch = torch
+        self.dev = "cuda:0"
+        self.stream = torch.cuda.Stream()
+        self.st = self.stream.cuda_stream
+        self.keep = []
+        self.w = {}
+        for name, (words, sc, N, K) in W.items():
+            q, s = torch.from_numpy(words.view(np.int32)).to(self.dev), torch.from_numpy(sc).to(self.dev)
+            self.w[name] = ha.MnbWeight(N, K, q, s, None)
+        self.v = {k: torch.from_numpy(x).to(self.dev) for k, x in V.items()}
+        self.mix = {}
+        for i, t in enumerate(TYPES):
+            if t != "adapter":
+                self.mix[i] = ha.Engine(ha.model_config([t], batch=1, max_ctx=4096, lin_dtype=ha.F16,
+                                                        full_dtype=ha.F16), device=0, stream=self.st)
+        for i, k, x in M:
+            self.mix[i].set_param(0, k, x)
+        torch.cuda.synchronize()
+
+    def forward(self, ids, rows, cache=None, keep=False):
+        torch = self.torch
+        L = len(ids)
+        f16, f32 = torch.float16, torch.float32
+        with torch.cuda.stream(self.stream):
+            idd = torch.from_numpy(np.asarray(ids, np.uint32).view(np.int32)).to(self.dev)
+            x = torch.empty(L, D, dtype=f32, device=self.dev)
+            h = torch.empty(L, D, dtype=f16, device=self.dev)
+            big = torch.empty(L, 2 * I, dtype=f16, device=self.dev)
+            o = torch.empty(L, D, dtype=f16, device=self.dev)
+            y = torch.empty(L, D, dtype=f16, device=self.dev)
+            mid = torch.empty(L, I, dtype=f16, device=self.dev)
+            rd = torch.from_numpy(np.asarray(rows, np.uint32).view(np.int32)).to(self.dev)
+            out = torch.empty(len(rows), D, dtype=f32, device=self.dev)
+            ha.embed(self.w["embed"], L, idd, x, stream=self.st)
+            snaps = {}
+            for i, t in enumerate(TYPES):
+                p = "layers.%d." % i
+                ha.add_norm(L, D, L, x, y if i > 0 else None, self.v[p + "in_norm"], h, stream=self.st)
+                if t == "adapter":
+                    self.w[p + "proj"].forward(L, h, y, self.st)
+                    ha.add_bias(L, D, y, self.v[p + "bias"], stream=self.st)
+                    continue
+                self.w[p + ("in_proj" if t == "linear_attention" else "qkv")].forward(L, h, big, self.st)
+                r = self.mix[i].forward(L, [big], [o], cache=cache[i] if cache else None, keep_cache=keep)
+                snaps[i] = r["cache"]
+                self.w[p + ("out_proj" if t == "linear_attention" else "o_proj")].forward(L, o, y, self.st)
+                ha.add_norm(L, D, L, x, y, self.v[p + "post_norm"], h, stream=self.st)
+                self.w[p + "gate_up"].forward(L, h, big, self.st)
+                ha.silu_mul(L, I, big, mid, stream=self.st)
+                self.w[p + "down"].forward(L, mid, y, self.st)
+            ha.add_norm(len(rows), D, L, x, y, self.v["final_norm"], out, out_f32=True, rows=rd, stream=self.st)
+        torch.cuda.synchronize()
+        return out.cpu().numpy(), snaps
+
+    def close(self):
+        for s in self.w.values():
+            s.close()
+
+
+def _oracle(W, V, M, ids, rows):
+    """fp64 composition, rounding to f16 where the reference stores f16; one forward over all of ids."""
+    f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).astype(np.float64)  # noqa: E731
+    deq = {}
+
+    def mm(a, name):
+        words, sc, N, K = W[name]
+        if name not in deq:
+            deq[name] = mo.dequant(words, sc, N, K)
+        return f16(mo.matmul(a.astype(np.float16), deq[name]))
+
+    params = {}
+    for i, k, x in M:
+        params.setdefault(i, {})[k] = x
+    words, sc, _, _ = W["embed"]
+    x = to.embed(words, sc, ids, D)
+    y = None
+    for i, t in enumerate(TYPES):
+        p = "layers.%d." % i
+        h, x = to.add_norm(x, y, V[p + "in_norm"])
+        h = f16(h)
+        if t == "adapter":
+            y = f16(mm(h, p + "proj") + V[p + "bias"][None, :])
+            continue
+        if t == "linear_attention":
+            big = mm(h, p + "in_proj")
+            out, _ = oracle_gdn(big[None].astype(np.float16), params[i], gnorm=True)
+        else:
+            big = mm(h, p + "qkv")
+            out, _ = oracle_gqa(big[None].astype(np.float16), params[i], 4096)
+        o = f16(out[0])
+        y = mm(o, p + ("out_proj" if t == "linear_attention" else "o_proj"))
+        h, x = to.add_norm(x, y, V[p + "post_norm"])
+        g = mm(f16(h), p + "gate_up")
+        y = mm(f16(to.silu_mul(g, I)), p + "down")
+    hid, _ = to.add_norm(x, y, V["final_norm"], rows=rows)
+    return hid
+
+
+def test_torso_forward_node_matches_c_abi_and_oracle(tmp_path):
+    d = str(tmp_path)
+    W, V, M = _model()
+    rng = np.random.default_rng(5)
+    ids = rng.integers(0, VOCAB, L0 + L1).astype(np.uint32)
+    spec = {"types": TYPES, "D": D, "I": I, "L0": L0, "L1": L1, "rows0": ROWS0, "rows1": ROWS1,
+            "weights": {k: {"N": v[2], "K": v[3]} for k, v in W.items()}, "vectors": sorted(V),
+            "mixer": [[i, k] for i, k, _ in M]}
+    for k, (words, sc, N, K) in W.items():
+        words.tofile(os.path.join(d, "w_%s.q" % k))
+        sc.tofile(os.path.join(d, "w_%s.s" % k))
+    for k, x in V.items():
+        x.tofile(os.path.join(d, "v_%s.bin" % k))
+    for i, k, x in M:
+        x.tofile(os.path.join(d, "m_%d_%s.bin" % (i, k)))
+    ids[:L0].tofile(os.path.join(d, "ids0.bin"))
+    ids[L0:].tofile(os.path.join(d, "ids1.bin"))
+    with open(os.path.join(d, "spec.json"), "w") as f:
+        json.dump(spec, f)
+    print("node torso: layers %s L0=%d L1=%d" % (TYPES, L0, L1), flush=True)
+    r = subprocess.run([shutil.which("node"), os.path.join(ROOT, "tests", "js", "napi_torso.js"), d],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    js0 = np.fromfile(os.path.join(d, "hidden0.bin"), np.float32).reshape(len(ROWS0), D)
+    js1 = np.fromfile(os.path.join(d, "hidden1.bin"), np.float32).reshape(len(ROWS1), D)
+
+    t = PyTorso(W, V, M)
+    py0, snaps = t.forward(ids[:L0], ROWS0, keep=True)
+    py1, _ = t.forward(ids[L0:], ROWS1, cache=snaps)
+    full, _ = t.forward(ids, ROWS0 + [L0 + r for r in ROWS1])
+    t.close()
+    assert np.array_equal(js0, py0), "prefix hidden rows differ between Node and the C ABI"
+    assert np.array_equal(js1, py1), "resumed hidden rows differ between Node and the C ABI"
+
+    ref = _oracle(W, V, M, ids, ROWS0 + [L0 + r for r in ROWS1])
+    e0 = mo.rel_err(py0, ref[:len(ROWS0)])
+    e1 = mo.rel_err(py1, ref[len(ROWS0):])
+    ef = mo.rel_err(full[len(ROWS0):], py1)
+    print("torso vs oracle: prefix %.1e, resumed suffix %.1e; resumed vs one forward %.1e" % (e0, e1, ef))
+    assert e0 < 1e-2 and e1 < 1e-2
+    # the mixers' prefix + suffix is bit-exact, and at 9 and 49 rows the projections take the same per-row path
+    # (the MFMA GEMV, M <= 64), so the resumed rows equal those of one forward bit for bit
+    assert np.array_equal(full[len(ROWS0):], py1)
