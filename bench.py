@@ -14,6 +14,8 @@ Also reported, on the same line:
   cpu_baseline  the CPU oracle (oracle/, fp64) on the host cores for a bounded sample, scaled to the metric
   projections   the MatMulNBits projections either side of the path: per-forward time at M = 1 (HBM roofline)
                 and M = 2048 (MFMA roofline), with their own CPU baseline (the numpy oracle)
+  torso         ms per whole torso forward (embedding to final norm, the reference torso's layer counts) at
+                68 / 512 / 2048 tokens, next to the reference's published M4 Pro GPU time per forward
 """
 import argparse
 import json
@@ -225,6 +227,67 @@ def mnb_cpu_baseline():
                       "counts"}
 
 
+# The reference's own torso (web/public/gemmbench/portable.js:69 counts its matmuls per forward: 11 in_proj, 4 qkv,
+# 15 MLPs, 16 2048 x 2048 projections): 11 gated-delta, 4 GQA and 1 adapter layer. The order is not published and
+# does not change the work.
+REF_TORSO = (["linear_attention"] * 3 + ["full_attention"]) * 3 + ["linear_attention"] * 2 + ["adapter"] + \
+    ["full_attention"]
+REF_TORSO_MS = {68: 29.0, 512: 161.0, 2048: 646.0}  # README.md:90-91, M4 Pro GPU time per forward
+
+
+def torso_measure(torch, ha, Ls=(68, 512, 2048), steps=5, types=REF_TORSO, vocab=4096):
+    """ms per whole torso forward (embedding, every layer's norms, projections, token mixer and MLP, final norm of
+    the last row) through hybrid_attention.Torso, batch 1, random int4 weights (scales as portable.js:29-30) and
+    synthetic mixer parameters, HIP events on the torso's stream around `steps` forwards after one warm-up."""
+    import numpy as np
+
+    import synth
+    D, I = 2048, 6144
+    t = ha.Torso(types, D=D, I=I)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0)
+
+    def quant(N, K):
+        q = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 32, 4), dtype=torch.int32, device="cuda:0", generator=g)
+        s = (0.004 + 0.002 * torch.rand(N, K // 32, device="cuda:0", generator=g)).to(torch.float16)
+        return ha.MnbWeight(N, K, q, s, None)
+
+    rng = np.random.default_rng(0)
+    vec = lambda: (1 + 0.1 * rng.normal(size=D)).astype(np.float32)  # noqa: E731
+    t.set_weight("embed", quant(vocab, D))
+    t.set_param("final_norm", vec())
+    for i, k in enumerate(types):
+        p = "layers.%d." % i
+        t.set_param(p + "in_norm", vec())
+        if k == "adapter":
+            t.set_weight(p + "proj", quant(D, D))
+            t.set_param(p + "bias", (0.05 * rng.normal(size=D)).astype(np.float32))
+            continue
+        lin = k == "linear_attention"
+        t.set_weight(p + ("in_proj" if lin else "qkv"), quant(8256 if lin else 5120, D))
+        t.set_weight(p + ("out_proj" if lin else "o_proj"), quant(D, 2048))
+        t.set_param(p + "post_norm", vec())
+        t.set_weight(p + "gate_up", quant(2 * I, D))
+        t.set_weight(p + "down", quant(D, I))
+        ps = synth.gdn_params(seed=0, layer=i) if lin else synth.gqa_params(seed=0, layer=i, noise=0.1)
+        for n, v in ps.items():
+            t.set_param(p + n, v)
+    res = {}
+    for L in Ls:
+        ids = rng.integers(0, vocab, L)
+        t.forward(ids, [L - 1])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(t.stream)
+        for _ in range(steps):
+            t.forward(ids, [L - 1])
+        e1.record(t.stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        res["L%d" % L] = {"ms": round(ms, 3), "tokens_per_s": round(L / (ms * 1e-3)),
+                          "reference_m4pro_ms": REF_TORSO_MS.get(L)}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -233,7 +296,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true", help="skip the T / B sweep")
     ap.add_argument("--no-mnb", action="store_true", help="skip the MatMulNBits projection measurement")
-    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy", "mnb"],
+    ap.add_argument("--no-torso", action="store_true", help="skip the whole-torso forward measurement")
+    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy", "mnb", "torso"],
                     help="run only one layer kind (T=2048, B=--profile-batch) --steps times, for rocprofv3; 'copy' runs a plain "
                          "512 MiB device-to-device copy kernel, the reference point that scales FETCH_SIZE / "
                          "WRITE_SIZE to bytes")
@@ -263,6 +327,12 @@ def main():
             torch.cuda.synchronize()
         print(json.dumps({"profile_kernel": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
                           "ms_per_launch": (time.perf_counter() - t0) * 1e3 / args.steps}), flush=True)
+        return
+    if args.profile_kernel == "torso":
+        t0 = time.perf_counter()
+        res = torso_measure(torch, ha, Ls=(2048,), steps=args.steps)
+        print(json.dumps({"profile_kernel": "torso", "steps": args.steps, "result": res,
+                          "wall_s": round(time.perf_counter() - t0, 2)}), flush=True)
         return
     if args.profile_kernel == "mnb":
         t0 = time.perf_counter()
@@ -358,6 +428,11 @@ def main():
         line["projections"] = mnb_measure(torch, ha, stream)
         line["projections"]["workload"] = ("MatMulNBits int4 group-32 projections of one forward, shapes x counts of "
                                            "web/public/gemmbench/portable.js:18,69, random weights")
+    if not args.no_torso:
+        line["torso"] = torso_measure(torch, ha)
+        line["torso"]["workload"] = ("whole torso forward, batch 1: embedding, 11 gated-delta + 4 GQA + 1 adapter "
+                                     "layers (the reference torso's counts) with norms, int4 projections and MLPs, "
+                                     "final norm of the last row; random weights")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
         if "projections" in line:

@@ -176,7 +176,7 @@ int ha_mnb_destroy(ha_mnb* w);
    (FWHT, web/public/engine/wgsl.js:91-108; applied before the matmul at engine.js:240). */
 int ha_fwht(void* x, long elems, int n, int device, void* stream);
 
-/* ---- The rest of the torso forward (web/public/engine/engine.js:248-291): all device pointers, all on `stream`
+/* ---- The rest of the torso forward (web/public/engine/engine.js:247-284): all device pointers, all on `stream`
    (hipStream_t as void*, NULL: the null stream), on HIP device `device`. */
 
 /* x[t][0..K) = f32 row ids[t] of the quantised embedding table held by `table` (a MatMulNBits handle with N = table
@@ -187,7 +187,7 @@ int ha_embed(const ha_mnb* table, int L, const void* ids, void* x, void* stream)
 /* Residual add + RMSNorm (ADD_NORM, wgsl.js:64-87): for output row r with source row s = rows[r] (rows NULL: s = r),
    if y != NULL first x[s] += y[s] (f32 += f16, written back), then
    h[r] = x[s] * (mean(x[s]^2) + eps)^-1/2 * w   (w: D f32, already 1 + w where the model says so),
-   h f16, or f32 when out_f32 (the final norm, engine.js:290-291). x has nx rows of D (D % 8 == 0, D <= 8192);
+   h f16, or f32 when out_f32 (the final norm, engine.js:283-284, 342). x has nx rows of D (D % 8 == 0, D <= 8192);
    a source row >= nx gives a NaN output row. */
 int ha_add_norm(int R, int D, int nx, void* x, const void* y, const float* w, void* h, int out_f32,
                 const void* rows, float eps, int device, void* stream);

@@ -2,7 +2,7 @@
 // gather, the residual add + RMSNorm before each projection, the MLP's SiLU gate and an adapter layer's bias.
 //
 // Reference: web/public/engine/wgsl.js:42-61 (EMBED), 64-87 (ADD_NORM), 90-99 (SILU_MUL), 119-121 (ADD_BIAS), and
-// their dispatch in Engine.plan(), web/public/engine/engine.js:248-289 (final-norm row gather: engine.js:290-291,
+// their dispatch in Engine.plan(), web/public/engine/engine.js:247-281 (final-norm row gather: engine.js:283-284,
 // 342). All are HBM-bound: each element is read and written once, in 16-byte accesses.
 #include <hip/hip_runtime.h>
 

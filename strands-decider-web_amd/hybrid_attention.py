@@ -283,3 +283,79 @@ def add_bias(L, N, y, c, device=0, stream=None):
     """y[t][j] += c[j] (y f16, c f32; wgsl.js:119-121)."""
     load_library()
     _check(_lib.ha_add_bias(L, N, _ptr(y), _ptr(c), device, _st(stream)))
+
+
+class Torso:
+    """The whole torso forward (web/public/engine/engine.js:247-285, 313-376), batch 1, from the C ABI calls js/engine.js
+    Torso makes, in the same order, on one stream: EMBED; per layer the input norm (residual add from layer 1 on),
+    in_proj / qkv, the layer's token mixer (an Engine of its own), out_proj / o_proj, the post norm, gate_up,
+    SILU_MUL, down (an adapter layer: proj + bias); the final norm of the requested rows in f32.
+
+    set_weight(name, MnbWeight) for the quantised tensors ("embed", "layers.<i>.in_proj" | "qkv" | "out_proj" |
+    "o_proj" | "gate_up" | "down" | "proj"); set_param(name, f32 array) for "final_norm", "layers.<i>.in_norm" |
+    "post_norm" | "bias" and the mixers' "conv" | "neg_exp_A" | "dt_bias" | "gnorm" | "q_norm" | "k_norm"."""
+
+    _MIXER = ("conv", "neg_exp_A", "dt_bias", "gnorm", "q_norm", "k_norm")
+
+    def __init__(self, layer_types, D=2048, I=6144, max_ctx=4096, device=0):
+        import torch
+        self.torch = torch
+        self.types, self.D, self.I, self.device = list(layer_types), D, I, device
+        self.dev = "cuda:%d" % device
+        self.stream = torch.cuda.Stream(device=self.dev)
+        self.st = self.stream.cuda_stream
+        self.mix = {i: Engine(model_config([t], batch=1, max_ctx=max_ctx, lin_dtype=F16, full_dtype=F16),
+                              device=device, stream=self.st)
+                    for i, t in enumerate(self.types) if t != "adapter"}
+        self.w, self.v = {}, {}
+
+    def set_weight(self, name, w):
+        self.w[name] = w
+
+    def set_param(self, name, data):
+        parts = name.split(".")
+        if len(parts) == 3 and parts[0] == "layers" and parts[2] in self._MIXER:
+            self.mix[int(parts[1])].set_param(0, parts[2], data)
+            return
+        self.v[name] = self.torch.as_tensor(data, dtype=self.torch.float32).to(self.dev)
+
+    def forward(self, ids, rows=None, cache=None, keep=False):
+        """ids: token rows of the embedding table; rows: indices into ids to return (default all). Returns
+        (hidden f32 [len(rows)][D] on the host, {layer: Snapshot} when keep)."""
+        import numpy as np
+        torch, D, I, st = self.torch, self.D, self.I, self.st
+        L = len(ids)
+        rows = list(range(L)) if rows is None else list(rows)
+        f16, f32 = torch.float16, torch.float32
+        maxN = max([2 * I] + [w.N for w in self.w.values()])
+        with torch.cuda.stream(self.stream):
+            idd = torch.as_tensor(np.asarray(ids, np.uint32).view(np.int32)).to(self.dev)
+            x = torch.empty(L, D, dtype=f32, device=self.dev)
+            h = torch.empty(L, D, dtype=f16, device=self.dev)
+            big = torch.empty(L, maxN, dtype=f16, device=self.dev)
+            o = torch.empty(L, D, dtype=f16, device=self.dev)
+            y = torch.empty(L, D, dtype=f16, device=self.dev)
+            mid = torch.empty(L, I, dtype=f16, device=self.dev)
+            rd = torch.as_tensor(np.asarray(rows, np.uint32).view(np.int32)).to(self.dev)
+            out = torch.empty(len(rows), D, dtype=f32, device=self.dev)
+            embed(self.w["embed"], L, idd, x, stream=st)
+            snaps = {}
+            for i, t in enumerate(self.types):
+                p = "layers.%d." % i
+                add_norm(L, D, L, x, y if i > 0 else None, self.v[p + "in_norm"], h, device=self.device, stream=st)
+                if t == "adapter":
+                    self.w[p + "proj"].forward(L, h, y, st)
+                    add_bias(L, D, y, self.v[p + "bias"], device=self.device, stream=st)
+                    continue
+                self.w[p + ("in_proj" if t == "linear_attention" else "qkv")].forward(L, h, big, st)
+                r = self.mix[i].forward(L, [big], [o], cache=cache[i] if cache else None, keep_cache=keep)
+                snaps[i] = r["cache"]
+                self.w[p + ("out_proj" if t == "linear_attention" else "o_proj")].forward(L, o, y, st)
+                add_norm(L, D, L, x, y, self.v[p + "post_norm"], h, device=self.device, stream=st)
+                self.w[p + "gate_up"].forward(L, h, big, st)
+                silu_mul(L, I, big, mid, device=self.device, stream=st)
+                self.w[p + "down"].forward(L, mid, y, st)
+            add_norm(len(rows), D, L, x, y, self.v["final_norm"], out, out_f32=True, rows=rd, device=self.device,
+                     stream=st)
+        self.stream.synchronize()
+        return out.cpu().numpy(), (snaps if keep else None)

@@ -237,7 +237,7 @@ function fwhtHost(a, off, n) {
 }
 
 /*
- * The whole torso forward of the reference engine (web/public/engine/engine.js:248-376), batch 1, on this GPU:
+ * The whole torso forward of the reference engine (web/public/engine/engine.js:247-285, 313-376), batch 1, on this GPU:
  * EMBED; per layer the input norm (with the residual add from layer 1 on), the in_proj / qkv projection, the token
  * mixer, out_proj / o_proj, the post norm, gate_up, SILU_MUL and down (an adapter layer: proj + bias); then the final
  * norm of the requested rows, f32, and the CPU unrotate of a rotated torso. Every step runs on one stream.

@@ -1,6 +1,6 @@
 """GPU parity of the torso ops around the mixers and projections (ha_embed, ha_add_norm, ha_silu_mul, ha_add_bias
 through the C ABI) against the fp64 oracle: EMBED, ADD_NORM, SILU_MUL and ADD_BIAS of web/public/engine/wgsl.js:42-121
-at the model's widths (D = 2048, I = 6144), the final norm's gathered rows in f32 (engine.js:290-291), every
+at the model's widths (D = 2048, I = 6144), the final norm's gathered rows in f32 (engine.js:283-284, 342), every
 embedding format, and out-of-range indices (a NaN row, no out-of-bounds access)."""
 import os
 import sys
@@ -65,7 +65,7 @@ def test_add_norm(add, D):
 
 
 def test_final_norm_gathered_rows_f32():
-    # the final norm: residual add and norm only for the requested rows, f32 out (engine.js:290-291, 342);
+    # the final norm: residual add and norm only for the requested rows, f32 out (engine.js:283-284, 342);
     # a row index past the end gives a NaN row
     import torch
     rng = np.random.default_rng(9)

@@ -1,8 +1,9 @@
-"""A whole torso forward (web/public/engine/engine.js:248-376) on the GPU: embedding, a linear-attention, a full-
+"""A whole torso forward (web/public/engine/engine.js:247-285, 313-376) on the GPU: embedding, a linear-attention, a full-
 attention, an adapter and a second linear-attention layer, each with its projections, norms and MLP at the model's
 widths (D = 2048, I = 6144), random int4 weights, then the final norm of a few rows. Three checks:
-- the Node host API (Torso in js/engine.js over the N-API addon) gives, bit for bit, what the same C ABI calls made
-  from Python give, for a prefix forward that keeps its cache and a suffix forward resumed from it;
+- the Node host API (Torso in js/engine.js over the N-API addon) gives, bit for bit, what the Python host mirror
+  (hybrid_attention.Torso, the same C ABI calls) gives, for a prefix forward that keeps its cache and a suffix
+  forward resumed from it;
 - both against an fp64 composition of the oracles (oracle/ C restatement for the token mixers, mnb_oracle for the
   projections, torso_oracle for the rest) that rounds to f16 where the reference stores f16
   (wgsl.js: matmul inputs and outputs, the mixers' outputs);
@@ -68,68 +69,19 @@ def _model(seed=11):
     return W, V, M
 
 
-class PyTorso:
-    """The same C ABI calls as js/engine.js Torso.forward, in the same order, on one stream."""
-
-    def __init__(self, W, V, M):
-        import torch
-        self.torch = torch
-        self.dev = "cuda:0"
-        self.stream = torch.cuda.Stream()
-        self.st = self.stream.cuda_stream
-        self.keep = []
-        self.w = {}
-        for name, (words, sc, N, K) in W.items():
-            q, s = torch.from_numpy(words.view(np.int32)).to(self.dev), torch.from_numpy(sc).to(self.dev)
-            self.w[name] = ha.MnbWeight(N, K, q, s, None)
-        self.v = {k: torch.from_numpy(x).to(self.dev) for k, x in V.items()}
-        self.mix = {}
-        for i, t in enumerate(TYPES):
-            if t != "adapter":
-                self.mix[i] = ha.Engine(ha.model_config([t], batch=1, max_ctx=4096, lin_dtype=ha.F16,
-                                                        full_dtype=ha.F16), device=0, stream=self.st)
-        for i, k, x in M:
-            self.mix[i].set_param(0, k, x)
-        torch.cuda.synchronize()
-
-    def forward(self, ids, rows, cache=None, keep=False):
-        torch = self.torch
-        L = len(ids)
-        f16, f32 = torch.float16, torch.float32
-        with torch.cuda.stream(self.stream):
-            idd = torch.from_numpy(np.asarray(ids, np.uint32).view(np.int32)).to(self.dev)
-            x = torch.empty(L, D, dtype=f32, device=self.dev)
-            h = torch.empty(L, D, dtype=f16, device=self.dev)
-            big = torch.empty(L, 2 * I, dtype=f16, device=self.dev)
-            o = torch.empty(L, D, dtype=f16, device=self.dev)
-            y = torch.empty(L, D, dtype=f16, device=self.dev)
-            mid = torch.empty(L, I, dtype=f16, device=self.dev)
-            rd = torch.from_numpy(np.asarray(rows, np.uint32).view(np.int32)).to(self.dev)
-            out = torch.empty(len(rows), D, dtype=f32, device=self.dev)
-            ha.embed(self.w["embed"], L, idd, x, stream=self.st)
-            snaps = {}
-            for i, t in enumerate(TYPES):
-                p = "layers.%d." % i
-                ha.add_norm(L, D, L, x, y if i > 0 else None, self.v[p + "in_norm"], h, stream=self.st)
-                if t == "adapter":
-                    self.w[p + "proj"].forward(L, h, y, self.st)
-                    ha.add_bias(L, D, y, self.v[p + "bias"], stream=self.st)
-                    continue
-                self.w[p + ("in_proj" if t == "linear_attention" else "qkv")].forward(L, h, big, self.st)
-                r = self.mix[i].forward(L, [big], [o], cache=cache[i] if cache else None, keep_cache=keep)
-                snaps[i] = r["cache"]
-                self.w[p + ("out_proj" if t == "linear_attention" else "o_proj")].forward(L, o, y, self.st)
-                ha.add_norm(L, D, L, x, y, self.v[p + "post_norm"], h, stream=self.st)
-                self.w[p + "gate_up"].forward(L, h, big, self.st)
-                ha.silu_mul(L, I, big, mid, stream=self.st)
-                self.w[p + "down"].forward(L, mid, y, self.st)
-            ha.add_norm(len(rows), D, L, x, y, self.v["final_norm"], out, out_f32=True, rows=rd, stream=self.st)
-        torch.cuda.synchronize()
-        return out.cpu().numpy(), snaps
-
-    def close(self):
-        for s in self.w.values():
-            s.close()
+def _torso(W, V, M):
+    """The Python host mirror (hybrid_attention.Torso) loaded with the same model."""
+    import torch
+    t = ha.Torso(TYPES, D=D, I=I)
+    keep = []
+    for name, (words, sc, N, K) in W.items():
+        q, s = torch.from_numpy(words.view(np.int32)).to("cuda:0"), torch.from_numpy(sc).to("cuda:0")
+        t.set_weight(name, ha.MnbWeight(N, K, q, s, None))
+    for k, x in V.items():
+        t.set_param(k, x)
+    for i, k, x in M:
+        t.set_param("layers.%d.%s" % (i, k), x)
+    return t
 
 
 def _oracle(W, V, M, ids, rows):
@@ -197,11 +149,10 @@ def test_torso_forward_node_matches_c_abi_and_oracle(tmp_path):
     js0 = np.fromfile(os.path.join(d, "hidden0.bin"), np.float32).reshape(len(ROWS0), D)
     js1 = np.fromfile(os.path.join(d, "hidden1.bin"), np.float32).reshape(len(ROWS1), D)
 
-    t = PyTorso(W, V, M)
+    t = _torso(W, V, M)
     py0, snaps = t.forward(ids[:L0], ROWS0, keep=True)
     py1, _ = t.forward(ids[L0:], ROWS1, cache=snaps)
     full, _ = t.forward(ids, ROWS0 + [L0 + r for r in ROWS1])
-    t.close()
     assert np.array_equal(js0, py0), "prefix hidden rows differ between Node and the C ABI"
     assert np.array_equal(js1, py1), "resumed hidden rows differ between Node and the C ABI"
 
