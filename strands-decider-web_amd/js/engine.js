@@ -90,6 +90,11 @@ class DeviceBuffer {
     native.copyToDevice(this._engine._h, this.ptr, typedArray);
     return this;
   }
+  uploadAt(offset, typedArray) {
+    if (offset < 0 || offset + typedArray.byteLength > this.bytes) throw new RangeError('upload outside the buffer');
+    native.copyToDevice(this._engine._h, this.ptr + BigInt(offset), typedArray);
+    return this;
+  }
   download(typedArray) {
     if (typedArray.byteLength > this.bytes) throw new RangeError('download larger than the buffer');
     native.copyToHost(this._engine._h, typedArray, this.ptr);
@@ -267,6 +272,7 @@ class Torso {
     this.mixers.forEach((m) => { if (m && m !== this.lead) native.shareStream(m._h, this.lead._h); });
     this.weights = {};
     this.vectors = {};
+    this.embedRows = null;  // optional ids -> rows of the embedding table (a lazily filled table, loader.js)
   }
   setWeight(name, w) {
     const h = new MatMulNBits(this.lead, w.N, w.K, w.q, w.s, pick(w, 'b', null),
@@ -318,8 +324,9 @@ class Torso {
     let maxN = 2 * I;
     Object.keys(this.weights).forEach((k) => { maxN = Math.max(maxN, this.weights[k].N); });
     const al = (bytes) => this.lead.alloc(bytes);
+    const tableRows = this.embedRows ? this.embedRows(ids) : ids;
     const bufs = {
-      ids: al(L * 4).upload(Uint32Array.from(ids)), x: al(L * D * 4), h: al(L * D * 2), big: al(L * maxN * 2),
+      ids: al(L * 4).upload(Uint32Array.from(tableRows)), x: al(L * D * 4), h: al(L * D * 2), big: al(L * maxN * 2),
       o: al(L * D * 2), y: al(L * D * 2), mid: al(L * I * 2), rows: al(Math.max(R.length, 1) * 4),
       out: al(Math.max(R.length, 1) * D * 4),
     };
