@@ -323,13 +323,9 @@ class Torso {
     const R = rows ? rows : Array.from({ length: L }, (_, i) => i);
     let maxN = 2 * I;
     Object.keys(this.weights).forEach((k) => { maxN = Math.max(maxN, this.weights[k].N); });
-    const al = (bytes) => this.lead.alloc(bytes);
     const tableRows = this.embedRows ? this.embedRows(ids) : ids;
-    const bufs = {
-      ids: al(L * 4).upload(Uint32Array.from(tableRows)), x: al(L * D * 4), h: al(L * D * 2), big: al(L * maxN * 2),
-      o: al(L * D * 2), y: al(L * D * 2), mid: al(L * I * 2), rows: al(Math.max(R.length, 1) * 4),
-      out: al(Math.max(R.length, 1) * D * 4),
-    };
+    const bufs = this._work(L, Math.max(R.length, 1), maxN);
+    bufs.ids.upload(Uint32Array.from(tableRows));
     const snaps = [];
     try {
       native.embed(this._w('embed').h._h, L, bufs.ids.ptr, bufs.x.ptr, this.lead._h);
@@ -370,11 +366,28 @@ class Torso {
       }
       return { hidden: out, d: D, cache: snap };
     } finally {
-      this.lead.synchronize();  // nothing queued may still use the buffers
-      Object.keys(bufs).forEach((k) => bufs[k].free());
+      this.lead.synchronize();  // the next call may overwrite the work buffers
     }
   }
+  // Work buffers for L rows and R returned rows, kept between calls and grown when a call needs more (no device
+  // allocation on the steady path).
+  _work(L, R, maxN) {
+    const D = this.D, I = this.I;
+    const need = { ids: L * 4, x: L * D * 4, h: L * D * 2, big: L * maxN * 2, o: L * D * 2, y: L * D * 2,
+      mid: L * I * 2, rows: R * 4, out: R * D * 4 };
+    if (!this._bufs) this._bufs = {};
+    Object.keys(need).forEach((k) => {
+      const b = this._bufs[k];
+      if (!b || b.bytes < need[k]) {
+        if (b) b.free();
+        this._bufs[k] = this.lead.alloc(need[k]);
+      }
+    });
+    return this._bufs;
+  }
   destroy() {
+    if (this._bufs) Object.keys(this._bufs).forEach((k) => this._bufs[k].free());
+    this._bufs = null;
     Object.keys(this.weights).forEach((k) => this.weights[k].h.destroy());
     Object.keys(this.vectors).forEach((k) => this.vectors[k].free());
     this.weights = {};

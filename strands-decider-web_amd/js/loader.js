@@ -131,7 +131,10 @@ function loadTorso(dir, opts) {
   const destroy = torso.destroy.bind(torso);
   torso.destroy = function () {
     shardBufs.forEach((b) => b.free());
-    if (lazy) lazy.bufs.forEach((b) => b.free());
+    if (lazy) {
+      lazy.bufs.forEach((b) => b.free());
+      fs.closeSync(lazy.fd);
+    }
     destroy();
   };
   return torso;
@@ -176,6 +179,7 @@ function initLazyEmbed(torso, dir, manifest, o) {
     N: R + e.slots, K: fmtT.K || manifest.config.hidden_size, bits: fmtT.bits || 4, group: fmtT.group || 32,
     asym: !!fmtT.asym });
   const fd = fs.openSync(rowsPath, 'r');
+  E.fd = fd;  // closed by torso.destroy()
   torso.embedRows = function (tokIds) {
     let need = Array.from(new Set(tokIds)).filter((t) => E.slot[t] < 0);
     if (E.next + need.length > R + e.slots) {  // out of slots: drop every fetched row
