@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the hybrid-attention hot path on one MI355X.
 
-Headline (BASELINE.json metric): ms per forward of the 24-layer hybrid attention stack (18 gated-delta + 6 gated
-GQA layers in the 3:1 pattern) at T = 2048 for a batch of B = 8 independent sequences (
+Headline metric: ms per forward of the 24-layer hybrid attention stack (18 gated-delta + 6 gated
+GQA layers in the 3:1 pattern) at T = 2048 for a batch of B = 8 independent sequences (the benchmark's B=8, T=2048 configuration,
 projections excluded, synthetic post-projection rows ~N(0,1) already resident in HBM). One "step" is one such
 forward: every layer in stack order on one stream.
 
@@ -409,7 +409,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32 recurrence state + f16 MFMA operands (f32 accumulate); gated-delta rows f32, GQA rows f16",
         "data": "synthetic: post-projection rows ~N(0,1) (torch GPU RNG), conv taps ~N(0,0.5^2), unit q/k norm gain",
-        "config": {"workload": "BASELINE config 4: 24-layer hybrid stack (18 gated-delta + 6 GQA, 3:1), "
+        "config": {"workload": "24-layer hybrid stack (18 gated-delta + 6 GQA, 3:1), "
                                "B=8 sequences, T=2048, projections excluded",
                    "batch": B, "seq_len": T, "layers": len(KINDS), "gdn_recurrence": "chunked (64)"},
         "per_kind_ms": {"gated_delta_18": round(gdn_ms, 4), "gqa_6": round(gqa_ms, 4)},

@@ -29,7 +29,7 @@ def gdn_rows(T, B=1, H=16, DK=128, DV=128, stride=8256, seed=0, layer=0, part=0)
 
 
 def gdn_params(H=16, DK=128, DV=128, KC=4, seed=0, layer=0, neg_exp_A=-1.0, dt_bias=0.0, gnorm_noise=0.1):
-    """conv taps ~N(0, 0.5^2) (BASELINE config 0 reads "N(0,0.5)" as std 0.5), negA / dt_bias constants
+    """conv taps ~N(0, 0.5^2) ("N(0,0.5)" read as std 0.5), negA / dt_bias constants
     (alpha = exp(negA * softplus(a + dt_bias))), gated-norm weight 1 + gnorm_noise * N(0,1)."""
     C = 2 * H * DK + H * DV
     conv = (0.5 * rng(seed, layer, "conv").standard_normal((C, KC))).astype(np.float32)
@@ -48,7 +48,7 @@ def gqa_rows(T, B=1, HQ=8, HK=2, HD=256, stride=5120, seed=0, layer=0, part=0):
 
 
 def gqa_params(HD=256, seed=0, layer=0, noise=0.0):
-    """q_norm / k_norm as stored by the manifest (1 + w); noise = 0 gives unit gain (BASELINE config 1)."""
+    """q_norm / k_norm as stored by the manifest (1 + w); noise = 0 gives unit gain."""
     q = (1.0 + noise * rng(seed, layer, "q_norm").standard_normal(HD)).astype(np.float32)
     k = (1.0 + noise * rng(seed, layer, "k_norm").standard_normal(HD)).astype(np.float32)
     return {"q_norm": q, "k_norm": k}

@@ -38,7 +38,7 @@ def test_config0_chunked(gnorm, mode):
 
 
 def test_config2_T2048_against_oracle_and_sequential(mode):
-    # config-0 distributions at T=2048; chunked result vs the sequential fp32 recurrence
+    # one gated-delta layer at T=2048 with the T=64 case's input distributions; chunked result vs the sequential fp32 recurrence
     x = gdn_inputs(2048, seed=7)
     p = synth.gdn_params(seed=7)
     r = Runner(["linear_attention"], gnorm=False)

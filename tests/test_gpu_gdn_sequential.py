@@ -17,7 +17,7 @@ def _state(snap, B=1):
 
 @pytest.mark.parametrize("gnorm", [False, True])
 def test_config0_sequential(gnorm):
-    # T=64, 16 heads, fp32 rows, conv taps N(0, 0.5^2), negA = -1, dt_bias = 0, S0 = 0
+    # the CPU-runnable case: T=64, 16 heads, fp32 rows, conv taps N(0, 0.5^2), negA = -1, dt_bias = 0, S0 = 0
     x = gdn_inputs(64)
     p = synth.gdn_params()
     r = Runner(["linear_attention"], gnorm=gnorm)

@@ -11,7 +11,7 @@ TOL = 1e-2  # north-star bar for fp16 MFMA attention
 
 
 def test_config1_T2048():
-    # T=2048, 8 q heads, 2 KV heads, head_dim 256, f16 rows ~N(0,1), RoPE 64 dims base 1e7,
+    # one GQA layer at T=2048: 8 q heads, 2 KV heads, head_dim 256, f16 rows ~N(0,1), RoPE 64 dims base 1e7,
     # unit q/k norm gain, sigmoid gate
     x = synth.gqa_rows(2048)
     p = synth.gqa_params()

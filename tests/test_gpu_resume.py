@@ -1,4 +1,4 @@
-"""BASELINE config 3 on the GPU: a 1,536-token prefix through 3 gated-delta layers + 1 GQA layer, snapshot, then
+"""The prefix-cache case on the GPU: a 1,536-token prefix through 3 gated-delta layers + 1 GQA layer, snapshot, then
 5 independent 64-token suffixes resumed from it; each must equal the last 64 rows of a full 1,600-token forward
 bit for bit (the reference claims the same for its engine, README.md:60-61). Also the failure paths of the
 snapshot boundary (engine.js:316 context guard, released / foreign handles)."""
