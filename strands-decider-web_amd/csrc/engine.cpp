@@ -400,6 +400,18 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   // kernel otherwise. The two round differently, so the choice must not depend on the call (a resumed suffix must
   // match the same rows of one longer forward bit for bit).
   const bool split = mode == HA_CHUNKED_SPLIT || (mode == HA_CHUNKED && c.batch * c.H <= 32);
+  // raw-row tails: the copy reads only the call's input rows and the resumed tail, so the layers' copies are
+  // gathered into one launch after the mixers (per layer when per-layer times are asked for, so that each layer's
+  // time includes its own copy)
+  ha::TailArgs t{};
+  t.B = c.batch; t.stride = c.lin_stride; t.C = e->C; t.ab_off = e->C + c.H * c.DV; t.ab_n = 2 * c.H;
+  t.P = P; t.L = L; t.s0 = s0; t.KC = kKC; t.tail_cap_in = resume ? resume->tail_rows : kKC - 1;
+  t.tail_cap_out = kTailCap; t.dst_first = s1 - (kKC - 1); t.dtype = c.lin_dtype == HA_F16 ? 1 : 0;
+  auto flush_tails = [&]() {
+    const hipError_t he = ha::launch_tail_update(t, st);
+    t.n = 0;
+    return he;
+  };
   if (timing) HA_HIP(hipEventRecord(e->ev[0], st));
   for (int i = 0; i < c.n_layers; i++) {
     Layer& l = e->layers[i];
@@ -419,12 +431,11 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
                       : split ? ha::launch_gdn_split(a, st)
                               : ha::launch_gdn_chunked(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " gated-delta launch: " + hipGetErrorString(he));
-      ha::TailArgs t{};
-      t.B = c.batch; t.stride = c.lin_stride; t.C = e->C; t.ab_off = e->C + c.H * c.DV; t.ab_n = 2 * c.H;
-      t.P = P; t.L = L; t.s0 = s0; t.KC = kKC; t.tail_cap_in = a.tail_cap; t.tail_cap_out = kTailCap;
-      t.dst_first = s1 - (kKC - 1); t.dtype = a.dtype; t.in = a.in; t.tail = a.tail; t.tail_out = l.tail;
-      he = ha::launch_tail_update(t, st);
-      if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " tail update: " + hipGetErrorString(he));
+      t.in[t.n] = a.in; t.tail[t.n] = a.tail; t.tail_out[t.n] = l.tail; t.n++;
+      if ((opts && opts->layer_ms) || t.n == ha::kTailLayers) {
+        he = flush_tails();
+        if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " tail update: " + hipGetErrorString(he));
+      }
     } else if (l.kind == HA_FULL_ATTENTION) {
       ha::GqaArgs a{};
       a.B = c.batch; a.HQ = c.HQ; a.HK = c.HK; a.HD = c.HD; a.RD = c.rot_dim; a.stride = c.full_stride; a.LT = c.max_ctx;
@@ -435,6 +446,10 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       hipError_t he = ha::launch_gqa(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " attention launch: " + hipGetErrorString(he));
     }  // HA_ADAPTER: no token mixer, nothing to run
+  }
+  if (t.n > 0) {
+    const hipError_t he = flush_tails();
+    if (he != hipSuccess) return fail(HA_ERR_DEVICE, std::string("tail update: ") + hipGetErrorString(he));
   }
   if (opts && opts->layer_ms) HA_HIP(hipEventRecord(e->lev[c.n_layers], st));
   if (timing) HA_HIP(hipEventRecord(e->ev[1], st));

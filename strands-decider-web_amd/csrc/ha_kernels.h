@@ -54,12 +54,14 @@ size_t gqa_part_slot_bytes();
 
 // Copy the raw rows [dst_first, P + L) (dst_first >= s0 - (KC-1)) of every sequence from (tail, in) into
 // `tail_out` ([B][tail_cap][stride]); only the conv channels [0, C) and the a/b columns are kept.
+constexpr int kTailLayers = 32;  // gated-delta layers whose raw-row tails one launch updates
 struct TailArgs {
   int B, stride, C, ab_off, ab_n;
   int P, L, s0, KC, tail_cap_in, tail_cap_out, dst_first, dtype;
-  const void* in;
-  const void* tail;
-  void* tail_out;
+  int n;                          // layers in this launch, 1..kTailLayers
+  const void* in[kTailLayers];    // per layer: the call's input rows, [B][L][stride]
+  const void* tail[kTailLayers];  // per layer: the raw-row tail the call resumed from, [B][tail_cap_in][stride]
+  void* tail_out[kTailLayers];    // per layer: the working raw-row tail, [B][tail_cap_out][stride]
 };
 
 hipError_t launch_gdn_sequential(const GdnArgs& a, hipStream_t s);
