@@ -111,21 +111,40 @@ __device__ __forceinline__ void load8f<_Float16>(gptr<_Float16> p, float* o) {
   for (int i = 0; i < 8; i++) o[i] = (float)x[i];
 }
 
-// K rows and V^T columns for rows [t0, t0 + 64) of one (sequence, KV head). Wave w takes rows 16 w .. 16 w + 15,
-// lane l dims 4 l .. 4 l + 3: every row's k and v loads are issued before any is used. k: RMSNorm (wave-wide sum
-// of squares), gain, rotate-half RoPE on dims [0, 64) (dim i < 32 pairs with i + 32, held by lane l ^ 8), f16.
-// v: f16 into LDS, then each thread writes one dim's 64 positions of V^T, 16 bytes at a time when aligned.
+// Sum over the 64 lanes of a wave without LDS: row rotations inside each 16-lane row, then v_permlane16_swap
+// (rows 2r <-> 2r+1) and v_permlane32_swap (halves). Every lane ends with the same bits (each step adds two values
+// that the lanes it pairs see in the other order).
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+  v += dpp<0x128>(v);  // row_ror:8
+  v += dpp<0x124>(v);  // row_ror:4
+  v += dpp<0x122>(v);  // row_ror:2
+  v += dpp<0x121>(v);  // row_ror:1
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+  v = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  return sum_halves(v);
+}
+
+// K rows and V^T columns for rows [t0, t0 + 64) of one (sequence, KV head). Wave w takes rows kKvRows w ..
+// kKvRows w + kKvRows - 1, lane l dims 4 l .. 4 l + 3: every row's k and v loads are issued before any is used. k:
+// RMSNorm (wave-wide sum of squares), gain, rotate-half RoPE on dims [0, 64) (dim i < 32 pairs with i + 32, held by
+// lane l ^ 8), f16. v: f16 into LDS, then each thread writes 32 positions of one dim of V^T, 16 bytes at a time when
+// aligned.
+constexpr int kKvWaves = 8, kKvRows = 64 / kKvWaves;
 template <typename T>
-__global__ __launch_bounds__(256) void gqa_kv_kernel(GqaArgs a) {
+__global__ __launch_bounds__(64 * kKvWaves) void gqa_kv_kernel(GqaArgs a) {
   __shared__ _Float16 vs[64][kHD + 8];
   const int t0 = blockIdx.x * 64, kh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const size_t kvb = ((size_t)b * a.HK + kh) * a.LT * kHD;
   const f4 kw = *(gptr<f4>)(gp<float>(a.kw) + 4 * lane);
-  f4 x[16], vv[16];
+  f4 x[kKvRows], vv[kKvRows];
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int t = min(t0 + 16 * wave + r, a.L - 1);
+  for (int r = 0; r < kKvRows; r++) {
+    const int t = min(t0 + kKvRows * wave + r, a.L - 1);
     gptr<T> row = gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)a.HQ * 2 * kHD;
     x[r] = ld4(row + (size_t)kh * kHD + 4 * lane);
     vv[r] = ld4(row + (size_t)a.HK * kHD + (size_t)kh * kHD + 4 * lane);
@@ -133,11 +152,9 @@ __global__ __launch_bounds__(256) void gqa_kv_kernel(GqaArgs a) {
   const bool rot = lane < 16;  // dims 0 .. 63 (RD = 64)
   const int ri = 4 * (lane & 7);
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int t = t0 + 16 * wave + r, pos = a.P + min(t, a.L - 1);
-    float ss = (x[r][0] * x[r][0] + x[r][1] * x[r][1]) + (x[r][2] * x[r][2] + x[r][3] * x[r][3]);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m);
+  for (int r = 0; r < kKvRows; r++) {
+    const int t = t0 + kKvRows * wave + r, pos = a.P + min(t, a.L - 1);
+    const float ss = wave_sum64((x[r][0] * x[r][0] + x[r][1] * x[r][1]) + (x[r][2] * x[r][2] + x[r][3] * x[r][3]));
     const float inv = rsqrtf(ss / kHD + 1e-6f);
     f4 k = x[r] * inv * kw;
     f4 pk;
@@ -153,23 +170,23 @@ __global__ __launch_bounds__(256) void gqa_kv_kernel(GqaArgs a) {
     if (t < a.L)
       *(__attribute__((address_space(1))) h4*)(gpw<_Float16>(a.K) + kvb + (size_t)pos * kHD + 4 * lane) =
           h4{(_Float16)k[0], (_Float16)k[1], (_Float16)k[2], (_Float16)k[3]};
-    *reinterpret_cast<h4*>(&vs[16 * wave + r][4 * lane]) =
+    *reinterpret_cast<h4*>(&vs[kKvRows * wave + r][4 * lane]) =
         h4{(_Float16)vv[r][0], (_Float16)vv[r][1], (_Float16)vv[r][2], (_Float16)vv[r][3]};
   }
   __syncthreads();
-  const int d = tid;
+  const int d = tid & (kHD - 1), p0 = 32 * (tid >> 8);  // dim, first of this thread's 32 positions
   const int n = min(64, a.L - t0);
   __attribute__((address_space(1))) _Float16* vt = gpw<_Float16>(a.V) + kvb + (size_t)d * a.LT + a.P + t0;
   if (n == 64 && ((a.P + t0) & 7) == 0) {
 #pragma unroll
-    for (int g = 0; g < 8; g++) {
+    for (int g = 0; g < 4; g++) {
       h8 v8;
 #pragma unroll
-      for (int e = 0; e < 8; e++) v8[e] = vs[8 * g + e][d];
-      *(__attribute__((address_space(1))) h8*)(vt + 8 * g) = v8;
+      for (int e = 0; e < 8; e++) v8[e] = vs[p0 + 8 * g + e][d];
+      *(__attribute__((address_space(1))) h8*)(vt + p0 + 8 * g) = v8;
     }
   } else {
-    for (int r = 0; r < n; r++) vt[r] = vs[r][d];
+    for (int r = p0; r < min(n, p0 + 32); r++) vt[r] = vs[r][d];
   }
 }
 
@@ -626,7 +643,7 @@ hipError_t launch_gqa(const GqaArgs& a, hipStream_t s) {
   // RD = 64 puts both halves of every rotated q pair in one lane of the fused q preparation
   if (a.HD != kHD || a.RD != 64 || a.HQ % a.HK || a.HQ / a.HK != 4) return hipErrorInvalidValue;
   if (a.LT % kBK) return hipErrorInvalidValue;  // V^T tiles are read 64 positions at a time, inside [0, LT)
-  dim3 kgrid((a.L + 63) / 64, a.HK, a.B), kblock(256);
+  dim3 kgrid((a.L + 63) / 64, a.HK, a.B), kblock(64 * kKvWaves);
   if (a.dtype == 0)
     hipLaunchKernelGGL(gqa_kv_kernel<float>, kgrid, kblock, 0, s, a);
   else

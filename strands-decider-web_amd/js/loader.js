@@ -84,8 +84,11 @@ function readFile(dir, p) {
 }
 
 /*
- * loadTorso(dir, {maxCtx, device, readShard}) -> Torso. readShard(path) may supply a shard's bytes (for example from
- * a download); by default shards are read from dir. The torso's buffers are freed by torso.destroy().
+ * loadTorso(dir, {maxCtx, device, readShard, onProgress}) -> Torso. readShard(path) may supply a shard's bytes (for
+ * example from a download); by default shards are read from dir. onProgress(path) is called once per shard after it
+ * is on the device, as Engine.create calls it (engine.js:83). The reference's `subgroups` option chooses between two
+ * WGSL kernels for the same recurrence; there is one implementation here, so it is accepted and has no effect. The
+ * torso's buffers are freed by torso.destroy().
  */
 function loadTorso(dir, opts) {
   const o = opts || {};
@@ -101,7 +104,9 @@ function loadTorso(dir, opts) {
     const raw = o.readShard ? o.readShard(s.path) : readFile(dir, s.path);
     const data = s.wire ? unpackShard(raw, s, tensors) : raw;
     host.push(data);
-    return torso.lead.alloc(Math.max(data.byteLength, 4)).upload(data);
+    const buf = torso.lead.alloc(Math.max(data.byteLength, 4)).upload(data);
+    if (o.onProgress) o.onProgress(s.path);
+    return buf;
   });
   const at = (name) => {  // [shard index, byte offset in the shard] of a tensor
     const t = tensors[name];

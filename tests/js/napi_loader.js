@@ -9,7 +9,12 @@ const loader = require(path.join(__dirname, '..', '..', 'strands-decider-web_amd
 const [exp, work] = process.argv.slice(2);
 const u32 = (f) => { const b = fs.readFileSync(path.join(work, f)); return Array.from(new Uint32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength))); };
 const rows = JSON.parse(fs.readFileSync(path.join(work, 'rows.json'), 'utf8'));
-const torso = loader.loadTorso(exp, { maxCtx: 4096 });
+const progress = [];
+const torso = loader.loadTorso(exp, { maxCtx: 4096, onProgress: (p) => progress.push(p) });
+const manifest = JSON.parse(fs.readFileSync(path.join(exp, 'manifest.json'), 'utf8'));
+if (JSON.stringify(progress) !== JSON.stringify(manifest.shards.map((s) => s.path))) {
+  throw new Error('onProgress saw ' + JSON.stringify(progress));
+}
 const r0 = torso.forward(u32('ids0.bin'), rows[0]);
 fs.writeFileSync(path.join(work, 'hidden0.bin'), Buffer.from(r0.hidden.buffer));
 const r1 = torso.forward(u32('ids1.bin'), rows[1]);
