@@ -27,14 +27,15 @@ class Runner:
         d = self.cfg["lin_dtype"] if kind == ha.LINEAR else self.cfg["full_dtype"]
         return t.float16 if d == ha.F16 else t.float32
 
-    def forward(self, inputs, cache=None, keep=False, recurrence=ha.CHUNKED):
+    def forward(self, inputs, cache=None, keep=False, recurrence=ha.CHUNKED, layer_ms=False):
         t = self.torch
         L = inputs[0].shape[1]
         dev_in = [t.from_numpy(np.ascontiguousarray(x)).to("cuda:0", dtype=self._dt(k))
                   for x, k in zip(inputs, self.kinds)]
         dev_out = [t.full((self.B, L, 2048), float("nan"), dtype=self._dt(k), device="cuda:0") for k in self.kinds]
         t.cuda.synchronize()
-        res = self.eng.forward(L, dev_in, dev_out, cache=cache, keep_cache=keep, recurrence=recurrence, sync=True)
+        res = self.eng.forward(L, dev_in, dev_out, cache=cache, keep_cache=keep, recurrence=recurrence, sync=True,
+                               layer_ms=layer_ms)
         t.cuda.synchronize()
         return [o.float().cpu().numpy() for o in dev_out], res["cache"]
 
