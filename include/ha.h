@@ -170,6 +170,18 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
    dequantises weight tiles into LDS. With few output tiles it splits K over workgroups, using a workspace the
    handle owns (grown on demand, at most 64 MiB), so calls on one handle must be ordered. */
 int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream);
+/* No counterpart in the reference. ha_mnb_forward for callers that cannot allocate device memory (code under HIP
+   graph capture, serving loops or harnesses that forbid hipMalloc): the same kernels, K split and results, but a
+   split product's fp32 partials go to a fixed scratch array inside the library (HA_MNB_SCRATCH_BYTES per GPU, held
+   until the process ends) instead of the handle's on-demand workspace. It allocates nothing. The partials take
+   split x M x N x 4 bytes; K is split only when there are fewer than 256 output tiles of 128 x 128, which keeps
+   split x M x N below 638 x 128 x 128, so the scratch fits every shape (the 2B torso's projections need at most
+   33 MiB); a shape that did not fit would return HA_ERR_ARG. Every partial is written before it is read, so
+   nothing needs clearing. All calls
+   on one GPU share its scratch array and it keeps the last call's contents: calls that overlap on one GPU (other
+   streams, other threads) race, so order them on one stream. */
+#define HA_MNB_SCRATCH_BYTES (40u << 20)
+int ha_mnb_forward_noalloc(ha_mnb* w, int M, const void* a, void* y, void* stream);
 int ha_mnb_destroy(ha_mnb* w);
 /* In-place orthonormal Walsh-Hadamard transform of every contiguous n-block of the f16 array x (elems values, a
    multiple of n; n a power of two up to 8192): the online input rotation of a tensor exported with `had: n`

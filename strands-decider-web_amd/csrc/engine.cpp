@@ -197,6 +197,7 @@ void free_snapshot_buffers(ha_snapshot* s) {
 
 }  // namespace
 
+static_assert(ha::kMnbScratchBytes == HA_MNB_SCRATCH_BYTES, "ha.h states the no-allocation scratch size");
 constexpr uint32_t kMnbMagic = 0x48414d4eu;
 struct ha_mnb {
   uint32_t magic = kMnbMagic;
@@ -620,6 +621,9 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
   int ndev = 0;
   HA_HIP(hipGetDeviceCount(&ndev));
   if (device < 0 || device >= ndev) return fail(HA_ERR_ARG, "no HIP device " + std::to_string(device));
+  HA_HIP(hipSetDevice(device));
+  // the allocation-free entry point's scratch address on this device, looked up once per device
+  HA_HIP(ha::mnb_scratch_setup(device));
   ha_mnb* w = new ha_mnb();
   w->args = a;
   w->device = device;
@@ -627,7 +631,13 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
   return HA_OK;
 }
 
-int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// ha_mnb_forward and ha_mnb_forward_noalloc: the same kernels and K split; they differ only in where a split
+// product's fp32 partials go (the handle's workspace, grown on demand, or the library's fixed per-device scratch).
+int mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream, bool noalloc) {
   if (!w || w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
   if (M < 1 || !a || !y) return fail(HA_ERR_ARG, "M must be >= 1 and a, y non-NULL");
   if (w->args.N % 16) return fail(HA_ERR_ARG, "a matmul needs N % 16 == 0 (the exporter pads N to 64)");
@@ -640,7 +650,15 @@ int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
     return HA_OK;
   }
   g.split = ha::mnb_gemm_split(M, g.N, g.K);
-  if (g.split > 1) {
+  if (g.split > 1 && noalloc) {
+    const size_t need = sizeof(float) * (size_t)g.split * M * g.N;
+    if (need > ha::kMnbScratchBytes)
+      return fail(HA_ERR_ARG, "M = " + std::to_string(M) + " on this shape needs " + std::to_string(need) +
+                                  " bytes of split-K scratch, more than the " + std::to_string(ha::kMnbScratchBytes) +
+                                  " the allocation-free entry point has; use ha_mnb_forward");
+    g.ws = ha::mnb_scratch(w->device);
+    if (!g.ws) return fail(HA_ERR_DEVICE, "split-K scratch of this device was not set up");
+  } else if (g.split > 1) {
     const size_t need = sizeof(float) * (size_t)g.split * M * g.N;
     if (need > w->ws_bytes) {
       if (w->ws) {
@@ -657,6 +675,18 @@ int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
   }
   HA_HIP(ha::launch_mnb_gemm(g, st));
   return HA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ha_mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream) {
+  return mnb_forward(w, M, a, y, stream, false);
+}
+
+int ha_mnb_forward_noalloc(ha_mnb* w, int M, const void* a, void* y, void* stream) {
+  return mnb_forward(w, M, a, y, stream, true);
 }
 
 int ha_mnb_destroy(ha_mnb* w) {

@@ -87,6 +87,12 @@ bool mnb_packed_path(int M, int N, int K);  // whether launch_mnb_gemv (packed w
 hipError_t launch_mnb_gemv(const MnbArgs& a, hipStream_t s);  // M <= 64 (mnb_packed_path picks up to 48)
 int mnb_gemm_split(int M, int N, int K);  // K ranges the GEMM uses for this shape (1: none, no workspace)
 hipError_t launch_mnb_gemm(const MnbArgs& a, hipStream_t s);  // any M: tiled GEMM, weights dequantised into LDS
+// Scratch of the allocation-free GEMM entry point (mnb.hip): a file-scope device array of kMnbScratchBytes per GPU.
+// mnb_scratch_setup looks its address up on `device`, which must be current, once per device; mnb_scratch returns
+// that address (nullptr before the set-up).
+constexpr size_t kMnbScratchBytes = size_t(40) << 20;
+hipError_t mnb_scratch_setup(int device);
+float* mnb_scratch(int device);
 hipError_t launch_fwht(void* x, long elems, int n, hipStream_t s);
 hipError_t launch_tail_update(const TailArgs& a, hipStream_t s);
 

@@ -27,6 +27,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "ha_kernels.h"
@@ -527,6 +528,35 @@ int mnb_gemm_split(int M, int N, int K) {
 hipError_t launch_mnb_gemm(const MnbArgs& a, hipStream_t s) {
   if (a.M < 1 || !a.a || !a.y || a.split < 1 || (a.split > 1 && !a.ws)) return hipErrorInvalidValue;
   return dispatch_fmt<GemmF>(a, s);
+}
+
+// Fixed scratch for the allocation-free GEMM entry point: the fp32 partial products of a split K range. One copy per
+// GPU (a device global is instantiated on each device the code object is loaded on), held until the process ends.
+// Host code never passes the array's name to a kernel: it is a host-side stand-in there, not a device address. The
+// address is looked up once per device by mnb_scratch_setup (with that device current) and kept in g_scratch_ptr.
+static __device__ __align__(256) float scratch[kMnbScratchBytes / sizeof(float)];
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t mnb_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return hipSuccess;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!p) return hipErrorInvalidSymbol;
+  g_scratch_ptr[device] = p;
+  return hipSuccess;
+}
+
+float* mnb_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return static_cast<float*>(g_scratch_ptr[device]);
 }
 
 hipError_t launch_fwht(void* x, long rows_times_k, int n, hipStream_t s) {

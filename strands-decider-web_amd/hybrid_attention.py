@@ -80,6 +80,7 @@ def load_library(path=LIB_PATH):
         "ha_synchronize": ([vp], i),
         "ha_mnb_create": ([i, i, ctypes.POINTER(HaMnbFormat), vp, vp, vp, i, ctypes.POINTER(vp)], i),
         "ha_mnb_forward": ([vp, i, vp, vp, vp], i),
+        "ha_mnb_forward_noalloc": ([vp, i, vp, vp, vp], i),
         "ha_mnb_destroy": ([vp], i),
         "ha_fwht": ([vp, ctypes.c_long, i, i, vp], i),
         "ha_embed": ([vp, i, vp, vp, vp], i),
@@ -234,6 +235,11 @@ class MnbWeight:
 
     def forward(self, M, a, y, stream=None):
         _check(_lib.ha_mnb_forward(self._h, M, _ptr(a), _ptr(y), _ptr(stream) if stream is not None else None))
+
+    def forward_noalloc(self, M, a, y, stream=None):
+        """forward() without any device allocation: split-K partials go to the library's fixed per-GPU scratch
+        (ha_mnb_forward_noalloc; calls that overlap on one GPU race)."""
+        _check(_lib.ha_mnb_forward_noalloc(self._h, M, _ptr(a), _ptr(y), _ptr(stream) if stream is not None else None))
 
     def close(self):
         if self._h:
