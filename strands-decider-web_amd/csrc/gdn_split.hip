@@ -2,22 +2,27 @@
 //
 // Same semantics and chunk geometry as gdn_chunk.hip (the sequential rule of reference
 // web/public/engine/wgsl.js:124-187 + 252-268 in the chunked WY/UT form, chunk 64, chunk boundaries at s0 + 64 k),
-// split along the one dependency that is sequential: everything derived from a chunk's own rows (the q/k/v conv,
-// l2 norms, gates, A = strictly_lower(beta k k^T decay) and T = (I + A)^-1) does not depend on the state, so
+// split along the one dependency that is sequential. For a chunk with state S at its start:
+//   A = strictly_lower(beta_t (k^_t . k^_t') e^(gc_t - gc_t'))    T = (I + A)^-1
+//   W = T diag(beta e^gc) k^      U = T diag(beta) v^      V_new = U - W S
+//   o = diag(e^gc) q^ S + Att V_new,  Att = causal(q^ k^T e^(gc_t - gc_t'))   (t' <= t)
+//   S <- e^(gc_63) S + (diag(e^(gc_63 - gc)) k^)^T V_new                       (complete chunks only)
+// Everything except the three products with S depends only on the chunk's own rows, so
 //   gdn_prep_kernel  runs one workgroup per (chunk, sequence, head), all chunks at once over the whole chip, and
-//                    writes each chunk's "image" (q^, k^, T diag(beta), v^T in f16 and the gate vectors) to a
-//                    scratch buffer, in the exact layout the recurrence keeps in LDS;
-//   gdn_recur_kernel runs one workgroup per (sequence, head) through the chunks in order, holding the fp32 state in
-//                    MFMA accumulators (8 waves x 16 value columns). Per chunk it DMAs the next image into LDS while
-//                    it does the state work of the current one, and builds k^T and the decay-masked scores q^ k^T
-//                    itself (cheap, and their images would cost more HBM traffic than they save). V_new is formed as
-//                    T diag(beta) (v - diag(e^gc) k^ S), one product instead of two.
-// The state-independent work is then off the per-chunk critical path, which is what bounds the fused kernel when
-// there are fewer (sequence, head) pairs than CUs (B = 1: 16 of 256 CUs).
+//                    writes each chunk's "image": the MFMA A operands q~ = diag(e^gc) q^, W, K~^T and Att and the
+//                    matrix U, every operand block in lane order (64 lanes x 16 bytes), so that the recurrence
+//                    reads each with one conflict-free 16-byte LDS load and no lane moves;
+//   gdn_chain_kernel runs one workgroup per (sequence, head) through the chunks in order: 4 waves, each holding 32
+//                    value columns of the fp32 state in MFMA accumulators. Per chunk its dependent chain is
+//                    W S -> V_new -> state update; q~ S, Att V_new, the gated norm (GNORM) and the output are off
+//                    that chain. It DMAs image p+1 into the other of two LDS buffers while it works on chunk p.
 //
-// Both kernels share the fused kernel's helpers and MFMA operand conventions (gdn_common.h); the per-column state
-// arithmetic follows the fused kernel's except for the V_new bracket, and the gated norm's row sums are formed in
-// a different order (16-column partials).
+// MFMA operand convention (v_mfma_f32_16x16x32_f16): lane l supplies row l & 15 of A and column l & 15 of B, with
+// K indices assigned per (lane group l >> 4, element); D holds rows 4 (l >> 4) + e of column l & 15. A D tile pair
+// (rows 32 kb .. 32 kb + 31 of a column) is reused as a B operand with the permuted K order
+// {32 kb + 4 grp + e} U {32 kb + 16 + 4 grp + e}; the image's A operands are stored in that same order. The prep
+// kernel obtains most of them as D tiles of transposed products (W^T = k^T (T diag(beta e^gc))^T and
+// Att^T = k^ q^T), whose lanes already hold exactly those K indices.
 #include <stddef.h>
 
 #include "gdn_common.h"
@@ -25,46 +30,63 @@
 namespace ha {
 namespace {
 
-// One chunk's image. Member order and padding match the recurrence kernel's LDS copy byte for byte.
-struct Img {
-  _Float16 Qs[kCH * kQP];  // q^ / sqrt(DK), [t][i]
-  _Float16 Ks[kCH * kQP];  // k^, [t][i]
-  _Float16 Tb[kCH * kTP];  // T diag(beta), [t][t'] (blocks above the diagonal zero)
-  _Float16 VT[kDV * kTP];  // v^ = SiLU(conv(v)) transposed, [j][t], 8-row groups swizzled by vt16
-  float eg[kCH];           // e^gc
-  float ed[kCH];           // e^(gc_63 - gc)
-  float gc[kCH];           // cumulative log decay inside the chunk
-  float rowf[kCH];         // e^(gc_t - gc_16(t/16)), in (0, 1]
-  float colf[3][kCH];      // colf[i-1][t'] = e^(gc_16i - gc_t') for t' < 16 i, in (0, 1]
-};
-static_assert(sizeof(Img) % 16 == 0, "image is copied in 16-byte words");
-constexpr int kImg = (int)((sizeof(Img) + 1023) / 1024 * 1024);  // image size: whole 1 KiB DMA instructions
-// Per chunk, the image is followed by the gated norm's gate factors gnorm_w[j] * SiLU(z[t][j]) in fp32, [j][t]:
-// the recurrence reads them straight into the D layout of its output rows (4 consecutive rows per load).
-constexpr int kGate = (int)sizeof(float) * kDV * kCH;
+// ---- chunk image layout (bytes) ----
+constexpr int kBlk = 1024;            // one A-operand block: 64 lanes x 16 bytes (8 f16)
+constexpr int kOffQ = 0;              // q~ blocks [tb 0..3][kb 0..3]: rows 16 tb + (l & 15), state rows as K
+constexpr int kOffW = 16 * kBlk;      // W blocks [tb][kb], same arrangement
+constexpr int kOffK = 32 * kBlk;      // K~^T blocks [ib 0..7][kb 0..1]: state rows 16 ib + (l & 15), chunk rows as K
+constexpr int kOffA = 48 * kBlk;      // Att blocks [tb 0..3][kb 0..1] (blocks with kb > tb / 2 are zero, never read)
+constexpr int kOffU = 56 * kBlk;      // U in the D layout: blocks [tb 0..3][jt 0..7] of 64 lanes x 4 f16
+constexpr int kOffS = 72 * kBlk;      // e^(gc_63) as f32
+constexpr int kImg = 73 * kBlk;       // whole 1 KiB DMA instructions
+// After the image (not copied to LDS): the gated norm's factors gnorm_w[j] SiLU(z[t][j]) in fp32, in the lane order of
+// the recurrence's transposed output: block (w, tb, jj) of 64 lanes x 4 floats holds, for lane (grp, c16),
+// columns 32 w + 16 jj + 4 grp .. + 3 of chunk row 16 tb + c16.
+constexpr int kGate = 32 * kBlk;
 constexpr int kChunkScratch = kImg + kGate;
+
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i2v __attribute__((ext_vector_type(2)));
+
+// Stores into one chunk's image through a buffer resource (raw 16 / 8-byte stores; offsets in bytes).
+struct ImgOut {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ explicit ImgOut(void* base) : r(__builtin_amdgcn_make_buffer_rsrc(base, 0, kImg, 0x00020000)) {}
+  __device__ void st16(int off, const h8& v) const {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), r, off, 0, 0);
+  }
+  __device__ void st8(int off, const h4& v) const {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, v), r, off, 0, 0);
+  }
+  __device__ void st4(int off, float v) const { __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), r, off, 0, 0); }
+};
+
+__device__ __forceinline__ h8 join(const f4& lo, const f4& hi) { return pack_b(lo, hi); }
 
 // ------------------------------------------------------------------------------------------------------------------
 // gdn_prep_kernel: 4 waves. Conv lane pt: rows 8 (pt / 32) .. + 7 of the chunk, channels 4 (pt % 32) .. + 3 of each
-// of q, k and v. q^ and v^ go straight from registers to the image; k^ (the operand of A = k^ k^T) and T diag(beta)
-// are built in LDS and copied out with the gate vectors. Wave 3 also forms the gates, the diagonal blocks of A and
-// their forward substitution; waves 0..2 the six below-diagonal blocks of A and then one block column of T each.
+// of q, k and v; q^, k^, k^T and v^T go to LDS. Wave 3 forms the gates, the diagonal blocks of A and their forward
+// substitution; waves 0..2 the six below-diagonal blocks of A and then one block column of T each. The products
+// are then spread over the four waves and written to the image straight from registers.
 constexpr int kPW = 4, kPT = 64 * kPW;
 constexpr int kPRG = 8;  // rows per conv lane
 constexpr int kPG = kPW - 1;
 
 struct PrepLds {
-  _Float16 Ks[kCH * kQP];
-  _Float16 Tb[kCH * kTP];
-  float eg[kCH], ed[kCH], gc[kCH], rowf[kCH], colf[3][kCH];  // as in Img, in the same order
-  float Tm[kCH * kAP];     // A, then T (fp32)
-  float cw[12][32][kKC];   // conv taps: channel 4 g + c of q (c < 4), k (4 <= c < 8), v (c >= 8) at cw[c][g]
-  float bt[kCH];           // beta
-  float brow[kCH];         // beta_t rowf_t
+  _Float16 Qs[kCH * kQP];   // q^ / sqrt(DK), [t][i]
+  _Float16 Ks[kCH * kQP];   // k^, [t][i]
+  _Float16 KT[kDK * kTP];   // k^ transposed, [i][t], swizzled by kt16
+  _Float16 VT[kDV * kTP];   // v^ transposed, [j][t], swizzled by vt16
+  _Float16 Tb[kCH * kTP];   // T diag(beta), [t][t'] (blocks above the diagonal zero)
+  _Float16 Tw[kCH * kTP];   // T diag(beta e^gc)
+  float eg[kCH], ed[kCH], gc[kCH], rowf[kCH], colf[3][kCH];
+  float bt[kCH];            // beta
+  float brow[kCH];          // beta_t rowf_t
+  union {
+    float cw[12][32][kKC];  // conv taps: channel 4 g + c of q (c < 4), k (4 <= c < 8), v (c >= 8) at cw[c][g]
+    float Tm[kCH * kAP];    // A, then T (fp32), after the conv
+  };
 };
-static_assert(offsetof(PrepLds, colf) + sizeof(float) * 3 * kCH - offsetof(PrepLds, eg) ==
-                  offsetof(Img, colf) + sizeof(float) * 3 * kCH - offsetof(Img, eg),
-              "gate vectors are copied as one block");
 
 template <typename T>
 __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
@@ -79,7 +101,8 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
   const unsigned rowb = (unsigned)a.stride * sizeof(T);
   const char* const seq_in = (const char*)a.in + (size_t)b * a.L * rowb;
-  char* const dst = (char*)a.img + ((size_t)bh * a.img_chunks + c) * kChunkScratch;
+  char* const slot = (char*)a.img + ((size_t)bh * a.img_chunks + c) * kChunkScratch;
+  const ImgOut img(slot);
 
   const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
   const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
@@ -112,23 +135,37 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
     ga = (float)grow[aoff];
     gb = (float)grow[boff];
   }
+  // z for the gate factors: thread (w, lane) takes the recurrence's block (w, tb, jj) lane `lane`: row 16 tb + c16
+  // (rows outside [P, P + L) clamped: their outputs are never stored), columns 32 w + 16 jj + 4 grp .. + 3
+  f4 zr[4][2];
+  if (a.gnorm) {
+    const int lane = tid0 & 63, grp = lane >> 4, c16 = lane & 15;
+    const gptr<T> zb = gp<T>(seq_in) + a.C + h * kDV + 32 * w + 4 * grp;
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) {
+      const int rr = min(max(cs + 16 * tb + c16 - a.P, 0), a.L - 1);
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) zr[tb][jj] = ld4(zb + (size_t)rr * a.stride + 16 * jj);
+    }
+  }
   // conv taps to LDS, behind the row loads
   for (int i = tid0; i < 3 * 128 * kKC; i += kPT) {
     const int lc = i / kKC, j = i % kKC, part = lc >> 7;
     const int ch = part * a.H * kDK + h * kDK + (lc & 127);
     sm.cw[(lc & 3) + 4 * part][(lc & 127) >> 2][j] = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
   }
-  // blocks above the diagonal of T diag(beta) are read by full 32-wide K blocks and never written otherwise:
-  // row block rb (< 3) has 6 - 2 rb such 8-column groups per row, from column 16 (rb + 1)
+  // blocks above the diagonal of T diag(beta) and T diag(beta e^gc) are read by full 32-wide K blocks and never
+  // written otherwise: row block rb (< 3) has 6 - 2 rb such 8-column groups per row, from column 16 (rb + 1)
   if (tid0 < 192) {
     const int k = tid0, rb = k < 96 ? 0 : k < 160 ? 1 : 2, k2 = k - (rb == 0 ? 0 : rb == 1 ? 96 : 160);
     const int ng = 6 - 2 * rb, t = 16 * rb + k2 / ng, g = k2 % ng + 2 * (rb + 1);
     *reinterpret_cast<h8*>(sm.Tb + t * kTP + 8 * g) = h8{};
+    *reinterpret_cast<h8*>(sm.Tw + t * kTP + 8 * g) = h8{};
   }
   __syncthreads();  // conv taps visible
 
   // conv + SiLU; q and k rows l2-normalised (q also scaled by 1/sqrt(DK); a row's 128 channels of q, of k, sit in
-  // the 32 lanes of a half wave): q^ to the image, k^ to LDS; v^ columns (8 rows each) to the image's v^T
+  // the 32 lanes of a half wave): q^ and k^ rows to LDS, k^ and v^ columns (8 rows each) to the transposed tiles
   {
     float u[kPRG][12], ssq[kPRG], ssk[kPRG];
 #pragma unroll
@@ -149,34 +186,30 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
           ssk[r] = fmaf(u[r][k], u[r][k], ssk[r]);
       }
     }
+    float rkv[kPRG];
 #pragma unroll
     for (int r = 0; r < kPRG; r++) {
       float sq = row_sum16(ssq[r]), sk = row_sum16(ssk[r]);
       sq += __shfl_xor(sq, 16);
       sk += __shfl_xor(sk, 16);
       const float rq = rsqrtf(sq + 1e-6f) * qscale, rk = rsqrtf(sk + 1e-6f);
+      rkv[r] = rk;
       const int t = kPRG * rg + r;
-      *(__attribute__((address_space(1))) h4*)(dst + offsetof(Img, Qs) + 2 * (size_t)(t * kQP + 4 * cl)) =
+      *reinterpret_cast<h4*>(sm.Qs + t * kQP + 4 * cl) =
           h4{(_Float16)(u[r][0] * rq), (_Float16)(u[r][1] * rq), (_Float16)(u[r][2] * rq), (_Float16)(u[r][3] * rq)};
       *reinterpret_cast<h4*>(sm.Ks + t * kQP + 4 * cl) =
           h4{(_Float16)(u[r][4] * rk), (_Float16)(u[r][5] * rk), (_Float16)(u[r][6] * rk), (_Float16)(u[r][7] * rk)};
     }
 #pragma unroll
     for (int cc = 0; cc < 4; cc++) {
-      h8 vt;
+      h8 kt, vt;
 #pragma unroll
-      for (int r = 0; r < kPRG; r++) vt[r] = (_Float16)u[r][8 + cc];
-      *(__attribute__((address_space(1))) h8*)(dst + offsetof(Img, VT) + 2 * (size_t)vt16(4 * cl + cc, rg)) = vt;
-    }
-  }
-  // z of rows 8 rg .. + 7 (this lane's 4 channels) for the gate factors, in flight behind the work below; rows
-  // outside [P, P + L) are clamped (their outputs are never stored)
-  float zr[kPRG][4];
-  if (a.gnorm) {
-#pragma unroll
-    for (int r = 0; r < kPRG; r++) {
-      const int rr = min(max(cs + kPRG * rg + r - a.P, 0), a.L - 1);
-      load4(gp<T>(seq_in) + (size_t)rr * a.stride + a.C + h * kDV + 4 * cl, zr[r]);
+      for (int r = 0; r < kPRG; r++) {
+        kt[r] = (_Float16)(u[r][4 + cc] * rkv[r]);
+        vt[r] = (_Float16)u[r][8 + cc];
+      }
+      *reinterpret_cast<h8*>(sm.KT + kt16(4 * cl + cc, rg)) = kt;
+      *reinterpret_cast<h8*>(sm.VT + vt16(4 * cl + cc, rg)) = vt;
     }
   }
   // gates: beta, the cumulative log decay (lane = row) and the vectors derived from it
@@ -207,7 +240,7 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
       sm.colf[i - 1][lane] = lane < 16 * i ? __expf(gi - gcr) : 0.0f;
     }
   }
-  __syncthreads();
+  __syncthreads();  // q^, k^, k^T, v^T, gates; the taps are dead (Tm reuses them)
 
   const int lane = tid0 & 63, grp = lane >> 4, c16 = lane & 15;
   if (w == kPG) {
@@ -247,11 +280,12 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
       for (int j = 0; j < r; j++) acc = fmaf(-ar[j], pc[j], acc);
       pc[r] = acc;
     }
-    const float cb = sm.bt[base + c16];
+    const float cb = sm.bt[base + c16], cw = cb * sm.eg[base + c16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       sm.Tm[(base + r) * kAP + base + c16] = pc[r];
       sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cb);
+      sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cw);
     }
   } else {
     // below-diagonal blocks of A: tiles 1,3,4,6,7,8 of the 10 on or below the diagonal, two per wave
@@ -275,361 +309,379 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
   }
   __syncthreads();
   if (w == 0)
-    t_column<0, false>(sm, grp, c16);
+    t_column<0, true>(sm, grp, c16);
   else if (w == 1)
-    t_column<1, false>(sm, grp, c16);
+    t_column<1, true>(sm, grp, c16);
   else if (w == 2)
-    t_column<2, false>(sm, grp, c16);
-  __syncthreads();
+    t_column<2, true>(sm, grp, c16);
+  __syncthreads();  // T diag(beta), T diag(beta e^gc) complete
 
-  if (a.gnorm) {
-    const f4 gw = ld4(gp<float>(a.gnorm) + 4 * cl);
+  const int lo16 = 16 * lane;
+  // W^T = k^T (T diag(beta e^gc))^T: tiles (ib, tb), ib in {2w, 2w+1}: lane holds W[16 tb + c16][16 ib + 4 grp + e],
+  // so the tile pair (2w, 2w+1) of one tb is W's A-operand block (tb, kb = w). T is lower triangular: the second
+  // K block (chunk rows 32..63) only contributes to tb >= 2.
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++) {
-      float* g = (float*)(dst + kImg) + (size_t)(4 * cl + cc) * kCH + kPRG * rg;
-      f4 lo, hi;
+  for (int tb = 0; tb < 4; tb++) {
+    f4 d[2];
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        lo[r] = gw[cc] * silu(zr[r][cc]);
-        hi[r] = gw[cc] * silu(zr[r + 4][cc]);
+    for (int k = 0; k < 2; k++) {
+      const int i = 16 * (2 * w + k) + c16;
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        if (kb == 1 && tb < 2) continue;
+        const h8 av = *reinterpret_cast<const h8*>(sm.KT + kt16(i, 4 * kb + grp));
+        const h8 bv = *reinterpret_cast<const h8*>(sm.Tw + (16 * tb + c16) * kTP + 32 * kb + 8 * grp);
+        acc = mfma16(av, bv, acc);
       }
-      store4(gpw<float>(g), lo);
-      store4(gpw<float>(g + 4), hi);
+      d[k] = acc;
+    }
+    img.st16(kOffW + (tb * 4 + w) * kBlk + lo16, join(d[0], d[1]));
+  }
+  // U = T diag(beta) v^: tiles (tb, jt), jt in {2w, 2w+1}, in the D layout
+#pragma unroll
+  for (int tb = 0; tb < 4; tb++) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int jt = 2 * w + k;
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        if (kb == 1 && tb < 2) continue;
+        const h8 av = *reinterpret_cast<const h8*>(sm.Tb + (16 * tb + c16) * kTP + 32 * kb + 8 * grp);
+        const h8 bv = *reinterpret_cast<const h8*>(sm.VT + vt16(16 * jt + c16, 4 * kb + grp));
+        acc = mfma16(av, bv, acc);
+      }
+      img.st8(kOffU + (tb * 8 + jt) * 512 + 8 * lane,
+              h4{(_Float16)acc[0], (_Float16)acc[1], (_Float16)acc[2], (_Float16)acc[3]});
     }
   }
-  // k^, T diag(beta) and the gate vectors out, 16 bytes per lane per step
-  auto copy_out = [&](size_t img_off, const void* from, int bytes) {
-    for (int i = tid0; i < bytes / 16; i += kPT)
-      *(__attribute__((address_space(1))) f4*)(dst + img_off + 16 * (size_t)i) =
-          *reinterpret_cast<const f4*>((const char*)from + 16 * i);
-  };
-  copy_out(offsetof(Img, Ks), sm.Ks, (int)sizeof(sm.Ks));
-  copy_out(offsetof(Img, Tb), sm.Tb, (int)sizeof(sm.Tb));
-  copy_out(offsetof(Img, eg), sm.eg, (int)(sizeof(Img) - offsetof(Img, eg)));
+  // Att^T = k^ q^T, decay-masked: tile (a, tb) holds Att[16 tb + c16][16 a + 4 grp + e]; Att block (tb, kb) is the
+  // tile pair a = 2 kb, 2 kb + 1 (a tile above the diagonal, a > tb, is zero). The six blocks that are read:
+  // wave 0: (0,0) and (2,1); wave 1: (1,0); wave 2: (2,0); wave 3: (3,0) and (3,1).
+  {
+    auto att_tile = [&](int ta, int tb) {
+      const _Float16* ab = sm.Ks + (16 * ta + c16) * kQP + 8 * grp;
+      const _Float16* bb = sm.Qs + (16 * tb + c16) * kQP + 8 * grp;
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++)
+        acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
+      const int t = 16 * tb + c16, tp0 = 16 * ta + 4 * grp;
+      const float gt = sm.gc[t];
+      const f4 gp4 = lds4(&sm.gc[tp0]);
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[e] = tp0 + e <= t ? acc[e] * __expf(fminf(gt - gp4[e], 0.0f)) : 0.0f;
+      return acc;
+    };
+    const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto att_block = [&](int tb, int kb) {
+      const f4 lo = att_tile(2 * kb, tb);
+      const f4 hi = 2 * kb + 1 <= tb ? att_tile(2 * kb + 1, tb) : z4;
+      img.st16(kOffA + (tb * 2 + kb) * kBlk + lo16, join(lo, hi));
+    };
+    if (w == 0) {
+      att_block(0, 0);
+      att_block(2, 1);
+    } else if (w == 1) {
+      att_block(1, 0);
+    } else if (w == 2) {
+      att_block(2, 0);
+    } else {
+      att_block(3, 0);
+      att_block(3, 1);
+    }
+  }
+  // q~ blocks (tb = w, kb 0..3): q^ rows scaled by e^gc, K in the permuted order
+  {
+    const int t = 16 * w + c16;
+    const float eg = sm.eg[t];
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++) {
+      const h8 q = perm_a(sm.Qs, kQP, t, kb, grp);
+      h8 o;
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[e] = (_Float16)((float)q[e] * eg);
+      img.st16(kOffQ + (w * 4 + kb) * kBlk + lo16, o);
+    }
+  }
+  // K~^T blocks (ib in {2w, 2w+1}, kb 0..1): k^ columns with chunk row t scaled by e^(gc_63 - gc_t)
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int i = 16 * (2 * w + k) + c16;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      const h8 kv = perm_a_kt(sm.KT, i, kb, grp);
+      const f4 dlo = lds4(&sm.ed[32 * kb + 4 * grp]), dhi = lds4(&sm.ed[32 * kb + 16 + 4 * grp]);
+      h8 o;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        o[e] = (_Float16)((float)kv[e] * dlo[e]);
+        o[4 + e] = (_Float16)((float)kv[4 + e] * dhi[e]);
+      }
+      img.st16(kOffK + ((2 * w + k) * 2 + kb) * kBlk + lo16, o);
+    }
+  }
+  if (tid0 == 0) img.st4(kOffS, sm.eg[kCH - 1]);
+  if (a.gnorm) {
+    const f4 gw0 = ld4(gp<float>(a.gnorm) + 32 * w + 4 * grp), gw1 = ld4(gp<float>(a.gnorm) + 32 * w + 16 + 4 * grp);
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) {
+        const f4 gw = jj ? gw1 : gw0;
+        f4 g;
+#pragma unroll
+        for (int e = 0; e < 4; e++) g[e] = gw[e] * silu(zr[tb][jj][e]);
+        store4(gpw<float>(slot + kImg + ((w * 4 + tb) * 2 + jj) * kBlk + lo16), g);
+      }
+  }
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// gdn_recur_kernel: 8 waves; wave w owns value columns 16 w .. 16 w + 15 of the fp32 state (MFMA D layout:
-// S[it][e] = S[16 it + 4 grp + e][16 w + c16]) and all of every chunk's work for them. Per period p, two segments:
-//   A: chunk p's state work (k^ S, V_new, q^ S, o, the state update, the gated-norm row partials); the DMA of image
-//      p+1 into the other image buffer is issued at its start
-//   B: chunk p's gated norm and output store; k^T and the masked scores of chunk p+1; z of p+1
-constexpr int kRW = 8, kRT = 64 * kRW;
+// gdn_chain_kernel: 4 waves; wave w owns value columns 32 w .. 32 w + 31 of the fp32 state (MFMA D layout:
+// S[ib][jj][e] = S[16 ib + 4 grp + e][32 w + 16 jj + c16]). Per period p (chunk p, image in LDS buffer p & 1):
+//   the DMA of image p+1 into the other buffer and the z rows of chunk p+1, issued first;
+//   X = W S (eight accumulator chains) and the first half of o^T = S^T q~^T, both from the packed state Sb;
+//   V_new = U - X; the state update S <- e^(gc_63) S + K~^T V_new (complete chunks), the dependent chain into the
+//   next chunk; o^T += V_new^T Att^T; the gated norm's factors w SiLU(z) in the shadow of those MFMAs;
+//   the 32-column row partials of the gated norm to LDS; barrier; 1/rms per row, output; wait for this wave's loads;
+//   barrier.
+// o is computed transposed (o^T = S^T q~^T + V_new^T Att^T: the packed state and V_new serve as A operands with the
+// same permuted K order in which they serve as B operands, and the image blocks of q~ and Att as B operands), so a
+// lane holds 4 consecutive value columns of one row: z loads and output stores are 16-byte accesses.
+constexpr int kCW = 4, kCT = 64 * kCW;
 
-// One halving step of a transposed 16-lane reduction over v[0 .. 2N): a lane whose selection bit is clear keeps the
-// low half v[0 .. N), otherwise the high half, adds the partner's copy (DPP control CTRL) and leaves it in v[0 .. N).
-template <int N, int CTRL>
-__device__ __forceinline__ void halve(float* v, int hi) {
-#pragma unroll
-  for (int i = 0; i < N; i++) {
-    const float keep = hi ? v[N + i] : v[i], send = hi ? v[i] : v[N + i];
-    v[i] = keep + DPP_F(send, CTRL);
-  }
-}
-
-struct RecLds {
+struct ChainLds {
   unsigned char img[2][kImg];  // chunk images; chunk p in img[p & 1]
-  _Float16 KT[kDK * kTP];      // k^ transposed, [i][t], 8-column groups swizzled by kt16
-  _Float16 Att[kCH * kTP];     // decay-masked causal q^ k^T, [t][t']
-  float red[kCH * kRW];        // gated-norm partial sums, [t][wave]
-  float inv[kRW][kCH];         // per wave: 1 / rms of each row
+  float red[kCH * kCW];        // gated-norm partial sums, [t][wave]
 };
 
+__device__ __forceinline__ h8 lds16(const unsigned char* p) { return *reinterpret_cast<const h8*>(p); }
+
+// sum of x over the four lanes c16, c16 + 16, c16 + 32, c16 + 48 (v_permlane16_swap pairs rows 2r and 2r + 1,
+// v_permlane32_swap the two halves); every lane gets the same bits
+__device__ __forceinline__ float sum_col4(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+  x = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+  return __builtin_bit_cast(float, (unsigned)q[0]) + __builtin_bit_cast(float, (unsigned)q[1]);
+}
+
 template <typename T>
-__global__ __launch_bounds__(kRT) void gdn_recur_kernel(GdnArgs a) {
+__global__ __launch_bounds__(kCT) void gdn_chain_kernel(GdnArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[];
-  RecLds& sm = *reinterpret_cast<RecLds*>(lds_raw);
+  ChainLds& sm = *reinterpret_cast<ChainLds*>(lds_raw);
   const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
   const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
   const int end = a.P + a.L;
   const int nchunks = (a.L + (a.P - a.s0) + kCH - 1) / kCH;
-  const unsigned rowb = (unsigned)a.stride * sizeof(T);
-  const unsigned orowb = (unsigned)(a.H * kDV) * sizeof(T);
-  const char* const seq_in = (const char*)a.in + (size_t)b * a.L * rowb;
   const char* const imgs = (const char*)a.img + (size_t)bh * a.img_chunks * kChunkScratch;
   const size_t sbase = ((size_t)b * a.H + h) * kDK * kDV;
+  const int ostride = a.H * kDV;
 
-  for (int idx = tid0; idx < kCH * kCH; idx += kRT) {
-    const int t = idx >> 6, tp = idx & 63;
-    if ((tp >> 4) > (t >> 4)) sm.Att[t * kTP + tp] = (_Float16)0.0f;
-  }
-
-  // this wave's share of one chunk image: 1 KiB DMA instructions w, w + 8, ...
-  auto issue_img = [&](int p) {
+  // this wave's share of one chunk image, 1 KiB DMA instructions w, w + 4, ..., issued in three groups spread over
+  // the period (a wave that issues them all at once stalls until the memory pipeline has taken them)
+  auto issue_img = [&](int p, int part) {
     const char* src = imgs + (size_t)p * kChunkScratch;
     unsigned char* dst = sm.img[p & 1];
     const int ln = opaque(tid0) & 63;
-    for (int i = w; i < kImg / 1024; i += kRW)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + 1024 * (size_t)i + 16 * ln),
-                                       (__attribute__((address_space(3))) void*)(dst + 1024 * i), 16, 0, 0);
+    constexpr int kPer = (kImg / kBlk + 3 * kCW - 1) / (3 * kCW);
+    for (int k = part * kPer; k < (part + 1) * kPer; k++) {
+      const int i = w + kCW * k;
+      if (i < kImg / kBlk)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(src + kBlk * (size_t)i + 16 * ln),
+            (__attribute__((address_space(3))) void*)(dst + kBlk * i), 16, 0, 0);
+    }
   };
-  // gate factors of chunk q in the MFMA D layout of this lane's output: rows 16 ti + 4 grp .. +3, column 16 w + c16
-  f4 zq[4];
-  auto fetch_z = [&](int q) {
-    const int lane = opaque(tid0) & 63, grp = lane >> 4, c16 = lane & 15;
-    gptr<float> g = gp<float>(imgs + (size_t)q * kChunkScratch + kImg) + (size_t)(16 * w + c16) * kCH + 4 * grp;
+  // the gate factors of chunk q at this lane's (transposed) output positions, straight into registers
+  f4 zq[4][2], zn[4][2];
+  auto fetch_z = [&](f4 (*z)[2], int q) {
+    const int lane = opaque(tid0) & 63;
+    const gptr<float> g = gp<float>(imgs + (size_t)q * kChunkScratch + kImg) + (size_t)(w * 8) * (kBlk / 4) + 4 * lane;
 #pragma unroll
-    for (int ti = 0; ti < 4; ti++) zq[ti] = ld4(g + 16 * ti);
+    for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) z[tb][jj] = ld4(g + (size_t)(tb * 2 + jj) * (kBlk / 4));
   };
 
-  f4 S[8];
-  {
-    const int g0 = (tid0 & 63) >> 4, l16 = tid0 & 15;
+  const int lane0 = tid0 & 63, grp0 = lane0 >> 4, c160 = lane0 & 15;
+  f4 S[8][2];
 #pragma unroll
-    for (int it = 0; it < 8; it++)
+  for (int ib = 0; ib < 8; ib++)
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
-        S[it][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 16 * w + l16] : 0.0f;
-  }
-  // Drain these loads here: the compiler's wait counting merges the loop's entry state into every iteration, so a
-  // state load still outstanding at the loop head would make each period's first use of S wait for the image DMA
-  // issued just before it.
-  __builtin_amdgcn_s_waitcnt(0);
-
-  // chunk q's k^T and decay-masked scores (image q in LDS)
-  auto prep_chunk = [&](int q) {
-    const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
-    const Img& nx = *reinterpret_cast<const Img*>(sm.img[q & 1]);
-    // k^T from k^: items (channel i, 8-row group g8), two per lane
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int item = tid + kRT * k, i = item & 127, g8 = item >> 7;
-      h8 v;
-#pragma unroll
-      for (int r = 0; r < 8; r++) v[r] = nx.Ks[(8 * g8 + r) * kQP + i];
-      *reinterpret_cast<h8*>(sm.KT + kt16(i, g8)) = v;
-    }
-    // decay-masked causal scores q^ k^T: tiles w and, for waves 0 and 1, w + 8 of the 10 on or below the diagonal
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int jt = w + 8 * k;
-      if (jt < 10) {
-        const int ti = jt >= 6 ? 3 : jt >= 3 ? 2 : jt >= 1 ? 1 : 0, tj = jt - ti * (ti + 1) / 2;
-        const _Float16* ab = nx.Qs + (16 * ti + c16) * kQP + 8 * grp;
-        const _Float16* bb = nx.Ks + (16 * tj + c16) * kQP + 8 * grp;
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-          acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
-        const int tp = 16 * tj + c16, t0 = 16 * ti + 4 * grp;
-        if (ti != tj) {
-          const float cf = nx.colf[ti - 1][tp];
-          const f4 rf = lds4(&nx.rowf[t0]);
-#pragma unroll
-          for (int e = 0; e < 4; e++) sm.Att[(t0 + e) * kTP + tp] = (_Float16)(acc[e] * rf[e] * cf);
-        } else {
-          const float gp_ = nx.gc[tp];
-          const f4 gt = lds4(&nx.gc[t0]);
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int t = t0 + e;
-            const float dec = __expf(fminf(gt[e] - gp_, 0.0f));
-            sm.Att[t * kTP + tp] = (_Float16)(tp <= t ? acc[e] * dec : 0.0f);
-          }
-        }
-      }
-    }
-  };
-
-  // prologue: chunk 0's image, then its k^T and scores. The loop is entered with only z loads in flight, which
-  // nothing in segment A overwrites, so no wait in A depends on the DMA issued at its start.
-  issue_img(0);
+        S[ib][jj][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * ib + 4 * grp0 + e) * kDV + 32 * w + 16 * jj + c160]
+                              : 0.0f;
+  issue_img(0, 0);
+  issue_img(0, 1);
+  issue_img(0, 2);
+  if (a.gnorm) fetch_z(zq, 0);
+  // Drain the prologue's loads: the compiler's wait counting merges the loop's entry state into every iteration,
+  // so a load still outstanding at the loop head would make each period's first use of it wait for the DMA issued
+  // just before.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  prep_chunk(0);
-  if (a.gnorm) fetch_z(0);
-  __syncthreads();
+
   for (int p = 0; p < nchunks; p++) {
     const int c0 = a.s0 + kCH * p;
-    f4 O[4];
     const int m = min(kCH, end - c0);
     const bool full = m == kCH;
     const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
-    const int col = 16 * w + c16;
+    const int lo16 = 16 * lane;
+    const bool more = p + 1 < nchunks;
+    if (more) issue_img(p + 1, 0);
+    // z of the next chunk, every period (past the last chunk on the last chunk's rows, never used): conditional
+    // loads would make the loop-carried registers a merge of old and new values, resolved with early waits
+    if (a.gnorm) fetch_z(zn, min(p + 1, nchunks - 1));
+    const unsigned char* im = sm.img[p & 1];
 
-    // ---- A: chunk p ----
-    {
-      // The MFMA work runs in groups; the LDS operands of each group are read while the previous group's MFMAs
-      // issue. An empty asm that takes a group's B operand and clobbers memory sits after the next group's reads,
-      // so those reads are issued before the group's MFMAs without waiting for them, and a scheduling barrier
-      // after the MFMAs keeps the reads of the group after next from being hoisted above them.
-      if (p + 1 < nchunks) issue_img(p + 1);
-      const Img& im = *reinterpret_cast<const Img*>(sm.img[p & 1]);
-      // k^ S and q^ S, one 32-wide K block of the state per group, 8 accumulator chains
-      h8 Aq[2][8];
-      auto read_kq = [&](h8* A, int kb) {
+    // the state as f16 operands: Sb[kb][jj] holds state rows {32 kb + 4 grp + e} U {32 kb + 16 + 4 grp + e} of
+    // column 32 w + 16 jj + c16 (B operand of W S; A operand, as S^T, of S^T q~^T)
+    h8 Sb[4][2];
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-          A[ti] = perm_a(im.Ks, kQP, 16 * ti + c16, kb, grp);
-          A[4 + ti] = perm_a(im.Qs, kQP, 16 * ti + c16, kb, grp);
-        }
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) Sb[kb][jj] = pack_b(S[2 * kb][jj], S[2 * kb + 1][jj]);
+    // X = W S first (it feeds the dependent chain), then o^T = S^T q~^T; each K block's operands are read while
+    // the previous block's MFMAs issue
+    f4 X[4][2], O[2][4];
+    const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    {
+      h8 wa[2][4];
+      auto read_w = [&](int s, int kb) {
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) wa[s][tb] = lds16(im + kOffW + (tb * 4 + kb) * kBlk + lo16);
       };
-      read_kq(Aq[0], 0);
-      f4 KS[4];
-      h8 tb[4][2];
-      h4 vlo[2], vhi[2];
-      f4 eg4[4];
+      read_w(0, 0);
 #pragma unroll
       for (int kb = 0; kb < 4; kb++) {
-        if (kb < 3) {
-          read_kq(Aq[(kb + 1) & 1], kb + 1);
-        } else {
-          // V_new operands: rows of T diag(beta) in the permuted K order, this column's v^ rows in the same order
-          // (rows 32 k2 + 4 grp .. +3 and 32 k2 + 16 + 4 grp .. +3), e^gc of this lane's D-layout rows
+        if (kb < 3) read_w((kb + 1) & 1, kb + 1);
+        asm volatile("" : "+v"(Sb[kb][0]), "+v"(Sb[kb][1])::"memory");
 #pragma unroll
-          for (int ti = 0; ti < 4; ti++) {
+        for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int k2 = 0; k2 <= (ti >> 1); k2++) tb[ti][k2] = perm_a(im.Tb, kTP, 16 * ti + c16, k2, grp);
-            eg4[ti] = lds4(&im.eg[16 * ti + 4 * grp]);
-          }
-#pragma unroll
-          for (int k2 = 0; k2 < 2; k2++) {
-            vlo[k2] = *reinterpret_cast<const h4*>(im.VT + vt16(col, 4 * k2 + (grp >> 1)) + 4 * (grp & 1));
-            vhi[k2] = *reinterpret_cast<const h4*>(im.VT + vt16(col, 4 * k2 + 2 + (grp >> 1)) + 4 * (grp & 1));
-          }
-        }
-        h8 S16 = pack_b(S[2 * kb], S[2 * kb + 1]);
-        asm volatile("" : "+v"(S16)::"memory");
-#pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-          const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
-          KS[ti] = mfma16(Aq[kb & 1][ti], S16, kb ? KS[ti] : z4);
-          O[ti] = mfma16(Aq[kb & 1][4 + ti], S16, kb ? O[ti] : z4);
-        }
+          for (int jj = 0; jj < 2; jj++) X[tb][jj] = mfma16(wa[kb & 1][tb], Sb[kb][jj], kb ? X[tb][jj] : z4);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // V_new = T diag(beta) (v - diag(e^gc) k^ S): the bracket is formed in fp32 in the D layout of k^ S and
-      // rounded once to f16 as the B operand
-      h8 Bv[2];
+      if (more) issue_img(p + 1, 1);
+      h8 qa[2][4];
+      auto read_q = [&](int s, int kb) {
 #pragma unroll
-      for (int k2 = 0; k2 < 2; k2++) {
-        const f4 lo = f4{(float)vlo[k2][0], (float)vlo[k2][1], (float)vlo[k2][2], (float)vlo[k2][3]} - eg4[2 * k2] * KS[2 * k2];
-        const f4 hi = f4{(float)vhi[k2][0], (float)vhi[k2][1], (float)vhi[k2][2], (float)vhi[k2][3]} - eg4[2 * k2 + 1] * KS[2 * k2 + 1];
-        Bv[k2] = pack_b(lo, hi);
-      }
-      f4 Vn[4];
+        for (int tb = 0; tb < 4; tb++) qa[s][tb] = lds16(im + kOffQ + (tb * 4 + kb) * kBlk + lo16);
+      };
+      read_q(0, 0);
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++) {
-        f4 u = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int kb = 0; kb < 4; kb++) {
+        if (kb < 3) read_q((kb + 1) & 1, kb + 1);
+        asm volatile("" ::: "memory");
 #pragma unroll
-        for (int k2 = 0; k2 <= (ti >> 1); k2++) u = mfma16(tb[ti][k2], Bv[k2], u);
-        Vn[ti] = u;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // o = e^gc (q^ S) + scores V_new
-      {
-        h8 att[4][2];
+        for (int jj = 0; jj < 2; jj++)
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-          att[ti][0] = perm_a(sm.Att, kTP, 16 * ti + c16, 0, grp);
-          if (ti >= 2) att[ti][1] = perm_a(sm.Att, kTP, 16 * ti + c16, 1, grp);
-        }
-        const h8 Vb0 = pack_b(Vn[0], Vn[1]), Vb1 = pack_b(Vn[2], Vn[3]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-          O[ti] = mfma16(att[ti][0], Vb0, O[ti] * eg4[ti]);
-          if (ti >= 2) O[ti] = mfma16(att[ti][1], Vb1, O[ti]);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (full) {
-        // rows of V_new scaled by e^(gl - gc_t), then S <- e^gl S + k^T (scaled V_new), in two halves of the rows
-        // of S; the second half's k^T operands are read behind the first half's MFMAs
-        h8 kt[2][4][2];
-        auto read_kt = [&](h8 (*K)[2], int half) {
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int it = 4 * half + i;
-            K[i][0] = perm_a_kt(sm.KT, 16 * it + c16, 0, grp);
-            K[i][1] = perm_a_kt(sm.KT, 16 * it + c16, 1, grp);
-          }
-        };
-        read_kt(kt[0], 0);
-#pragma unroll
-        for (int ti = 0; ti < 4; ti++) Vn[ti] *= lds4(&im.ed[16 * ti + 4 * grp]);
-        h8 Vd0 = pack_b(Vn[0], Vn[1]), Vd1 = pack_b(Vn[2], Vn[3]);
-        const float el = im.eg[kCH - 1];
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-          if (half == 0) read_kt(kt[1], 1);
-          asm volatile("" : "+v"(Vd0), "+v"(Vd1)::"memory");
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int it = 4 * half + i;
-            S[it] = mfma16(kt[half][i][1], Vd1, mfma16(kt[half][i][0], Vd0, S[it] * el));
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-      if (a.gnorm) {
-        // This wave's 16-column partial of the sum of squares of each of its 16 rows, reduced over the 16 lanes of
-        // a DPP row by halving: at each step a lane keeps the half of its values selected by one lane bit, adds the
-        // partner lane's copy of that half, and passes on the other half. The partners are the row mirror (lane
-        // 15 - i), the half-row mirror (7 - i), then i ^ 2 and i ^ 1; each keeps the bits already used for selection,
-        // so partners always hold the same index set. Lane c16 ends with value index c16 = 4 ti + e.
-        float v[16];
-#pragma unroll
-        for (int ti = 0; ti < 4; ti++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) v[4 * ti + e] = O[ti][e] * O[ti][e];
-        halve<8, 0x140>(v, c16 & 8);
-        halve<4, 0x141>(v, c16 & 4);
-        halve<2, 0x4E>(v, c16 & 2);
-        halve<1, 0xB1>(v, c16 & 1);
-        sm.red[(16 * (c16 >> 2) + 4 * grp + (c16 & 3)) * kRW + w] = v[0];
+          for (int tb = 0; tb < 4; tb++) O[jj][tb] = mfma16(Sb[kb][jj], qa[kb & 1][tb], kb ? O[jj][tb] : z4);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next image has landed
-    __syncthreads();                // B
-
-    // ---- B: chunk p's gated norm and store; k^T, scores and v conv of chunk p+1; z of p+1 ----
+    if (more) issue_img(p + 1, 2);
+    // V_new = U - X, kept in fp32 in the D layout and rounded once as an operand (K = chunk rows)
+    h8 Vb[2][2];
     {
-      float Y[4][4];
+      f4 Vn[4][2];
 #pragma unroll
-      for (int ti = 0; ti < 4; ti++)
+      for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) Y[ti][e] = O[ti][e];
-      if (a.gnorm) {
-        // lane t: row t's eight wave partials -> 1 / rms, through this wave's slot to the lanes that hold row t
-        const f4 r0 = lds4(&sm.red[lane * kRW]), r1 = lds4(&sm.red[lane * kRW + 4]);
-        sm.inv[w][lane] = rsqrtf((((r0[0] + r0[1]) + (r0[2] + r0[3])) + ((r1[0] + r1[1]) + (r1[2] + r1[3]))) / kDV + 1e-6f);
-        wave_sync();
-#pragma unroll
-        for (int ti = 0; ti < 4; ti++) {
-          const f4 iv = lds4(&sm.inv[w][16 * ti + 4 * grp]);
-#pragma unroll
-          for (int e = 0; e < 4; e++) Y[ti][e] = Y[ti][e] * iv[e] * zq[ti][e];
+        for (int jj = 0; jj < 2; jj++) {
+          const h4 u = *reinterpret_cast<const h4*>(im + kOffU + (tb * 8 + 2 * w + jj) * 512 + 8 * lane);
+          Vn[tb][jj] = f4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]} - X[tb][jj];
         }
-      }
-      __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * (a.H * kDV) + (size_t)h * kDV + col;
-      if (m == kCH && c0 >= a.P) {
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++)
+      for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) ob[(size_t)(c0 - a.P + 16 * ti + 4 * grp + e) * (a.H * kDV)] = (T)Y[ti][e];
-      } else {
+        for (int jj = 0; jj < 2; jj++) Vb[kb][jj] = pack_b(Vn[2 * kb][jj], Vn[2 * kb + 1][jj]);
+    }
+    // the state update (the dependent chain into the next chunk)
+    if (full) {
+      // all sixteen first-block products before any second-block one, so that no MFMA waits for its predecessor
+      const float eL = *reinterpret_cast<const float*>(im + kOffS);
+      h8 kt[8];
 #pragma unroll
-        for (int ti = 0; ti < 4; ti++)
+      for (int ib = 0; ib < 8; ib++) kt[ib] = lds16(im + kOffK + (ib * 2 + 0) * kBlk + lo16);
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int t = 16 * ti + 4 * grp + e, r = c0 + t;
-            if (t < m && r >= a.P) ob[(size_t)(r - a.P) * (a.H * kDV)] = (T)Y[ti][e];
-          }
+      for (int ib = 0; ib < 8; ib++)
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) S[ib][jj] = mfma16(kt[ib], Vb[0][jj], S[ib][jj] * eL);
+#pragma unroll
+      for (int ib = 0; ib < 8; ib++) kt[ib] = lds16(im + kOffK + (ib * 2 + 1) * kBlk + lo16);
+#pragma unroll
+      for (int ib = 0; ib < 8; ib++)
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) S[ib][jj] = mfma16(kt[ib], Vb[1][jj], S[ib][jj]);
+    }
+    // o^T += V_new^T Att^T (causal: the second K block only for row blocks 2 and 3)
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) {
+      const h8 a0 = lds16(im + kOffA + (tb * 2 + 0) * kBlk + lo16);
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) O[jj][tb] = mfma16(Vb[0][jj], a0, O[jj][tb]);
+      if (tb >= 2) {
+        const h8 a1 = lds16(im + kOffA + (tb * 2 + 1) * kBlk + lo16);
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) O[jj][tb] = mfma16(Vb[1][jj], a1, O[jj][tb]);
       }
     }
-    if (p + 1 < nchunks) prep_chunk(p + 1);
-    // The v and z loads run every period (past the last chunk on the last chunk's rows, never used): conditional
-    // loads would make the loop-carried registers a merge of old and new values, resolved with copies that wait
-    // for the loads right after they are issued.
-    if (a.gnorm) fetch_z(min(p + 1, nchunks - 1));
-    __syncthreads();  // A
+    if (a.gnorm) {
+      // row 16 tb + c16: this wave's 32-column sum of squares (8 values here, 4 lanes c16 + 16 g)
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) {
+        float v = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) v = fmaf(O[jj][tb][e], O[jj][tb][e], v);
+        v = sum_col4(v);
+        if (grp == tb) sm.red[(16 * tb + c16) * kCW + w] = v;
+      }
+    }
+    __syncthreads();
+    if (a.gnorm) {
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) {
+        const f4 r = lds4(&sm.red[(16 * tb + c16) * kCW]);
+        const float iv = rsqrtf(((r[0] + r[1]) + (r[2] + r[3])) / kDV + 1e-6f);
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) O[jj][tb] = O[jj][tb] * iv * zq[tb][jj];
+      }
+    }
+    {
+      __attribute__((address_space(1))) T* ob =
+          gpw<T>(a.out) + (size_t)b * a.L * ostride + (size_t)h * kDV + 32 * w + 4 * grp;
+#pragma unroll
+      for (int tb = 0; tb < 4; tb++) {
+        const int t = 16 * tb + c16, r = c0 + t;
+        if (t < m && r >= a.P) {
+          __attribute__((address_space(1))) T* orow = ob + (size_t)(r - a.P) * ostride;
+          store4(orow, O[0][tb]);
+          store4(orow + 16, O[1][tb]);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next image and the next z rows have landed
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) zq[tb][jj] = zn[tb][jj];
+    __syncthreads();
   }
-  const int g0 = (tid0 & 63) >> 4, l16 = tid0 & 15;
 #pragma unroll
-  for (int it = 0; it < 8; it++)
+  for (int ib = 0; ib < 8; ib++)
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-      gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 16 * w + l16] = S[it][e];
+    for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        gpw<float>(a.S_out)[sbase + (size_t)(16 * ib + 4 * grp0 + e) * kDV + 32 * w + 16 * jj + c160] = S[ib][jj][e];
 }
 
 template <typename T>
@@ -642,11 +694,11 @@ hipError_t launch(const GdnArgs& a, hipStream_t s) {
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kp, dim3(nchunks, a.B * a.H), dim3(kPT), sizeof(PrepLds), s, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  auto kr = gdn_recur_kernel<T>;
+  auto kr = gdn_chain_kernel<T>;
   e = hipFuncSetAttribute(reinterpret_cast<const void*>(kr), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)sizeof(RecLds));
+                          (int)sizeof(ChainLds));
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kr, dim3(a.B * a.H), dim3(kRT), sizeof(RecLds), s, a);
+  hipLaunchKernelGGL(kr, dim3(a.B * a.H), dim3(kCT), sizeof(ChainLds), s, a);
   return hipGetLastError();
 }
 
