@@ -11,7 +11,9 @@ Also reported, on the same line:
                 launch time from HIP events on the launch stream, against 8 TB/s
   roofline_gqa  the GQA layer: algorithmic MFMA flops / average layer time, against 2.5 PFLOP/s dense f16
   sweep         the stack at T = 8, 128, 512 (B = 8) and at T = 2048 with B = 1
-  cpu_baseline  the CPU oracle (oracle/, fp64) on the host cores for a bounded sample, scaled to the metric
+  cpu_baseline  a PyTorch CPU fp32 restatement of the same layers (oracle/torch_cpu.py: chunk-64 gated-delta,
+                F.conv1d(groups=C), explicit masked-softmax GQA) on the host cores, one full B=8, T=2048 layer of
+                each kind on the same PCG64 inputs as the GPU stack, scaled by the layer counts (18, 6)
   projections   the MatMulNBits projections either side of the path: per-forward time at M = 1 (HBM roofline)
                 and M = 2048 (MFMA roofline), with their own CPU baseline (the numpy oracle)
   torso         ms per whole torso forward (embedding to final norm, the reference torso's layer counts) at
@@ -83,11 +85,29 @@ def make_engine(ha, kinds, B, max_ctx, stream):
     return eng
 
 
-def make_buffers(torch, kinds, B, T, seed=0):
+def host_inputs(B, T, seed=0):
+    """One post-projection input per layer kind, NumPy PCG64 (synth.py, one stream per tensor): the rows every layer
+    of that kind reads in the headline stack, and the rows the CPU baseline runs on."""
+    import synth
+    return {"linear_attention": synth.gdn_rows(T, B, seed=seed), "full_attention": synth.gqa_rows(T, B, seed=seed)}
+
+
+def make_buffers(torch, kinds, B, T, seed=0, host=None):
+    """Device inputs and outputs for one forward. With `host` (host_inputs()), each kind's rows are uploaded once
+    and shared by all layers of that kind; otherwise every layer gets its own rows from torch's GPU generator."""
     g = torch.Generator(device="cuda:0")
     g.manual_seed(seed)
     ins, outs = [], []
+    shared = {}
+    if host is not None:
+        shared = {"linear_attention": torch.from_numpy(host["linear_attention"]).to("cuda:0"),
+                  "full_attention": torch.from_numpy(host["full_attention"]).to("cuda:0")}
     for k in kinds:
+        if k in shared:
+            ins.append(shared[k])
+            outs.append(torch.empty(B, T, H * DV if k == "linear_attention" else HQ * HD, device="cuda:0",
+                                    dtype=torch.float32 if k == "linear_attention" else torch.float16))
+            continue
         if k == "linear_attention":
             x = torch.zeros(B, T, STRIDE_LIN, device="cuda:0", dtype=torch.float32)
             x[:, :, :LIN_W] = torch.randn(B, T, LIN_W, device="cuda:0", generator=g)
@@ -114,34 +134,55 @@ def time_forwards(torch, eng, T, ins, outs, steps, warmup, stream):
     return wall, e0.elapsed_time(e1) / steps
 
 
-def cpu_baseline(T=2048, reps=2):
-    """The fp64 CPU oracle on a bounded sample: one gated-delta layer (sequential rule) and one GQA layer for one
-    sequence at T = 2048, median of `reps`; scaled to the metric (18 + 6 layers, 8 sequences)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    import oracle
+
+def cpu_baseline(host, B=8, T=2048, reps=3):
+    """PyTorch CPU fp32 restatement (oracle/torch_cpu.py) of one gated-delta and one GQA layer over the whole
+    B x T workload, on the same PCG64 rows the GPU stack reads; warm-up 1, median of `reps`, scaled by the layer
+    counts (18, 6). Threads: the host cores this process may use (OMP_NUM_THREADS caps it, as on the GPU box)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import torch
+
     import synth
-    x = synth.gdn_rows(T)[0]
-    p = synth.gdn_params()
-    xa = synth.gqa_rows(T)[0].astype(np.float32)
-    pa = synth.gqa_params()
-    rope = oracle.rope_table(4096, 64, 1e7)
+    import torch_cpu
+    cores = len(os.sched_getaffinity(0))
+    threads = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    torch.set_num_threads(threads)
+    x = torch.from_numpy(host["linear_attention"])
+    p = {k: torch.from_numpy(v) for k, v in synth.gdn_params(seed=0, layer=0).items()}
+    xa = torch.from_numpy(host["full_attention"])
+    pa = {k: torch.from_numpy(v) for k, v in synth.gqa_params(seed=0, layer=3).items()}
+    cos, sin = torch_cpu.rope_table(T)
     tg, ta = [], []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        oracle.gdn_forward(x, p, oracle.GdnState())
-        tg.append(time.perf_counter() - t0)
-        t0 = time.perf_counter()
-        oracle.gqa_forward(xa, pa, oracle.GqaCache(4096), rope)
-        ta.append(time.perf_counter() - t0)
+    with torch.no_grad():
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            torch_cpu.gdn_layer(x, p["conv"], p["neg_exp_A"], p["dt_bias"], p["gnorm"])
+            t1 = time.perf_counter()
+            torch_cpu.gqa_layer(xa, pa["q_norm"], pa["k_norm"], cos, sin)
+            t2 = time.perf_counter()
+            if r:
+                tg.append(t1 - t0)
+                ta.append(t2 - t1)
     tg, ta = sorted(tg)[len(tg) // 2], sorted(ta)[len(ta) // 2]
-    cores = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
-    ms = 8 * (18 * tg + 6 * ta) * 1e3
-    return {"value": round(ms, 1), "unit": "ms", "cores": cores, "kind": "port",
-            "sample": "oracle (C, fp64, OpenMP over heads) on 1 gated-delta layer (sequential rule) + 1 GQA layer, "
-                      "B=1, T=2048; median of %d; scaled x8 sequences x (18, 6) layers; per layer %.0f / %.0f ms"
-                      % (reps, tg * 1e3, ta * 1e3)}
+    ms = (18 * tg + 6 * ta) * 1e3
+    return {"value": round(ms, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "torch_threads": torch.get_num_threads(), "host_cores_visible": cores,
+            "tokens_per_s": round(B * T / (ms * 1e-3)),
+            "sample": "PyTorch %s CPU fp32 (oracle/torch_cpu.py): one gated-delta layer (chunk-64 WY form, "
+                      "F.conv1d(groups=C), gated RMSNorm) and one GQA layer (explicit masked softmax), each over "
+                      "the whole B=%d, T=%d workload on the GPU stack's PCG64 rows; warm-up 1, median of %d; "
+                      "per layer %.0f / %.0f ms; scaled x (18, 6) layers" % (torch.__version__, B, T, reps,
+                                                                           tg * 1e3, ta * 1e3)}
 
 
 # The model's int4 projection shapes (K, N) and how many of each one forward runs, as the reference's matmul
@@ -359,9 +400,10 @@ def main():
         print(json.dumps({"profile_kernel": args.profile_kernel, "B": B, "T": T, "steps": args.steps,
                           "ms_per_launch": (time.perf_counter() - t0) * 1e3 / args.steps}), flush=True)
         return
+    host = host_inputs(B, T)
     with torch.cuda.stream(stream):
         eng = make_engine(ha, KINDS, B, 4096, stream.cuda_stream)
-        ins, outs = make_buffers(torch, KINDS, B, T)
+        ins, outs = make_buffers(torch, KINDS, B, T, host=host)
         torch.cuda.synchronize()
         wall_ms, ev_ms = time_forwards(torch, eng, T, ins, outs, args.steps, args.warmup, stream)
         res = eng.forward(T, ins, outs, timestamps=True, layer_ms=True)
@@ -410,7 +452,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32 recurrence state + f16 MFMA operands (f32 accumulate); gated-delta rows f32, GQA rows f16",
-        "data": "synthetic: post-projection rows ~N(0,1) (torch GPU RNG), conv taps ~N(0,0.5^2), unit q/k norm gain",
+        "data": "synthetic: post-projection rows ~N(0,1) (NumPy PCG64, one input per layer kind shared by that "
+                "kind's layers), conv taps ~N(0,0.5^2), unit q/k norm gain",
         "config": {"workload": "24-layer hybrid stack (18 gated-delta + 6 GQA, 3:1), "
                                "B=8 sequences, T=2048, projections excluded",
                    "batch": B, "seq_len": T, "layers": len(KINDS), "gdn_recurrence": "chunked (64)"},
@@ -436,7 +479,7 @@ def main():
                                      "layers (the reference torso's counts) with norms, int4 projections and MLPs, "
                                      "final norm of the last row; random weights")
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"] = cpu_baseline(host, B, T)
         if "projections" in line:
             line["projections"]["cpu_baseline"] = mnb_cpu_baseline()
     print(json.dumps(line), flush=True)
