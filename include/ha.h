@@ -120,11 +120,14 @@ int ha_set_param(ha_engine* e, int layer, const char* name, const float* host, s
      layer_out[i]: [batch][L][H*DV] or [batch][L][HQ*HD] in that kind's dtype
    resume: continue from this snapshot (engine.js:325-327); NULL starts from an empty context
    keep:   if non-NULL, receives a new snapshot of the context after this call (engine.js:349-362)
-   Returns HA_ERR_CONTEXT if P + L > max_ctx. Layers run in order on the engine's stream. */
+   Returns HA_ERR_CONTEXT if P + L > max_ctx. Layers run in order on the engine's stream. No layer_out buffer may
+   overlap any layer_in buffer of the same call: the gated-delta layers' raw rows (conv history and replay rows) are
+   copied from layer_in after all layers have run. */
 int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* layer_out, const ha_snapshot* resume,
                ha_snapshot** keep, ha_forward_opts* opts);
 
-/* Snapshot queries. P is the number of tokens the snapshot covers (engine.js:352 snap.P). */
+/* Snapshot queries. P is the number of tokens the snapshot covers (engine.js:352 snap.P). Every snapshot entry point
+   looks the handle up among the live snapshots first: a destroyed or forged handle gives HA_ERR_HANDLE. */
 int ha_snapshot_tokens(const ha_snapshot* s, int* P);
 /* Position of the stored recurrent state (a multiple of 64 after chunked forwards, P after sequential ones) and
    the number of raw rows kept for replay and conv history, [state_pos - (conv_k-1), P). */

@@ -49,6 +49,10 @@ std::atomic<uint64_t> g_engine_ids{1};
 // outliving its engine (any order of release is allowed, e.g. under a garbage collector) never touches freed memory.
 std::mutex g_live_mu;
 std::unordered_set<const ha_engine*> g_live;
+// Snapshot handles that exist (created and not yet destroyed): every snapshot entry point looks a handle up here
+// before reading through it, so a destroyed handle is refused instead of read after it was freed.
+std::unordered_set<const ha_snapshot*> g_live_snaps;
+std::unordered_set<const void*> g_live_mnbs;  // MatMulNBits handles, likewise
 
 struct Layer {
   int kind = 0;
@@ -108,6 +112,11 @@ namespace {
 bool engine_ok(const ha_engine* e) {
   std::lock_guard<std::mutex> lock(g_live_mu);
   return e && g_live.count(e) && e->magic == kEngineMagic;
+}
+
+bool snap_ok(const ha_snapshot* s) {
+  std::lock_guard<std::mutex> lock(g_live_mu);
+  return s && g_live_snaps.count(s) && s->magic == kSnapMagic;
 }
 
 // The live engine that made a snapshot, or nullptr once that engine is gone.
@@ -206,6 +215,13 @@ struct ha_mnb {
   float* ws = nullptr;  // fp32 partial products of a split GEMM, grown on demand
   size_t ws_bytes = 0;
 };
+
+namespace {
+bool mnb_ok(const ha_mnb* w) {
+  std::lock_guard<std::mutex> lock(g_live_mu);
+  return w && g_live_mnbs.count(w) && w->magic == kMnbMagic;
+}
+}  // namespace
 
 extern "C" {
 
@@ -366,7 +382,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
     if (e->layers[i].kind != HA_ADAPTER && (!layer_in[i] || !layer_out[i]))
       return fail(HA_ERR_ARG, "layer " + std::to_string(i) + ": NULL input or output");
   if (resume) {
-    if (resume->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+    if (!snap_ok(resume)) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
     if (resume->owner != e || resume->owner_id != e->id) return fail(HA_ERR_HANDLE, "snapshot belongs to another engine");
     if (resume->released) return fail(HA_ERR_HANDLE, "snapshot was released");
     if ((int)resume->layers.size() != c.n_layers) return fail(HA_ERR_HANDLE, "snapshot layer count mismatch");
@@ -482,6 +498,10 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
           return bail(fail(HA_ERR_DEVICE, "snapshot copy failed"));
       }
     }
+    {
+      std::lock_guard<std::mutex> lock(g_live_mu);
+      g_live_snaps.insert(s);
+    }
     *keep = s;
   }
   if (timing || (opts && opts->sync)) {
@@ -496,21 +516,21 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
 }
 
 int ha_snapshot_tokens(const ha_snapshot* s, int* P) {
-  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (!snap_ok(s)) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
   if (!P) return fail(HA_ERR_ARG, "P is NULL");
   *P = s->P;
   return HA_OK;
 }
 
 int ha_snapshot_layout(const ha_snapshot* s, int* state_pos, int* tail_rows) {
-  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (!snap_ok(s)) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
   if (state_pos) *state_pos = s->s0;
   if (tail_rows) *tail_rows = s->tail_rows;
   return HA_OK;
 }
 
 int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* host, size_t bytes) {
-  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (!snap_ok(s)) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
   if (s->released) return fail(HA_ERR_HANDLE, "snapshot was released");
   if (!what || !host) return fail(HA_ERR_ARG, "what and host must be non-NULL");
   const ha_engine* e = snapshot_owner(s);
@@ -547,7 +567,7 @@ int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* ho
 }
 
 int ha_snapshot_release(ha_snapshot* s) {
-  if (!s || s->magic != kSnapMagic) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
+  if (!snap_ok(s)) return fail(HA_ERR_HANDLE, "invalid snapshot handle");
   if (s->released) return HA_OK;
   if (const ha_engine* e = snapshot_owner(s)) {
     (void)hipSetDevice(e->device);
@@ -561,6 +581,10 @@ int ha_snapshot_release(ha_snapshot* s) {
 int ha_snapshot_destroy(ha_snapshot* s) {
   int rc = ha_snapshot_release(s);
   if (rc) return rc;
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    g_live_snaps.erase(s);
+  }
   s->magic = kDeadMagic;
   delete s;
   return HA_OK;
@@ -627,6 +651,10 @@ int ha_mnb_create(int N, int K, const ha_mnb_format* fmt, const void* q, const v
   ha_mnb* w = new ha_mnb();
   w->args = a;
   w->device = device;
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    g_live_mnbs.insert(w);
+  }
   *out = w;
   return HA_OK;
 }
@@ -638,7 +666,7 @@ namespace {
 // ha_mnb_forward and ha_mnb_forward_noalloc: the same kernels and K split; they differ only in where a split
 // product's fp32 partials go (the handle's workspace, grown on demand, or the library's fixed per-device scratch).
 int mnb_forward(ha_mnb* w, int M, const void* a, void* y, void* stream, bool noalloc) {
-  if (!w || w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
+  if (!mnb_ok(w)) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
   if (M < 1 || !a || !y) return fail(HA_ERR_ARG, "M must be >= 1 and a, y non-NULL");
   if (w->args.N % 16) return fail(HA_ERR_ARG, "a matmul needs N % 16 == 0 (the exporter pads N to 64)");
   HA_HIP(hipSetDevice(w->device));
@@ -691,11 +719,16 @@ int ha_mnb_forward_noalloc(ha_mnb* w, int M, const void* a, void* y, void* strea
 
 int ha_mnb_destroy(ha_mnb* w) {
   if (!w) return HA_OK;
-  if (w->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
+  if (!mnb_ok(w)) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
   if (w->ws) {
     HA_HIP(hipSetDevice(w->device));
     HA_HIP(hipDeviceSynchronize());  // a split product in flight may still use the workspace
     (void)hipFree(w->ws);
+    w->ws = nullptr;
+  }
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    g_live_mnbs.erase(w);
   }
   w->magic = kDeadMagic;
   delete w;
@@ -712,7 +745,7 @@ int ha_fwht(void* x, long elems, int n, int device, void* stream) {
 }
 
 int ha_embed(const ha_mnb* table, int L, const void* ids, void* x, void* stream) {
-  if (!table || table->magic != kMnbMagic) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
+  if (!mnb_ok(table)) return fail(HA_ERR_HANDLE, "invalid MatMulNBits handle");
   if (L < 1 || !ids || !x) return fail(HA_ERR_ARG, "L must be >= 1 and ids, x non-NULL");
   HA_HIP(hipSetDevice(table->device));
   const ha::MnbArgs& t = table->args;

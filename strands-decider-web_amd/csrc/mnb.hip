@@ -282,7 +282,9 @@ __global__ __launch_bounds__(128 * WMW) void mnb_gemm_kernel(MnbArgs a) {
       blk = min(blk, nblk - 1);
       const _Float16* src = arow_p[i] + (size_t)blk * kBlk + 8 * (c & 3);
       // global_load_lds_dwordx4 written out: the compiler would otherwise wait for every DMA in flight before any
-      // LDS read; the k-loop's explicit waits order the DMAs instead
+      // LDS read; the k-loop's explicit waits order the DMAs instead. m0 (the DMA's LDS base) is a register the
+      // compiler reserves and does not preserve across asm; this is sound because no compiler-generated code in
+      // these kernels keeps a value in m0 (tests/test_asm_guards.py checks the assembly)
       const unsigned lds = __builtin_amdgcn_readfirstlane(
           (unsigned)(size_t)(__attribute__((address_space(3))) h8*)&stage[64 * (4 * w + i)]);
       asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");

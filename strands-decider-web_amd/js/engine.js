@@ -84,6 +84,7 @@ class DeviceBuffer {
     this._engine = engine;
     this.bytes = bytes;
     this.ptr = native.deviceAlloc(engine._h, bytes);
+    this._borrows = 0;  // MatMulNBits handles reading this buffer (the C handle keeps only its address)
   }
   upload(typedArray) {
     if (typedArray.byteLength > this.bytes) throw new RangeError('upload larger than the buffer');
@@ -100,11 +101,29 @@ class DeviceBuffer {
     native.copyToHost(this._engine._h, typedArray, this.ptr);
     return typedArray;
   }
+  // Frees the device memory. Refused while a MatMulNBits handle borrows the buffer: the handle would go on reading
+  // memory already returned to the allocator.
   free() {
+    if (this._borrows > 0) {
+      const e = new Error('device buffer is borrowed by ' + this._borrows + ' MatMulNBits handle(s); destroy them first');
+      e.code = 'HA_BORROWED';
+      throw e;
+    }
     if (this.ptr !== null) {
       native.deviceFree(this._engine._h, this.ptr);
       this.ptr = null;
     }
+  }
+}
+
+// A byte offset into a DeviceBuffer: a tensor that lives inside a larger buffer (a range of a loaded shard). A
+// MatMulNBits handle built on views borrows the underlying buffer.
+class DeviceView {
+  constructor(buf, offset) {
+    if (!(buf instanceof DeviceBuffer)) throw new TypeError('a DeviceView needs a DeviceBuffer');
+    if (offset < 0 || offset > buf.bytes) throw new RangeError('view offset outside the buffer');
+    this.buf = buf;
+    this.offset = offset;
   }
 }
 
@@ -134,6 +153,7 @@ function ptrOf(x) {
     if (x.ptr === null) throw new Error('device buffer was freed');
     return x.ptr;
   }
+  if (x instanceof DeviceView) return ptrOf(x.buf) + BigInt(x.offset);
   throw new TypeError('layer buffers must be DeviceBuffer or BigInt device pointers');
 }
 
@@ -195,9 +215,10 @@ class Engine {
 /*
  * A quantised projection weight (MatMulNBits, the formats of web/public/gemmbench/kernels.js:1-14) and its matmul,
  * y[M][N] = a[M][K] x W^T in f16 (the matmul dispatch of engine.js:236-246). q (packed blocks [N][K/32][bits] u32),
- * s (f16 scales [N][K/group]) and b (f16 biases, asymmetric formats only) are device buffers the caller keeps alive;
- * format {bits: 2|3|4, group: 32|64, asym: bool} defaults to the exporter's int4 / 32 / symmetric. The matmuls run on
- * the engine's stream, in order with its token mixers.
+ * s (f16 scales [N][K/group]) and b (f16 biases, asymmetric formats only) are device memory the handle borrows: given
+ * as DeviceBuffers, the handle holds them and their free() is refused until destroy(); given as BigInt addresses,
+ * keeping them alive is the caller's duty. format {bits: 2|3|4, group: 32|64, asym: bool} defaults to the exporter's
+ * int4 / 32 / symmetric. The matmuls run on the engine's stream, in order with its token mixers.
  */
 class MatMulNBits {
   constructor(engine, N, K, q, s, b, format) {
@@ -207,6 +228,8 @@ class MatMulNBits {
     this.K = K;
     this._h = native.mnbCreate(N, K, { bits: pick(f, 'bits', 4), group: pick(f, 'group', 32), asym: pick(f, 'asym', false) ? 1 : 0 },
       ptrOf(q), ptrOf(s), b === undefined || b === null ? null : ptrOf(b), engine ? engine.device : pick(f, 'device', 0));
+    this._borrowed = [q, s, b].map((x) => (x instanceof DeviceView ? x.buf : x)).filter((x) => x instanceof DeviceBuffer);
+    this._borrowed.forEach((x) => { x._borrows++; });
   }
   forward(M, a, y) {
     native.mnbForward(this._h, M, ptrOf(a), ptrOf(y), this.engine ? this.engine._h : null);
@@ -215,6 +238,8 @@ class MatMulNBits {
     if (this._h) {
       native.mnbDestroy(this._h);
       this._h = null;
+      this._borrowed.forEach((x) => { x._borrows--; });
+      this._borrowed = [];
     }
   }
 }
@@ -279,6 +304,12 @@ class Torso {
       { bits: pick(w, 'bits', 4), group: pick(w, 'group', 32), asym: pick(w, 'asym', false) });
     if (this.weights[name]) this.weights[name].h.destroy();
     this.weights[name] = { h: h, N: w.N, K: w.K, had: pick(w, 'had', 0) };
+  }
+  // Destroys the weight handles, so that the caller may free the device buffers they borrow (before destroy(), which
+  // destroys the engine those buffers were allocated on).
+  dropWeights() {
+    Object.keys(this.weights).forEach((k) => this.weights[k].h.destroy());
+    this.weights = {};
   }
   setParam(name, data) {
     const m = /^layers\.(\d+)\.(conv|neg_exp_A|dt_bias|gnorm|q_norm|k_norm)$/.exec(name);
@@ -405,6 +436,7 @@ module.exports = {
   fwht: fwht,
   Snapshot: Snapshot,
   DeviceBuffer: DeviceBuffer,
+  DeviceView: DeviceView,
   configFromManifest: configFromManifest,
   F32: F32,
   F16: F16,

@@ -114,7 +114,9 @@ function loadTorso(dir, opts) {
     if (i < 0) throw new Error('tensor ' + name + ' lies in no shard');
     return [i, t.offset - manifest.shards[i].start];
   };
-  const ptr = (name) => { const [i, off] = at(name); return shardBufs[i].ptr + BigInt(off); };
+  // a quantised tensor is a view of its shard's buffer: the weight handle borrows the buffer (its free() is refused
+  // while a handle reads it)
+  const ptr = (name) => { const [i, off] = at(name); return new ha.DeviceView(shardBufs[i], off); };
   let lazy = null;
   Object.keys(tensors).forEach((name) => {
     const t = tensors[name];
@@ -135,6 +137,9 @@ function loadTorso(dir, opts) {
   torso.loaded = { manifest: manifest, shards: shardBufs, lazy: lazy };
   const destroy = torso.destroy.bind(torso);
   torso.destroy = function () {
+    // the weight handles first (they borrow the shard and table buffers), then those buffers, then the rest of the
+    // torso with its engines (a buffer is freed through the engine that allocated it)
+    torso.dropWeights();
     shardBufs.forEach((b) => b.free());
     if (lazy) {
       lazy.bufs.forEach((b) => b.free());
@@ -180,7 +185,7 @@ function initLazyEmbed(torso, dir, manifest, o) {
   ids.forEach((t, i) => { E.slot[t] = i; });
   const q = manifest.tensors['embed.q'];
   const fmtT = q || {};
-  torso.setWeight('embed', { q: parts[0].buf.ptr, s: parts[1].buf.ptr, b: parts[2] ? parts[2].buf.ptr : null,
+  torso.setWeight('embed', { q: parts[0].buf, s: parts[1].buf, b: parts[2] ? parts[2].buf : null,
     N: R + e.slots, K: fmtT.K || manifest.config.hidden_size, bits: fmtT.bits || 4, group: fmtT.group || 32,
     asym: !!fmtT.asym });
   const fd = fs.openSync(rowsPath, 'r');

@@ -18,9 +18,14 @@
 /* Every external holds one of these boxes; `kind` tells them apart, so a handle of the wrong kind is a TypeError. */
 enum { BOX_ENGINE = 0x45, BOX_SNAPSHOT = 0x53, BOX_MNB = 0x4d };
 
-typedef struct {
+typedef struct engine_box {
   int kind;
   ha_engine* e;
+  /* shareStream: the engine whose stream this one runs on, held by a strong reference so that it cannot be
+     collected (and its stream destroyed) while this engine lives; and how many engines run on this one's stream */
+  napi_ref stream_owner;
+  struct engine_box* owner_box;
+  int borrowers;
 } engine_box;
 
 typedef struct {
@@ -149,10 +154,21 @@ static int get_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
 
 /* ---- finalizers ---- */
 
+/* drop an engine's link to the engine whose stream it borrowed */
+static void unshare_stream(napi_env env, engine_box* b) {
+  if (b->stream_owner) {
+    if (b->owner_box) b->owner_box->borrowers--;
+    napi_delete_reference(env, b->stream_owner);
+    b->stream_owner = NULL;
+    b->owner_box = NULL;
+  }
+}
+
 static void engine_finalize(napi_env env, void* data, void* hint) {
-  (void)env; (void)hint;
+  (void)hint;
   engine_box* b = (engine_box*)data;
   if (b->e) ha_destroy(b->e);
+  unshare_stream(env, b);
   free(b);
 }
 
@@ -243,6 +259,9 @@ static napi_value js_create(napi_env env, napi_callback_info info) {
   }
   b->kind = BOX_ENGINE;
   b->e = e;
+  b->stream_owner = NULL;
+  b->owner_box = NULL;
+  b->borrowers = 0;
   napi_value r;
   if (napi_create_external(env, b, engine_finalize, NULL, &r) != napi_ok) {
     ha_destroy(e);
@@ -258,9 +277,17 @@ static napi_value js_destroy(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 1, argv)) return NULL;
   engine_box* b = get_engine(env, argv[0]);
   if (!b) return type_error(env, "not an engine handle");
+  if (b->e && b->borrowers > 0) {
+    char msg[96];
+    snprintf(msg, sizeof(msg), "%d engine(s) run on this engine's stream (shareStream); destroy them first",
+             b->borrowers);
+    napi_throw_error(env, "HA_STREAM_SHARED", msg);
+    return NULL;
+  }
   if (b->e) {
     ha_engine* e = b->e;
     b->e = NULL;
+    unshare_stream(env, b);
     CHECK_HA(ha_destroy(e));
   }
   return NULL;
@@ -613,9 +640,20 @@ static napi_value js_share_stream(napi_env env, napi_callback_info info) {
   engine_box* a = get_engine(env, argv[0]);
   engine_box* b = get_engine(env, argv[1]);
   if (!a || !a->e || !b || !b->e) return type_error(env, "both arguments must be live engine handles");
+  if (a == b) return type_error(env, "an engine cannot borrow its own stream");
   void* st = NULL;
   CHECK_HA(ha_get_stream(b->e, &st));
-  CHECK_HA(ha_set_stream(a->e, st));
+  napi_ref ref;
+  CHECK_NAPI(napi_create_reference(env, argv[1], 1, &ref));
+  int rc = ha_set_stream(a->e, st);
+  if (rc) {
+    napi_delete_reference(env, ref);
+    return throw_status(env, rc);
+  }
+  unshare_stream(env, a);
+  a->stream_owner = ref;
+  a->owner_box = b;
+  b->borrowers++;
   return NULL;
 }
 

@@ -35,8 +35,27 @@ spec.Ms.forEach(function (M) {
 let threw = '';
 try { w.forward(0, a, a); } catch (e) { threw = e.code + ' ' + e.message; }
 if (threw.indexOf('HA_') !== 0) throw new Error('M = 0 did not throw a status error: ' + threw);
+// the handle borrows q and s: freeing them under it is refused, and the handle keeps working
+let borrowed = '';
+try { q.free(); } catch (e) { borrowed = e.code; }
+if (borrowed !== 'HA_BORROWED' || q.ptr === null) throw new Error('free() of a borrowed buffer was not refused');
+// a second handle on views of the same buffers borrows them as well
+const w2 = new ha.MatMulNBits(engine, spec.N, spec.K, new ha.DeviceView(q, 0), new ha.DeviceView(s, 0),
+  b ? new ha.DeviceView(b, 0) : null, { bits: spec.bits, group: spec.group, asym: spec.asym });
 w.destroy();
 w.destroy();  // idempotent
+borrowed = '';
+try { s.free(); } catch (e) { borrowed = e.code; }
+if (borrowed !== 'HA_BORROWED') throw new Error('free() of a buffer borrowed through a view was not refused');
+w2.destroy();
+// an engine whose stream another engine borrows cannot be destroyed first
+const e2 = ha.Engine.createSync({ layer_types: ['full_attention'] }, { batch: 1, maxCtx: 64 });
+const native = require(path.join(__dirname, '..', '..', 'strands-decider-web_amd', 'js', 'ha_napi.node'));
+native.shareStream(e2._h, engine._h);
+let shared = '';
+try { engine.destroy(); } catch (e) { shared = e.code; }
+if (shared !== 'HA_STREAM_SHARED' || engine._h === null) throw new Error('destroying a stream owner was not refused');
+e2.destroy();
 ha.fwht(engine, a, 64, 64);
 const f = new Uint16Array(64);
 a.download(f);

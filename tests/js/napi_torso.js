@@ -32,6 +32,7 @@ if (!r0.cache || r0.cache.P !== spec.L0) throw new Error('cache P ' + (r0.cache 
 const r1 = torso.forward(u32('ids1.bin'), spec.rows1, { cache: r0.cache });
 fs.writeFileSync(path.join(dir, 'hidden1.bin'), Buffer.from(r1.hidden.buffer));
 r0.cache.release();
-keep.forEach((b) => b.free());  // the weight buffers live on the torso's lead engine: free them first
+torso.dropWeights();  // the weight handles borrow these buffers
+keep.forEach((b) => b.free());  // the weight buffers live on the torso's lead engine: free them before destroy()
 torso.destroy();
 console.log(JSON.stringify({ ok: true }));

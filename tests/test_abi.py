@@ -74,3 +74,26 @@ def test_no_device_is_a_device_error_not_a_fallback():
     with pytest.raises(ha.HAError) as ei:
         ha.Engine(_cfg())
     assert ei.value.code == ha.HA_ERR_DEVICE
+
+
+def test_forged_handles_are_refused_not_read():
+    """Handles are looked up in the library's registries before any field is read: a block of memory that merely
+    starts with a handle's magic value (as a freed handle would) is refused with HA_ERR_HANDLE."""
+    lib = ha.load_library()
+    buf = (ctypes.c_uint32 * 64)()
+    p = ctypes.c_int()
+    for magic in (0x48415350, 0x48414D4E, 0x4841454E):  # snapshot, MatMulNBits, engine
+        buf[0] = magic
+        h = ctypes.cast(buf, ctypes.c_void_p)
+        assert lib.ha_snapshot_tokens(h, ctypes.byref(p)) == ha.HA_ERR_HANDLE
+        assert lib.ha_snapshot_layout(h, ctypes.byref(p), ctypes.byref(p)) == ha.HA_ERR_HANDLE
+        assert lib.ha_snapshot_read(h, 0, b"state", ctypes.cast(buf, ctypes.c_void_p), 4) == ha.HA_ERR_HANDLE
+        assert lib.ha_snapshot_release(h) == ha.HA_ERR_HANDLE
+        assert lib.ha_snapshot_destroy(h) == ha.HA_ERR_HANDLE
+        assert lib.ha_mnb_forward(h, 1, h, h, None) == ha.HA_ERR_HANDLE
+        assert lib.ha_mnb_forward_noalloc(h, 1, h, h, None) == ha.HA_ERR_HANDLE
+        assert lib.ha_mnb_destroy(h) == ha.HA_ERR_HANDLE
+        assert lib.ha_embed(h, 1, h, h, None) == ha.HA_ERR_HANDLE
+        assert lib.ha_destroy(h) == ha.HA_ERR_HANDLE
+        assert lib.ha_set_stream(h, None) == ha.HA_ERR_HANDLE
+    assert buf[0] == 0x4841454E  # nothing wrote through the forged handles
