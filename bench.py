@@ -185,6 +185,72 @@ def cpu_baseline(host, B=8, T=2048, reps=3):
                                                                            tg * 1e3, ta * 1e3)}
 
 
+def decode_measure(torch, ha, stream, steps=50, P=1536):
+    """Decode and resume from a prefix cache: a P-row prefix through the engine (chunked prefill) kept as a snapshot,
+    then calls of L new rows resumed from it, each timed alone (HIP events on the engine's stream around one call,
+    median over `steps`).
+      gdn_seq   one gated-delta layer, L = 1 and 8 rows, HA_SEQUENTIAL, B = 1 and 8: GB/s against the algorithmic
+                bytes (fp32 state in and out, 64 KiB each per head, plus the rows read and written)
+      stack     the 24-layer stack at B = 1 and 8, L = 1 (sequential recurrence for the gated-delta layers)
+      resume    the prefix-cache case: 3 gated-delta + 1 GQA layers, one 64-row suffix at P = 1536 (B = 1, default
+                recurrence), with and without keeping a snapshot of the result"""
+    import numpy as np
+    res = {}
+
+    def timed(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ts = []
+        for i in range(steps + 3):
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            e1.synchronize()
+            if i >= 3:
+                ts.append(e0.elapsed_time(e1))
+        return float(np.median(ts))
+
+    for B in (1, 8):
+        eng = make_engine(ha, ["linear_attention"], B, 4096, stream.cuda_stream)
+        pi, po = make_buffers(torch, ["linear_attention"], B, P, seed=7)
+        snap = eng.forward(P, pi, po, keep_cache=True)["cache"]
+        for L in (1, 8):
+            si, so = make_buffers(torch, ["linear_attention"], B, L, seed=8)
+            ms = timed(lambda: eng.forward(L, si, so, cache=snap, recurrence=ha.SEQUENTIAL))
+            byt = B * (2 * H * DK * DV * 4 + L * gdn_bytes_per_token())
+            res["gdn_seq_B%d_L%d" % (B, L)] = {"us": round(ms * 1e3, 2), "GB_per_s": round(byt / (ms * 1e-3) / 1e9, 1),
+                                               "bytes": byt, "frac": round(byt / (ms * 1e-3) / 8e12, 4)}
+            del si, so
+        snap.release()
+        del eng, pi, po
+        es = make_engine(ha, KINDS, B, 4096, stream.cuda_stream)
+        pi, po = make_buffers(torch, KINDS, B, P, seed=9)
+        snap = es.forward(P, pi, po, keep_cache=True)["cache"]
+        si, so = make_buffers(torch, KINDS, B, 1, seed=10)
+        ms = timed(lambda: es.forward(1, si, so, cache=snap, recurrence=ha.SEQUENTIAL))
+        res["stack_B%d_L1" % B] = {"ms": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3))}
+        snap.release()
+        del es, pi, po, si, so
+        torch.cuda.empty_cache()
+    kinds = ["linear_attention", "linear_attention", "linear_attention", "full_attention"]
+    er = make_engine(ha, kinds, 1, 4096, stream.cuda_stream)
+    pi, po = make_buffers(torch, kinds, 1, P, seed=11)
+    snap = er.forward(P, pi, po, keep_cache=True)["cache"]
+    si, so = make_buffers(torch, kinds, 1, 64, seed=12)
+    res["resume_P1536_L64"] = {"ms": round(timed(lambda: er.forward(64, si, so, cache=snap)), 4)}
+    kept = []
+
+    def with_keep():
+        kept.append(er.forward(64, si, so, cache=snap, keep_cache=True)["cache"])
+
+    res["resume_P1536_L64_keep"] = {"ms": round(timed(with_keep), 4)}
+    for k in kept:
+        k.release()
+    snap.release()
+    res["workload"] = ("resume from a %d-row prefix snapshot: gated-delta decode steps (HA_SEQUENTIAL), the 24-layer "
+                       "stack at L = 1, and the prefix-cache case (3 gated-delta + 1 GQA, 64-row suffix)" % P)
+    return res
+
+
 # The model's int4 projection shapes (K, N) and how many of each one forward runs, as the reference's matmul
 # benchmark weighs them (web/public/gemmbench/portable.js:18 and :69).
 MNB_SHAPES = [(2048, 12288, 15), (6144, 2048, 15), (2048, 8256, 11), (2048, 5120, 4), (2048, 2048, 16)]
@@ -340,7 +406,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true", help="skip the T / B sweep")
     ap.add_argument("--no-mnb", action="store_true", help="skip the MatMulNBits projection measurement")
     ap.add_argument("--no-torso", action="store_true", help="skip the whole-torso forward measurement")
-    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy", "mnb", "torso"],
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode / resume measurement")
+    ap.add_argument("--profile-kernel", choices=["gdn", "gdn-seq", "gqa", "copy", "mnb", "torso", "decode"],
                     help="run only one layer kind (T=2048, B=--profile-batch) --steps times, for rocprofv3; 'copy' runs a plain "
                          "512 MiB device-to-device copy kernel, the reference point that scales FETCH_SIZE / "
                          "WRITE_SIZE to bytes")
@@ -376,6 +443,11 @@ def main():
         res = torso_measure(torch, ha, Ls=(2048,), steps=args.steps)
         print(json.dumps({"profile_kernel": "torso", "steps": args.steps, "result": res,
                           "wall_s": round(time.perf_counter() - t0, 2)}), flush=True)
+        return
+    if args.profile_kernel == "decode":
+        with torch.cuda.stream(stream):
+            res = decode_measure(torch, ha, stream, steps=args.steps)
+        print(json.dumps({"profile_kernel": "decode", "steps": args.steps, "result": res}), flush=True)
         return
     if args.profile_kernel == "mnb":
         t0 = time.perf_counter()
@@ -469,6 +541,9 @@ def main():
                          "launch_ms": round(gqa_launch_ms, 5)},
         "sweep": sweep,
     }
+    if not args.no_decode:
+        with torch.cuda.stream(stream):
+            line["decode"] = decode_measure(torch, ha, stream)
     if not args.no_mnb:
         line["projections"] = mnb_measure(torch, ha, stream)
         line["projections"]["workload"] = ("MatMulNBits int4 group-32 projections of one forward, shapes x counts of "

@@ -84,6 +84,8 @@ struct ha_engine {
   void* zero_tail = nullptr;  // [B][3][lin_stride] zeros: the history of an empty context
   void* img = nullptr;        // [B][H][img_chunks] chunk images of the two-kernel chunked form
   int img_chunks = 0;
+  float* seq_raw = nullptr;     // [B][H][kSegRows][DV] raw outputs of the sequential form
+  unsigned* seq_cnt = nullptr;  // [B][H] its per-head arrival counters
   float* gqa_part = nullptr;  // partial results of split GQA key ranges
   int gqa_split = 0, gqa_part_slots = 0;
   hipEvent_t ev[2] = {nullptr, nullptr};
@@ -184,6 +186,8 @@ void free_engine(ha_engine* e) {
   if (e->rope) (void)hipFree(e->rope);
   if (e->zero_tail) (void)hipFree(e->zero_tail);
   if (e->img) (void)hipFree(e->img);
+  if (e->seq_raw) (void)hipFree(e->seq_raw);
+  if (e->seq_cnt) (void)hipFree(e->seq_cnt);
   if (e->gqa_part) (void)hipFree(e->gqa_part);
   for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
   for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
@@ -295,6 +299,11 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
     // chunk images: every chunk a call can touch (max_ctx / 64, plus the replayed open chunk)
     e->img_chunks = (c.max_ctx + ha::kChunk - 1) / ha::kChunk + 1;
     if ((rc = dalloc(&e->img, ha::gdn_split_image_bytes() * B * c.H * e->img_chunks))) return bail(rc);
+    if ((rc = dalloc(&e->seq_raw, sizeof(float) * B * c.H * ha::kSegRows * c.DV)) ||
+        (rc = dalloc(&e->seq_cnt, sizeof(unsigned) * B * c.H)))
+      return bail(rc);
+    if (hipMemset(e->seq_cnt, 0, sizeof(unsigned) * B * c.H) != hipSuccess)
+      return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
   }
   if (e->any_full) {
     // RoPE table as engine.js:105-106 builds it: angle t / theta^(2i/RD) in f64, stored as f32 (cos, sin)
@@ -444,6 +453,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.S_in = resume ? resume->layers[i].S : nullptr; a.S_out = l.S;
       a.conv_w = l.conv; a.negA = l.negA; a.dtb = l.dtb; a.gnorm = c.lin_gnorm ? l.gnorm : nullptr;
       a.img = e->img; a.img_chunks = e->img_chunks;
+      a.seq_raw = e->seq_raw; a.seq_cnt = e->seq_cnt;
       hipError_t he = !chunked ? ha::launch_gdn_sequential(a, st)
                       : split ? ha::launch_gdn_split(a, st)
                               : ha::launch_gdn_chunked(a, st);

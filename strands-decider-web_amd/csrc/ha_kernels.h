@@ -26,7 +26,10 @@ struct GdnArgs {
   const float* gnorm;               // [DV], or nullptr to output the raw core output
   void* img;                        // chunk-image scratch of the two-kernel form: [B][H][img_chunks] images
   int img_chunks;                   // image slots per (sequence, head)
+  float* seq_raw;                   // sequential form: raw outputs [B][H][kSegRows][DV] fp32 awaiting the gated norm
+  unsigned* seq_cnt;                // sequential form: [B][H] arrival counters (zero between launches)
 };
+constexpr int kSegRows = 64;        // output rows per launch of the sequential form
 
 // Full-attention prep (q/k RMSNorm, partial RoPE, K/V cache write) and attention for rows [P, P + L).
 struct GqaArgs {
