@@ -84,10 +84,11 @@ def _torso(W, V, M):
     return t
 
 
-def _oracle(W, V, M, ids, rows):
-    """fp64 composition, rounding to f16 where the reference stores f16; one forward over all of ids."""
+def _oracle(W, V, M, ids, rows, deq=None):
+    """fp64 composition, rounding to f16 where the reference stores f16; one forward over all of ids. `deq` keeps
+    the dequantised weights between calls on one model."""
     f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).astype(np.float64)  # noqa: E731
-    deq = {}
+    deq = {} if deq is None else deq
 
     def mm(a, name):
         words, sc, N, K = W[name]
