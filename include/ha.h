@@ -104,6 +104,14 @@ int ha_destroy(ha_engine* e);
 /* Bind the engine to an existing HIP stream (hipStream_t passed as void*), e.g. a framework's current stream.
    NULL rebinds the engine's own stream. */
 int ha_set_stream(ha_engine* e, void* stream);
+/* Let engine e use the call-time device buffers of `holder` (chunk images, the sequential form's raw outputs and
+   counters, split-GQA partials, the zero history), growing them to what e's shape needs, and free e's own set once
+   nothing else holds it. For engines whose calls never overlap, e.g. the per-layer engines of one torso on one
+   stream: their calls then run one after another and one set serves all of them. Calls of engines holding one set
+   must not overlap (one stream, or the host waiting between them). The set lives until the last engine holding it
+   is destroyed. No counterpart in the reference, whose engine holds one set of buffers for all its layers
+   (engine.js:89-107). Waits for the device to finish queued work. */
+int ha_share_scratch(ha_engine* e, ha_engine* holder);
 /* The stream the engine's calls run on (hipStream_t as void*): for a host that queues its own work, such as the
    projection matmuls (ha_mnb_forward), in order with the token mixers. No counterpart in the reference, whose
    WebGPU queue is implicit (engine.js:236-246 records everything into one command encoder). */

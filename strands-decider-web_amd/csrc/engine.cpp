@@ -18,6 +18,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <unordered_set>
@@ -70,6 +71,41 @@ struct Layer {
 
 size_t dtype_size(int dt) { return dt == HA_F16 ? 2 : 4; }
 
+// Device memory an engine's kernels use only inside a call: the two-kernel form's chunk images, the sequential
+// form's raw outputs and per-head arrival counters (zero between calls), split-GQA partial results, and the zero
+// history of an empty context. Engines whose calls never overlap may hold one set between them (ha_share_scratch);
+// it is freed with the last engine holding it. Every buffer only has to be large enough for each holder's shape.
+struct Scratch {
+  struct Buf {
+    void* p = nullptr;
+    size_t bytes = 0;
+  };
+  int device = 0;
+  Buf img, seq_raw, seq_cnt, gqa_part, zeros;
+  ~Scratch() {
+    (void)hipSetDevice(device);
+    for (Buf* b : {&img, &seq_raw, &seq_cnt, &gqa_part, &zeros})
+      if (b->p) (void)hipFree(b->p);
+  }
+};
+
+// Makes b hold at least `bytes`, zero-filled when a larger buffer replaces it. A buffer is only replaced after the
+// device has finished every queued call, since a call of any engine holding the set may still read the old one.
+int grow(Scratch::Buf& b, size_t bytes) {
+  if (bytes <= b.bytes) return HA_OK;
+  void* p = nullptr;
+  hipError_t he = hipMalloc(&p, bytes);
+  if (he != hipSuccess) return fail(HA_ERR_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(he));
+  if ((he = hipMemset(p, 0, bytes)) != hipSuccess || (he = hipDeviceSynchronize()) != hipSuccess) {
+    (void)hipFree(p);
+    return fail(HA_ERR_DEVICE, std::string("scratch set-up: ") + hipGetErrorString(he));
+  }
+  if (b.p) (void)hipFree(b.p);
+  b.p = p;
+  b.bytes = bytes;
+  return HA_OK;
+}
+
 }  // namespace
 
 struct ha_engine {
@@ -81,12 +117,12 @@ struct ha_engine {
   hipStream_t own = nullptr, stream = nullptr;
   std::vector<Layer> layers;
   float* rope = nullptr;
-  void* zero_tail = nullptr;  // [B][3][lin_stride] zeros: the history of an empty context
-  void* img = nullptr;        // [B][H][img_chunks] chunk images of the two-kernel chunked form
+  // call-time buffers, possibly held with other engines: zeros [B][3][lin_stride] (the history of an empty context),
+  // images [B][H][img_chunks] of the two-kernel form (allocated when a call can use that form), the sequential
+  // form's raw outputs [B][H][kSegRows][DV] and counters [B][H], split-GQA partials [gqa_part_slots]
+  std::shared_ptr<Scratch> scratch;
+  size_t need_zeros = 0, need_img = 0, need_seq_raw = 0, need_seq_cnt = 0, need_gqa = 0;
   int img_chunks = 0;
-  float* seq_raw = nullptr;     // [B][H][kSegRows][DV] raw outputs of the sequential form
-  unsigned* seq_cnt = nullptr;  // [B][H] its per-head arrival counters
-  float* gqa_part = nullptr;  // partial results of split GQA key ranges
   int gqa_split = 0, gqa_part_slots = 0;
   hipEvent_t ev[2] = {nullptr, nullptr};
   std::vector<hipEvent_t> lev;
@@ -127,6 +163,10 @@ const ha_engine* snapshot_owner(const ha_snapshot* s) {
   const ha_engine* e = s->owner;
   return (e && g_live.count(e) && e->id == s->owner_id) ? e : nullptr;
 }
+
+// HA_CHUNKED's choice of the two-kernel gated-delta form: few (sequence, head) recurrences for the 256 CUs (measured
+// crossover at T = 2048: B*H between 32 and 48). From the engine's shape alone, so every call rounds alike.
+bool split_by_shape(const ha_config& c) { return c.batch * c.H <= 32; }
 
 int check_config(const ha_config* c) {
   if (!c) return fail(HA_ERR_ARG, "config is NULL");
@@ -184,11 +224,7 @@ void free_engine(ha_engine* e) {
       if (p) (void)hipFree(p);
   }
   if (e->rope) (void)hipFree(e->rope);
-  if (e->zero_tail) (void)hipFree(e->zero_tail);
-  if (e->img) (void)hipFree(e->img);
-  if (e->seq_raw) (void)hipFree(e->seq_raw);
-  if (e->seq_cnt) (void)hipFree(e->seq_cnt);
-  if (e->gqa_part) (void)hipFree(e->gqa_part);
+  e->scratch.reset();
   for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
   for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
   if (e->own) (void)hipStreamDestroy(e->own);
@@ -292,18 +328,20 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
         return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
     }
   }
+  e->scratch = std::make_shared<Scratch>();
+  e->scratch->device = device;
   if (e->any_linear) {
-    const size_t bytes = dtype_size(c.lin_dtype) * B * (kKC - 1) * c.lin_stride;
-    if ((rc = dalloc(&e->zero_tail, bytes))) return bail(rc);
-    if (hipMemset(e->zero_tail, 0, bytes) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
-    // chunk images: every chunk a call can touch (max_ctx / 64, plus the replayed open chunk)
+    e->need_zeros = dtype_size(c.lin_dtype) * B * (kKC - 1) * c.lin_stride;
+    // chunk images: every chunk a call can touch (max_ctx / 64, plus the replayed open chunk); allocated here only
+    // when HA_CHUNKED picks the two-kernel form for this shape, else by the first call that forces that form
     e->img_chunks = (c.max_ctx + ha::kChunk - 1) / ha::kChunk + 1;
-    if ((rc = dalloc(&e->img, ha::gdn_split_image_bytes() * B * c.H * e->img_chunks))) return bail(rc);
-    if ((rc = dalloc(&e->seq_raw, sizeof(float) * B * c.H * ha::kSegRows * c.DV)) ||
-        (rc = dalloc(&e->seq_cnt, sizeof(unsigned) * B * c.H)))
+    e->need_img = ha::gdn_split_image_bytes() * B * c.H * e->img_chunks;
+    e->need_seq_raw = sizeof(float) * B * c.H * ha::kSegRows * c.DV;
+    e->need_seq_cnt = sizeof(unsigned) * B * c.H;
+    if ((rc = grow(e->scratch->zeros, e->need_zeros)) || (rc = grow(e->scratch->seq_raw, e->need_seq_raw)) ||
+        (rc = grow(e->scratch->seq_cnt, e->need_seq_cnt)) ||
+        (split_by_shape(c) && (rc = grow(e->scratch->img, e->need_img))))
       return bail(rc);
-    if (hipMemset(e->seq_cnt, 0, sizeof(unsigned) * B * c.H) != hipSuccess)
-      return bail(fail(HA_ERR_DEVICE, "hipMemset failed"));
   }
   if (e->any_full) {
     // RoPE table as engine.js:105-106 builds it: angle t / theta^(2i/RD) in f64, stored as f32 (cos, sin)
@@ -325,7 +363,8 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
       e->gqa_split = std::max(8, (N + 7) / 8);
       const size_t slots = ha::gqa_part_slots((int)B * c.HK, c.max_ctx, e->gqa_split);
       e->gqa_part_slots = (int)slots;
-      if ((rc = dalloc(&e->gqa_part, slots * ha::gqa_part_slot_bytes()))) return bail(rc);
+      e->need_gqa = slots * ha::gqa_part_slot_bytes();
+      if ((rc = grow(e->scratch->gqa_part, e->need_gqa))) return bail(rc);
     }
     if (hipMemcpy(e->rope, rope.data(), rope.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
       return bail(fail(HA_ERR_DEVICE, "hipMemcpy rope failed"));
@@ -343,6 +382,24 @@ int ha_destroy(ha_engine* e) {
 int ha_set_stream(ha_engine* e, void* stream) {
   if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
   e->stream = stream ? static_cast<hipStream_t>(stream) : e->own;
+  return HA_OK;
+}
+
+int ha_share_scratch(ha_engine* e, ha_engine* holder) {
+  if (!engine_ok(e) || !engine_ok(holder)) return fail(HA_ERR_HANDLE, "invalid engine handle");
+  if (e->device != holder->device) return fail(HA_ERR_ARG, "engines are on different devices");
+  if (e->scratch == holder->scratch) return HA_OK;
+  HA_HIP(hipSetDevice(e->device));
+  HA_HIP(hipDeviceSynchronize());  // no queued call of either engine may still use a buffer that is replaced
+  Scratch& to = *holder->scratch;
+  const Scratch& from = *e->scratch;
+  int rc;
+  // images only where e had them (its shape picks the two-kernel form, or a call forced it)
+  if ((rc = grow(to.zeros, e->need_zeros)) || (rc = grow(to.img, from.img.bytes ? e->need_img : 0)) ||
+      (rc = grow(to.seq_raw, e->need_seq_raw)) ||
+      (rc = grow(to.seq_cnt, e->need_seq_cnt)) || (rc = grow(to.gqa_part, e->need_gqa)))
+    return rc;
+  e->scratch = holder->scratch;
   return HA_OK;
 }
 
@@ -425,7 +482,12 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   // (sequence, head) recurrences for the 256 CUs (measured crossover at T = 2048: B*H between 32 and 48), the fused
   // kernel otherwise. The two round differently, so the choice must not depend on the call (a resumed suffix must
   // match the same rows of one longer forward bit for bit).
-  const bool split = mode == HA_CHUNKED_SPLIT || (mode == HA_CHUNKED && c.batch * c.H <= 32);
+  const bool split = mode == HA_CHUNKED_SPLIT || (mode == HA_CHUNKED && split_by_shape(c));
+  Scratch& sc = *e->scratch;
+  if (e->any_linear && chunked && split && sc.img.bytes < e->need_img) {
+    int rc = grow(sc.img, e->need_img);  // first call that forces the two-kernel form on a larger shape
+    if (rc) return rc;
+  }
   // raw-row tails: the copy reads only the call's input rows and the resumed tail, so the layers' copies are
   // gathered into one launch after the mixers (per layer when per-layer times are asked for, so that each layer's
   // time includes its own copy)
@@ -446,14 +508,14 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       ha::GdnArgs a{};
       a.B = c.batch; a.H = c.H; a.DK = c.DK; a.DV = c.DV; a.KC = kKC; a.stride = c.lin_stride; a.C = e->C;
       a.P = P; a.L = L; a.s0 = s0;
-      a.tail = resume ? resume->layers[i].tail : e->zero_tail;
+      a.tail = resume ? resume->layers[i].tail : sc.zeros.p;
       a.tail_cap = resume ? resume->tail_rows : kKC - 1;
       a.dtype = c.lin_dtype == HA_F16 ? 1 : 0;
       a.in = layer_in[i]; a.out = layer_out[i];
       a.S_in = resume ? resume->layers[i].S : nullptr; a.S_out = l.S;
       a.conv_w = l.conv; a.negA = l.negA; a.dtb = l.dtb; a.gnorm = c.lin_gnorm ? l.gnorm : nullptr;
-      a.img = e->img; a.img_chunks = e->img_chunks;
-      a.seq_raw = e->seq_raw; a.seq_cnt = e->seq_cnt;
+      a.img = sc.img.p; a.img_chunks = e->img_chunks;
+      a.seq_raw = static_cast<float*>(sc.seq_raw.p); a.seq_cnt = static_cast<unsigned*>(sc.seq_cnt.p);
       hipError_t he = !chunked ? ha::launch_gdn_sequential(a, st)
                       : split ? ha::launch_gdn_split(a, st)
                               : ha::launch_gdn_chunked(a, st);
@@ -469,7 +531,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.P = P; a.L = L; a.dtype = c.full_dtype == HA_F16 ? 1 : 0;
       a.in = layer_in[i]; a.out = layer_out[i]; a.qw = l.qn; a.kw = l.kn; a.rope = e->rope;
       a.K = l.K; a.V = l.V;
-      a.split = e->gqa_split; a.part_slots = e->gqa_part_slots; a.part = e->gqa_part;
+      a.split = e->gqa_split; a.part_slots = e->gqa_part_slots; a.part = static_cast<float*>(sc.gqa_part.p);
       hipError_t he = ha::launch_gqa(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " attention launch: " + hipGetErrorString(he));
     }  // HA_ADAPTER: no token mixer, nothing to run

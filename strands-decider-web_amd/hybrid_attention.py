@@ -65,6 +65,7 @@ def load_library(path=LIB_PATH):
         "ha_create": ([ctypes.POINTER(HaConfig), i, ctypes.POINTER(vp)], i),
         "ha_destroy": ([vp], i),
         "ha_set_stream": ([vp, vp], i),
+        "ha_share_scratch": ([vp, vp], i),
         "ha_set_param": ([vp, i, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), sz], i),
         "ha_forward": ([vp, i, ctypes.POINTER(vp), ctypes.POINTER(vp), vp, ctypes.POINTER(vp),
                         ctypes.POINTER(HaForwardOpts)], i),
@@ -175,6 +176,10 @@ class Engine:
 
     def set_stream(self, stream):
         _check(_lib.ha_set_stream(self._h, ctypes.c_void_p(stream) if stream else None))
+
+    def share_scratch(self, holder):
+        """Use `holder`'s call-time device buffers (ha_share_scratch); the two engines' calls must not overlap."""
+        _check(_lib.ha_share_scratch(self._h, holder._h))
 
     def set_param(self, layer, name, values):
         import numpy as np
@@ -313,6 +318,9 @@ class Torso:
         self.mix = {i: Engine(model_config([t], batch=1, max_ctx=max_ctx, lin_dtype=F16, full_dtype=F16),
                               device=device, stream=self.st)
                     for i, t in enumerate(self.types) if t != "adapter"}
+        engines = list(self.mix.values())
+        for m in engines[1:]:  # one stream orders every call, so one set of call-time buffers serves all
+            m.share_scratch(engines[0])
         self.w, self.v = {}, {}
 
     def set_weight(self, name, w):

@@ -633,7 +633,8 @@ static napi_value js_fwht(napi_env env, napi_callback_info info) {
 }
 
 /* shareStream(engine, other): run `engine`'s calls on `other`'s stream, so that work on several engines stays in
-   one order (ha_get_stream + ha_set_stream) */
+   one order (ha_get_stream + ha_set_stream); their calls then never overlap, so `engine` also uses `other`'s
+   call-time device buffers (ha_share_scratch) */
 static napi_value js_share_stream(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!get_args(env, info, 2, argv)) return NULL;
@@ -643,6 +644,7 @@ static napi_value js_share_stream(napi_env env, napi_callback_info info) {
   if (a == b) return type_error(env, "an engine cannot borrow its own stream");
   void* st = NULL;
   CHECK_HA(ha_get_stream(b->e, &st));
+  CHECK_HA(ha_share_scratch(a->e, b->e));
   napi_ref ref;
   CHECK_NAPI(napi_create_reference(env, argv[1], 1, &ref));
   int rc = ha_set_stream(a->e, st);

@@ -96,4 +96,5 @@ def test_forged_handles_are_refused_not_read():
         assert lib.ha_embed(h, 1, h, h, None) == ha.HA_ERR_HANDLE
         assert lib.ha_destroy(h) == ha.HA_ERR_HANDLE
         assert lib.ha_set_stream(h, None) == ha.HA_ERR_HANDLE
+        assert lib.ha_share_scratch(h, h) == ha.HA_ERR_HANDLE
     assert buf[0] == 0x4841454E  # nothing wrote through the forged handles
