@@ -221,6 +221,17 @@ int ha_silu_mul(int L, int I, const void* big, void* mid, int device, void* stre
 /* y[t][j] += c[j] for t < L, j < N (ADD_BIAS, wgsl.js:119-121): y f16, c f32 on the device, N % 8 == 0. */
 int ha_add_bias(int L, int N, void* y, const float* c, int device, void* stream);
 
+/* ---- GPU timestamps for diagnostics: the counterpart of the reference's WebGPU timestamp query sets, written at
+   compute-pass boundaries and resolved after the submit (engine.js:292-307 profile(), 331-348 timestamps). */
+typedef struct ha_timer ha_timer;
+/* n timestamps on HIP device `device` (createQuerySet({type: "timestamp", count: n})). */
+int ha_timer_create(int device, int n, ha_timer** t);
+/* Record timestamp i on `stream` (hipStream_t as void*, NULL: the null stream) after the work queued so far. */
+int ha_timer_mark(ha_timer* t, int i, void* stream);
+/* Wait for timestamps i and j (both recorded) and give the GPU time from i to j in milliseconds. */
+int ha_timer_elapsed(ha_timer* t, int i, int j, float* ms);
+int ha_timer_destroy(ha_timer* t);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,8 @@ std::unordered_set<const ha_engine*> g_live;
 // before reading through it, so a destroyed handle is refused instead of read after it was freed.
 std::unordered_set<const ha_snapshot*> g_live_snaps;
 std::unordered_set<const void*> g_live_mnbs;  // MatMulNBits handles, likewise
+std::unordered_set<const void*> g_live_timers;  // timestamp sets, likewise
+constexpr uint32_t kTimerMagic = 0x48415449u;
 
 struct Layer {
   int kind = 0;
@@ -855,6 +857,91 @@ int ha_add_bias(int L, int N, void* y, const float* c, int device, void* stream)
   if (!y || !c || L < 1 || N < 8 || N % 8) return fail(HA_ERR_ARG, "need y, c non-NULL, L >= 1, N % 8 == 0");
   HA_HIP(hipSetDevice(device));
   HA_HIP(ha::launch_add_bias(y, c, L, N, (hipStream_t)stream));
+  return HA_OK;
+}
+
+}  // extern "C"
+
+struct ha_timer {
+  uint32_t magic = kTimerMagic;
+  int device = 0;
+  std::vector<hipEvent_t> ev;
+  std::vector<char> marked;
+};
+
+namespace {
+
+bool timer_ok(const ha_timer* t) {
+  std::lock_guard<std::mutex> lock(g_live_mu);
+  return t && g_live_timers.count(t) && t->magic == kTimerMagic;
+}
+
+void free_timer(ha_timer* t) {
+  (void)hipSetDevice(t->device);
+  for (hipEvent_t ev : t->ev)
+    if (ev) (void)hipEventDestroy(ev);
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    g_live_timers.erase(t);
+  }
+  t->magic = kDeadMagic;
+  delete t;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ha_timer_create(int device, int n, ha_timer** out) {
+  if (!out) return fail(HA_ERR_ARG, "timer output pointer is NULL");
+  *out = nullptr;
+  if (n <= 0 || n > (1 << 20)) return fail(HA_ERR_ARG, "timestamp count must be in [1, 2^20]");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) return fail(HA_ERR_ARG, "device index out of range");
+  HA_HIP(hipSetDevice(device));
+  ha_timer* t = new ha_timer();
+  t->device = device;
+  t->ev.assign(n, nullptr);
+  t->marked.assign(n, 0);
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    g_live_timers.insert(t);
+  }
+  for (auto& ev : t->ev)
+    if (hipEventCreate(&ev) != hipSuccess) {
+      free_timer(t);
+      return fail(HA_ERR_DEVICE, "hipEventCreate failed");
+    }
+  *out = t;
+  return HA_OK;
+}
+
+int ha_timer_mark(ha_timer* t, int i, void* stream) {
+  if (!timer_ok(t)) return fail(HA_ERR_HANDLE, "invalid timer handle");
+  if (i < 0 || i >= (int)t->ev.size()) return fail(HA_ERR_ARG, "timestamp index out of range");
+  HA_HIP(hipSetDevice(t->device));
+  HA_HIP(hipEventRecord(t->ev[i], (hipStream_t)stream));
+  t->marked[i] = 1;
+  return HA_OK;
+}
+
+int ha_timer_elapsed(ha_timer* t, int i, int j, float* ms) {
+  if (!timer_ok(t)) return fail(HA_ERR_HANDLE, "invalid timer handle");
+  if (!ms) return fail(HA_ERR_ARG, "ms must be non-NULL");
+  const int n = (int)t->ev.size();
+  if (i < 0 || i >= n || j < 0 || j >= n) return fail(HA_ERR_ARG, "timestamp index out of range");
+  if (!t->marked[i] || !t->marked[j]) return fail(HA_ERR_ARG, "timestamp was not recorded");
+  HA_HIP(hipSetDevice(t->device));
+  HA_HIP(hipEventSynchronize(t->ev[i]));
+  HA_HIP(hipEventSynchronize(t->ev[j]));
+  HA_HIP(hipEventElapsedTime(ms, t->ev[i], t->ev[j]));
+  return HA_OK;
+}
+
+int ha_timer_destroy(ha_timer* t) {
+  if (!t) return HA_OK;
+  if (!timer_ok(t)) return fail(HA_ERR_HANDLE, "invalid timer handle");
+  free_timer(t);
   return HA_OK;
 }
 

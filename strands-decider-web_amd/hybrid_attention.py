@@ -88,6 +88,10 @@ def load_library(path=LIB_PATH):
         "ha_add_norm": ([i, i, i, vp, vp, vp, vp, i, vp, ctypes.c_float, i, vp], i),
         "ha_silu_mul": ([i, i, vp, vp, i, vp], i),
         "ha_add_bias": ([i, i, vp, vp, i, vp], i),
+        "ha_timer_create": ([i, i, ctypes.POINTER(vp)], i),
+        "ha_timer_mark": ([vp, i, vp], i),
+        "ha_timer_elapsed": ([vp, i, i, ctypes.POINTER(ctypes.c_float)], i),
+        "ha_timer_destroy": ([vp], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -296,6 +300,35 @@ def add_bias(L, N, y, c, device=0, stream=None):
     _check(_lib.ha_add_bias(L, N, _ptr(y), _ptr(c), device, _st(stream)))
 
 
+class Timer:
+    """n GPU timestamps (ha_timer_*): the counterpart of a WebGPU timestamp query set."""
+
+    def __init__(self, n, device=0):
+        lib = load_library()
+        h = ctypes.c_void_p()
+        _check(lib.ha_timer_create(device, n, ctypes.byref(h)))
+        self._h = h
+
+    def mark(self, i, stream=None):
+        _check(_lib.ha_timer_mark(self._h, i, _st(stream)))
+
+    def elapsed(self, i, j):
+        ms = ctypes.c_float()
+        _check(_lib.ha_timer_elapsed(self._h, i, j, ctypes.byref(ms)))
+        return ms.value
+
+    def close(self):
+        if self._h:
+            _check(_lib.ha_timer_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Torso:
     """The whole torso forward (web/public/engine/engine.js:247-285, 313-376), batch 1, from the C ABI calls js/engine.js
     Torso makes, in the same order, on one stream: EMBED; per layer the input norm (residual add from layer 1 on),
@@ -322,6 +355,7 @@ class Torso:
         for m in engines[1:]:  # one stream orders every call, so one set of call-time buffers serves all
             m.share_scratch(engines[0])
         self.w, self.v = {}, {}
+        self._prof, self.diag = None, {}
 
     def set_weight(self, name, w):
         self.w[name] = w
@@ -333,15 +367,33 @@ class Torso:
             return
         self.v[name] = self.torch.as_tensor(data, dtype=self.torch.float32).to(self.dev)
 
-    def forward(self, ids, rows=None, cache=None, keep=False):
+    def _step(self, label, fn):
+        pr = self._prof
+        if pr is None:
+            return fn()
+        k = len(pr["labels"])
+        pr["timer"].mark(2 * k, self.st)
+        r = fn()
+        pr["timer"].mark(2 * k + 1, self.st)
+        pr["labels"].append(label)
+        return r
+
+    def forward(self, ids, rows=None, cache=None, keep=False, timestamps=False, debug_layers=False):
         """ids: token rows of the embedding table; rows: indices into ids to return (default all). Returns
-        (hidden f32 [len(rows)][D] on the host, {layer: Snapshot} when keep)."""
+        (hidden f32 [len(rows)][D] on the host, {layer: Snapshot} when keep). The reference's diagnostics
+        (engine.js:313-376) go to self.diag: "gpu_ms" (timestamps: GPU time from the embedding to the final norm) and
+        "layers" (debug_layers: the residual stream x entering each layer i >= 1, f32 [L][D], read back between the
+        layers)."""
         import numpy as np
         torch, D, I, st = self.torch, self.D, self.I, self.st
         L = len(ids)
         rows = list(range(L)) if rows is None else list(rows)
         f16, f32 = torch.float16, torch.float32
         maxN = max([2 * I] + [w.N for w in self.w.values()])
+        step = self._step
+        self.diag = {}
+        timer = Timer(2, self.device) if timestamps else None
+        layers = []
         with torch.cuda.stream(self.stream):
             idd = torch.as_tensor(np.asarray(ids, np.uint32).view(np.int32)).to(self.dev)
             x = torch.empty(L, D, dtype=f32, device=self.dev)
@@ -350,26 +402,61 @@ class Torso:
             o = torch.empty(L, D, dtype=f16, device=self.dev)
             y = torch.empty(L, D, dtype=f16, device=self.dev)
             mid = torch.empty(L, I, dtype=f16, device=self.dev)
-            rd = torch.as_tensor(np.asarray(rows, np.uint32).view(np.int32)).to(self.dev)
+            rd = torch.as_tensor(np.asarray(rows or [0], np.uint32).view(np.int32)).to(self.dev)
             out = torch.empty(len(rows), D, dtype=f32, device=self.dev)
-            embed(self.w["embed"], L, idd, x, stream=st)
+            if timer:
+                timer.mark(0, st)
+            step("embed", lambda: embed(self.w["embed"], L, idd, x, stream=st))
             snaps = {}
             for i, t in enumerate(self.types):
-                p = "layers.%d." % i
-                add_norm(L, D, L, x, y if i > 0 else None, self.v[p + "in_norm"], h, device=self.device, stream=st)
+                p, S = "layers.%d." % i, "L%d/" % i
+                step(S + "in_norm", lambda: add_norm(L, D, L, x, y if i > 0 else None, self.v[p + "in_norm"], h,
+                                                     device=self.device, stream=st))
+                if debug_layers and i > 0:
+                    self.stream.synchronize()
+                    layers.append(x.cpu().numpy())
                 if t == "adapter":
-                    self.w[p + "proj"].forward(L, h, y, st)
-                    add_bias(L, D, y, self.v[p + "bias"], device=self.device, stream=st)
+                    step(S + "proj", lambda: self.w[p + "proj"].forward(L, h, y, st))
+                    step(S + "bias", lambda: add_bias(L, D, y, self.v[p + "bias"], device=self.device, stream=st))
                     continue
-                self.w[p + ("in_proj" if t == "linear_attention" else "qkv")].forward(L, h, big, st)
-                r = self.mix[i].forward(L, [big], [o], cache=cache[i] if cache else None, keep_cache=keep)
+                lin = t == "linear_attention"
+                step(S + ("in_proj" if lin else "qkv"),
+                     lambda: self.w[p + ("in_proj" if lin else "qkv")].forward(L, h, big, st))
+                r = step(S + ("gdn" if lin else "attn"),
+                         lambda: self.mix[i].forward(L, [big], [o], cache=cache[i] if cache else None, keep_cache=keep))
                 snaps[i] = r["cache"]
-                self.w[p + ("out_proj" if t == "linear_attention" else "o_proj")].forward(L, o, y, st)
-                add_norm(L, D, L, x, y, self.v[p + "post_norm"], h, device=self.device, stream=st)
-                self.w[p + "gate_up"].forward(L, h, big, st)
-                silu_mul(L, I, big, mid, device=self.device, stream=st)
-                self.w[p + "down"].forward(L, mid, y, st)
-            add_norm(len(rows), D, L, x, y, self.v["final_norm"], out, out_f32=True, rows=rd, device=self.device,
-                     stream=st)
+                step(S + ("out_proj" if lin else "o_proj"),
+                     lambda: self.w[p + ("out_proj" if lin else "o_proj")].forward(L, o, y, st))
+                step(S + "post_norm", lambda: add_norm(L, D, L, x, y, self.v[p + "post_norm"], h, device=self.device,
+                                                       stream=st))
+                step(S + "gate_up", lambda: self.w[p + "gate_up"].forward(L, h, big, st))
+                step(S + "silu", lambda: silu_mul(L, I, big, mid, device=self.device, stream=st))
+                step(S + "down", lambda: self.w[p + "down"].forward(L, mid, y, st))
+            if rows:
+                step("final_norm", lambda: add_norm(len(rows), D, L, x, y, self.v["final_norm"], out, out_f32=True,
+                                                    rows=rd, device=self.device, stream=st))
+            if timer:
+                timer.mark(1, st)
         self.stream.synchronize()
+        if timer:
+            self.diag["gpu_ms"] = timer.elapsed(0, 1)
+            timer.close()
+        if debug_layers:
+            self.diag["layers"] = layers
         return out.cpu().numpy(), (snaps if keep else None)
+
+    def profile(self, ids, cache=None):
+        """GPU time of every step of a forward over ids, summed over the layers by the step's name without its layer
+        prefix, in ms to 2 decimals, largest first (engine.js:292-307). A timestamp pair brackets every step."""
+        cap = 2 * (3 + 16 * len(self.types))
+        self._prof = {"timer": Timer(cap, self.device), "labels": []}
+        try:
+            self.forward(ids, [], cache=cache)
+            by = {}
+            for k, label in enumerate(self._prof["labels"]):
+                name = label.split("/", 1)[1] if label.startswith("L") and "/" in label else label
+                by[name] = by.get(name, 0.0) + self._prof["timer"].elapsed(2 * k, 2 * k + 1)
+            return {k: round(v, 2) for k, v in sorted(by.items(), key=lambda kv: -kv[1])}
+        finally:
+            self._prof["timer"].close()
+            self._prof = None

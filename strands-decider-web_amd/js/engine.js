@@ -332,10 +332,23 @@ class Torso {
     if (!v) throw new Error('no tensor ' + name);
     return v;
   }
-  _matmul(L, a, name, y) {
+  // One step of the forward: with a profile running, timestamps on the shared stream before and after it.
+  _step(label, fn) {
+    const pr = this._prof;
+    if (!pr) return fn();
+    if (2 * pr.labels.length + 2 > pr.cap) throw new Error('profile: more steps than timestamps');
+    native.timerMark(pr.timer, 2 * pr.labels.length, this.lead._h);
+    const r = fn();
+    native.timerMark(pr.timer, 2 * pr.labels.length + 1, this.lead._h);
+    pr.labels.push(label);
+    return r;
+  }
+  _matmul(L, a, name, y, label) {
     const w = this._w(name);
-    if (w.had) native.fwht(a.ptr, L * w.K, w.had, this.device, this.lead._h);  // a is not read again
-    w.h.forward(L, a, y);
+    if (w.had) {  // a is not read again
+      this._step(label + '/had', () => native.fwht(a.ptr, L * w.K, w.had, this.device, this.lead._h));
+    }
+    this._step(label, () => w.h.forward(L, a, y));
     return w.N;
   }
   _norm(R, nx, x, y, wname, h, outF32, rows) {
@@ -344,50 +357,68 @@ class Torso {
   }
   /*
    * ids: token rows of the embedding table; rows: indices into ids whose final-normed hidden states are returned
-   * (default all). options {cache, keepCache} as Engine.forward; the cache is {P, ids, layers, release()}.
-   * Returns {hidden: Float32Array(rows.length * D), d: D, cache}.
+   * (default all). options {cache, keepCache} as Engine.forward (the cache is {P, ids, layers, release()}), and the
+   * reference's diagnostics (engine.js:313-376):
+   *   timestamps: gpu_ms, the GPU time from the embedding to the final norm;
+   *   debugLayers: layers[i - 1] = the residual stream x entering layer i >= 1 (f32 [L][D], after the residual add
+   *     that opens the layer: the output of layer i - 1), read back between the layers.
+   * Returns {hidden: Float32Array(rows.length * D), d: D, cache, fetch_ms (host time of embedRows)[, gpu_ms][,
+   * layers]}.
    */
   forward(ids, rows, options) {
     const o = options || {};
     const L = ids.length, D = this.D, I = this.I;
     const cache = pick(o, 'cache', null), keep = !!pick(o, 'keepCache', false);
+    const debug = !!pick(o, 'debugLayers', false), stamps = !!pick(o, 'timestamps', false);
     const R = rows ? rows : Array.from({ length: L }, (_, i) => i);
     let maxN = 2 * I;
     Object.keys(this.weights).forEach((k) => { maxN = Math.max(maxN, this.weights[k].N); });
+    const t0 = process.hrtime.bigint();
     const tableRows = this.embedRows ? this.embedRows(ids) : ids;
+    const fetchMs = Number(process.hrtime.bigint() - t0) / 1e6;
     const bufs = this._work(L, Math.max(R.length, 1), maxN);
     bufs.ids.upload(Uint32Array.from(tableRows));
-    const snaps = [];
+    const snaps = [], layers = [];
+    const timer = stamps ? native.timerCreate(this.device, 2) : null;
     try {
-      native.embed(this._w('embed').h._h, L, bufs.ids.ptr, bufs.x.ptr, this.lead._h);
+      if (timer) native.timerMark(timer, 0, this.lead._h);
+      this._step('embed', () => native.embed(this._w('embed').h._h, L, bufs.ids.ptr, bufs.x.ptr, this.lead._h));
       this.types.forEach((t, i) => {
-        const P = 'layers.' + i + '.';
-        this._norm(L, L, bufs.x, i > 0 ? bufs.y : null, P + 'in_norm', bufs.h, false, null);
+        const P = 'layers.' + i + '.', S = 'L' + i + '/';
+        this._step(S + 'in_norm', () => this._norm(L, L, bufs.x, i > 0 ? bufs.y : null, P + 'in_norm', bufs.h, false,
+          null));
+        if (debug && i > 0) layers.push(bufs.x.download(new Float32Array(L * D)));
         if (t === 'adapter') {  // x += proj(rms_norm(x)) + bias, the add in the next norm (engine.js:256-261)
-          this._matmul(L, bufs.h, P + 'proj', bufs.y);
-          native.addBias(L, D, bufs.y.ptr, this._v(P + 'bias').ptr, this.device, this.lead._h);
+          this._matmul(L, bufs.h, P + 'proj', bufs.y, S + 'proj');
+          this._step(S + 'bias', () => native.addBias(L, D, bufs.y.ptr, this._v(P + 'bias').ptr, this.device,
+            this.lead._h));
           snaps.push(null);
           return;
         }
-        const stride = t === 'linear_attention' ? this.mixers[i].config.linStride : this.mixers[i].config.fullStride;
-        const pname = P + (t === 'linear_attention' ? 'in_proj' : 'qkv');
-        if (this._w(pname).N !== stride) throw new Error(pname + ' has ' + this._w(pname).N + ' columns, the mixer reads rows of ' + stride);
-        this._matmul(L, bufs.h, pname, bufs.big);
-        const r = this.mixers[i].forward(L, [bufs.big], [bufs.o],
-          { cache: cache ? cache.layers[i] : null, keepCache: keep });
+        const lin = t === 'linear_attention';
+        const stride = lin ? this.mixers[i].config.linStride : this.mixers[i].config.fullStride;
+        const pname = lin ? 'in_proj' : 'qkv';
+        if (this._w(P + pname).N !== stride) {
+          throw new Error(P + pname + ' has ' + this._w(P + pname).N + ' columns, the mixer reads rows of ' + stride);
+        }
+        this._matmul(L, bufs.h, P + pname, bufs.big, S + pname);
+        const r = this._step(S + (lin ? 'gdn' : 'attn'), () => this.mixers[i].forward(L, [bufs.big], [bufs.o],
+          { cache: cache ? cache.layers[i] : null, keepCache: keep }));
         snaps.push(r.cache);
-        this._matmul(L, bufs.o, P + (t === 'linear_attention' ? 'out_proj' : 'o_proj'), bufs.y);
-        this._norm(L, L, bufs.x, bufs.y, P + 'post_norm', bufs.h, false, null);
-        this._matmul(L, bufs.h, P + 'gate_up', bufs.big);
-        native.siluMul(L, I, bufs.big.ptr, bufs.mid.ptr, this.device, this.lead._h);
-        this._matmul(L, bufs.mid, P + 'down', bufs.y);
+        this._matmul(L, bufs.o, P + (lin ? 'out_proj' : 'o_proj'), bufs.y, S + (lin ? 'out_proj' : 'o_proj'));
+        this._step(S + 'post_norm', () => this._norm(L, L, bufs.x, bufs.y, P + 'post_norm', bufs.h, false, null));
+        this._matmul(L, bufs.h, P + 'gate_up', bufs.big, S + 'gate_up');
+        this._step(S + 'silu', () => native.siluMul(L, I, bufs.big.ptr, bufs.mid.ptr, this.device, this.lead._h));
+        this._matmul(L, bufs.mid, P + 'down', bufs.y, S + 'down');
       });
       const out = new Float32Array(R.length * D);
       if (R.length) {
         bufs.rows.upload(Uint32Array.from(R));
-        this._norm(R.length, L, bufs.x, bufs.y, 'final_norm', bufs.out, true, bufs.rows);
-        bufs.out.download(out);  // synchronous on the shared stream
+        this._step('final_norm', () => this._norm(R.length, L, bufs.x, bufs.y, 'final_norm', bufs.out, true,
+          bufs.rows));
       }
+      if (timer) native.timerMark(timer, 1, this.lead._h);
+      if (R.length) bufs.out.download(out);  // synchronous on the shared stream
       const c = this.unrotate;  // rotated torso: the original basis is c * FWHT(row) (engine.js:365-366)
       if (c) for (let r = 0; r < R.length; r++) { fwhtHost(out, r * D, D); for (let j = 0; j < D; j++) out[r * D + j] *= c[j]; }
       let snap = null;
@@ -395,9 +426,38 @@ class Torso {
         snap = { P: (cache ? cache.P : 0) + L, ids: (cache ? cache.ids : []).concat(Array.from(ids)), layers: snaps,
           release: function () { snaps.forEach((s) => { if (s) s.release(); }); } };
       }
-      return { hidden: out, d: D, cache: snap };
+      const res = { hidden: out, d: D, cache: snap, fetch_ms: fetchMs };
+      if (timer) res.gpu_ms = native.timerElapsed(timer, 0, 1);
+      if (debug) res.layers = layers;
+      return res;
     } finally {
       this.lead.synchronize();  // the next call may overwrite the work buffers
+      if (timer) native.timerDestroy(timer);
+    }
+  }
+  /*
+   * GPU time of every step of a forward over ids (options as forward), summed over the layers by the step's name
+   * without its layer prefix (embed, in_norm, in_proj, gdn, out_proj, qkv, attn, o_proj, post_norm, gate_up, silu,
+   * down, proj, bias, .../had, final_norm), in ms to 2 decimals, largest first (engine.js:292-307). Diagnostics
+   * only: a timestamp pair brackets every step. The reference's `force` (its matmul kernel override) has no
+   * counterpart here: there is one projection kernel.
+   */
+  profile(ids, options) {
+    const cap = 2 * (3 + 16 * this.types.length);
+    this._prof = { timer: native.timerCreate(this.device, cap), cap: cap, labels: [] };
+    try {
+      this.forward(ids, [], options);
+      const by = {};
+      this._prof.labels.forEach((label, k) => {
+        const name = label.replace(/^L\d+\//, '');
+        by[name] = (by[name] || 0) + native.timerElapsed(this._prof.timer, 2 * k, 2 * k + 1);
+      });
+      const out = {};
+      Object.keys(by).sort((a, b) => by[b] - by[a]).forEach((k) => { out[k] = +by[k].toFixed(2); });
+      return out;
+    } finally {
+      native.timerDestroy(this._prof.timer);
+      this._prof = null;
     }
   }
   // Work buffers for L rows and R returned rows, kept between calls and grown when a call needs more (no device

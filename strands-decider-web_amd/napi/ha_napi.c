@@ -16,7 +16,7 @@
 #include "ha.h"
 
 /* Every external holds one of these boxes; `kind` tells them apart, so a handle of the wrong kind is a TypeError. */
-enum { BOX_ENGINE = 0x45, BOX_SNAPSHOT = 0x53, BOX_MNB = 0x4d };
+enum { BOX_ENGINE = 0x45, BOX_SNAPSHOT = 0x53, BOX_MNB = 0x4d, BOX_TIMER = 0x54 };
 
 typedef struct engine_box {
   int kind;
@@ -37,6 +37,11 @@ typedef struct {
   int kind;
   ha_mnb* w;
 } mnb_box;
+
+typedef struct {
+  int kind;
+  ha_timer* t;
+} timer_box;
 
 static napi_value throw_status(napi_env env, int rc) {
   char code[16];
@@ -130,6 +135,7 @@ static void* get_box(napi_env env, napi_value v, int kind) {
 static engine_box* get_engine(napi_env env, napi_value v) { return (engine_box*)get_box(env, v, BOX_ENGINE); }
 static snap_box* get_snap(napi_env env, napi_value v) { return (snap_box*)get_box(env, v, BOX_SNAPSHOT); }
 static mnb_box* get_mnb(napi_env env, napi_value v) { return (mnb_box*)get_box(env, v, BOX_MNB); }
+static timer_box* get_timer(napi_env env, napi_value v) { return (timer_box*)get_box(env, v, BOX_TIMER); }
 
 /* host bytes of a TypedArray / ArrayBuffer view */
 static int get_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
@@ -183,6 +189,13 @@ static void mnb_finalize(napi_env env, void* data, void* hint) {
   (void)env; (void)hint;
   mnb_box* b = (mnb_box*)data;
   if (b->w) ha_mnb_destroy(b->w);
+  free(b);
+}
+
+static void timer_finalize(napi_env env, void* data, void* hint) {
+  (void)env; (void)hint;
+  timer_box* b = (timer_box*)data;
+  if (b->t) ha_timer_destroy(b->t);
   free(b);
 }
 
@@ -615,6 +628,75 @@ static napi_value js_mnb_destroy(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* timerCreate(device, n): n GPU timestamps (a WebGPU timestamp query set's counterpart) */
+static napi_value js_timer_create(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  int32_t device, n;
+  if (napi_get_value_int32(env, argv[0], &device) != napi_ok || napi_get_value_int32(env, argv[1], &n) != napi_ok)
+    return type_error(env, "device and n must be integers");
+  ha_timer* t = NULL;
+  CHECK_HA(ha_timer_create(device, n, &t));
+  timer_box* b = (timer_box*)malloc(sizeof(timer_box));
+  if (!b) {
+    ha_timer_destroy(t);
+    return type_error(env, "out of host memory");
+  }
+  b->kind = BOX_TIMER;
+  b->t = t;
+  napi_value r;
+  if (napi_create_external(env, b, timer_finalize, NULL, &r) != napi_ok) {
+    ha_timer_destroy(t);
+    free(b);
+    napi_throw_error(env, NULL, "napi_create_external failed");
+    return NULL;
+  }
+  return r;
+}
+
+/* timerMark(timer, i, engine|null): timestamp i after the work queued so far on the engine's stream */
+static napi_value js_timer_mark(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return NULL;
+  timer_box* tb = get_timer(env, argv[0]);
+  if (!tb || !tb->t) return type_error(env, "not a live timer handle");
+  int32_t i;
+  void* st;
+  if (napi_get_value_int32(env, argv[1], &i) != napi_ok) return type_error(env, "i must be an integer");
+  if (!stream_of(env, argv[2], &st)) return type_error(env, "the last argument must be an engine handle or null");
+  CHECK_HA(ha_timer_mark(tb->t, i, st));
+  return NULL;
+}
+
+/* timerElapsed(timer, i, j) -> milliseconds from timestamp i to j (waits for both) */
+static napi_value js_timer_elapsed(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return NULL;
+  timer_box* tb = get_timer(env, argv[0]);
+  if (!tb || !tb->t) return type_error(env, "not a live timer handle");
+  int32_t i, j;
+  if (napi_get_value_int32(env, argv[1], &i) != napi_ok || napi_get_value_int32(env, argv[2], &j) != napi_ok)
+    return type_error(env, "i and j must be integers");
+  float ms = 0.0f;
+  CHECK_HA(ha_timer_elapsed(tb->t, i, j, &ms));
+  napi_value r;
+  CHECK_NAPI(napi_create_double(env, (double)ms, &r));
+  return r;
+}
+
+static napi_value js_timer_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  timer_box* tb = get_timer(env, argv[0]);
+  if (!tb) return type_error(env, "not a timer handle");
+  if (tb->t) {
+    ha_timer* t = tb->t;
+    tb->t = NULL;
+    CHECK_HA(ha_timer_destroy(t));
+  }
+  return NULL;
+}
+
 /* fwht(x: BigInt, elems, n, device, engine|null) */
 static napi_value js_fwht(napi_env env, napi_callback_info info) {
   napi_value argv[5];
@@ -741,6 +823,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"embed", js_embed},                  {"addNorm", js_add_norm},
       {"siluMul", js_silu_mul},             {"addBias", js_add_bias},
       {"shareStream", js_share_stream},
+      {"timerCreate", js_timer_create},     {"timerMark", js_timer_mark},
+      {"timerElapsed", js_timer_elapsed},   {"timerDestroy", js_timer_destroy},
   };
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); i++) {
     napi_value f;

@@ -4,7 +4,9 @@
 // L1 more tokens, returning final-normed hidden rows. Files in the directory named by the first argument:
 //   spec.json {types, D, I, L0, L1, rows0, rows1, weights: {name: {N, K}}, vectors: [names], mixer: [[i, name]...]}
 //   w_<name>.q / w_<name>.s (u32 blocks, f16 scales), v_<name>.bin (f32), ids0.bin / ids1.bin (u32)
-// and writes hidden0.bin / hidden1.bin (f32 rows x D).
+// and writes hidden0.bin / hidden1.bin (f32 rows x D). Then the diagnostics: a forward over ids0 with timestamps and
+// debugLayers (layers.bin: the residual stream entering layers 1.., f32 [n-1][L0][D]) and a profile(); prints
+// {gpu_ms, n_layers, profile} as JSON.
 const fs = require('fs');
 const path = require('path');
 const ha = require(path.join(__dirname, '..', '..', 'strands-decider-web_amd', 'js', 'engine.js'));
@@ -32,7 +34,18 @@ if (!r0.cache || r0.cache.P !== spec.L0) throw new Error('cache P ' + (r0.cache 
 const r1 = torso.forward(u32('ids1.bin'), spec.rows1, { cache: r0.cache });
 fs.writeFileSync(path.join(dir, 'hidden1.bin'), Buffer.from(r1.hidden.buffer));
 r0.cache.release();
+const rd = torso.forward(u32('ids0.bin'), spec.rows0, { timestamps: true, debugLayers: true });
+const stack = new Float32Array(rd.layers.length * spec.L0 * spec.D);
+rd.layers.forEach((x, i) => stack.set(x, i * spec.L0 * spec.D));
+fs.writeFileSync(path.join(dir, 'layers.bin'), Buffer.from(stack.buffer));
+for (let j = 0; j < rd.hidden.length; j++) {
+  if (rd.hidden[j] !== r0.hidden[j] && !(Number.isNaN(rd.hidden[j]) && Number.isNaN(r0.hidden[j]))) {
+    throw new Error('diagnostics changed the hidden rows');
+  }
+}
+const prof = torso.profile(u32('ids0.bin'));
 torso.dropWeights();  // the weight handles borrow these buffers
 keep.forEach((b) => b.free());  // the weight buffers live on the torso's lead engine: free them before destroy()
 torso.destroy();
-console.log(JSON.stringify({ ok: true }));
+console.log(JSON.stringify({ ok: true, gpu_ms: rd.gpu_ms, fetch_ms: rd.fetch_ms, n_layers: rd.layers.length,
+  profile: prof }));

@@ -97,4 +97,8 @@ def test_forged_handles_are_refused_not_read():
         assert lib.ha_destroy(h) == ha.HA_ERR_HANDLE
         assert lib.ha_set_stream(h, None) == ha.HA_ERR_HANDLE
         assert lib.ha_share_scratch(h, h) == ha.HA_ERR_HANDLE
+        ms = ctypes.c_float()
+        assert lib.ha_timer_mark(h, 0, None) == ha.HA_ERR_HANDLE
+        assert lib.ha_timer_elapsed(h, 0, 0, ctypes.byref(ms)) == ha.HA_ERR_HANDLE
+        assert lib.ha_timer_destroy(h) == ha.HA_ERR_HANDLE
     assert buf[0] == 0x4841454E  # nothing wrote through the forged handles

@@ -84,9 +84,10 @@ def _torso(W, V, M):
     return t
 
 
-def _oracle(W, V, M, ids, rows, deq=None):
+def _oracle(W, V, M, ids, rows, deq=None, trace=None):
     """fp64 composition, rounding to f16 where the reference stores f16; one forward over all of ids. `deq` keeps
-    the dequantised weights between calls on one model."""
+    the dequantised weights between calls on one model; `trace` (a list) receives the residual stream x entering
+    each layer after the first (after the residual add that opens it)."""
     f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).astype(np.float64)  # noqa: E731
     deq = {} if deq is None else deq
 
@@ -105,6 +106,8 @@ def _oracle(W, V, M, ids, rows, deq=None):
     for i, t in enumerate(TYPES):
         p = "layers.%d." % i
         h, x = to.add_norm(x, y, V[p + "in_norm"])
+        if trace is not None and i > 0:
+            trace.append(np.array(x, np.float64))
         h = f16(h)
         if t == "adapter":
             y = f16(mm(h, p + "proj") + V[p + "bias"][None, :])
@@ -147,6 +150,7 @@ def test_torso_forward_node_matches_c_abi_and_oracle(tmp_path):
     r = subprocess.run([shutil.which("node"), os.path.join(ROOT, "tests", "js", "napi_torso.js"), d],
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
+    info = json.loads(r.stdout.strip().splitlines()[-1])
     js0 = np.fromfile(os.path.join(d, "hidden0.bin"), np.float32).reshape(len(ROWS0), D)
     js1 = np.fromfile(os.path.join(d, "hidden1.bin"), np.float32).reshape(len(ROWS1), D)
 
@@ -166,3 +170,24 @@ def test_torso_forward_node_matches_c_abi_and_oracle(tmp_path):
     # the mixers' prefix + suffix is bit-exact, and at 9 and 49 rows the projections take the same per-row path
     # (the MFMA GEMV, M <= 64), so the resumed rows equal those of one forward bit for bit
     assert np.array_equal(full[len(ROWS0):], py1)
+
+    # diagnostics (engine.js:292-307, 331-348): the residual stream entering layers 1.. against the oracle's and, bit
+    # for bit, the Python mirror's; the GPU time of the forward; a per-step profile naming every kind of step
+    trace = []
+    _oracle(W, V, M, ids[:L0], ROWS0, trace=trace)
+    js_layers = np.fromfile(os.path.join(d, "layers.bin"), np.float32).reshape(len(TYPES) - 1, L0, D)
+    t.forward(ids[:L0], ROWS0, timestamps=True, debug_layers=True)
+    assert info["n_layers"] == len(TYPES) - 1 and len(t.diag["layers"]) == len(TYPES) - 1
+    for i, (a, b, ref_x) in enumerate(zip(js_layers, t.diag["layers"], trace)):
+        assert np.array_equal(a, b), "layer %d residual differs between Node and the C ABI" % (i + 1)
+        e = mo.rel_err(a, ref_x)
+        print("residual entering layer %d vs oracle: %.1e" % (i + 1, e))
+        assert e < 1e-2
+    print("gpu_ms Node %.3f, Python %.3f; fetch_ms %.3f; profile %s" % (
+        info["gpu_ms"], t.diag["gpu_ms"], info["fetch_ms"], info["profile"]))
+    assert 0 < info["gpu_ms"] < 1000 and 0 < t.diag["gpu_ms"] < 1000
+    prof, pyprof = info["profile"], t.profile(ids[:L0])
+    for step in ("embed", "in_norm", "in_proj", "gdn", "out_proj", "qkv", "attn", "o_proj", "proj", "bias",
+                 "post_norm", "gate_up", "silu", "down"):
+        assert step in prof and step in pyprof, step
+    assert list(prof.values()) == sorted(prof.values(), reverse=True)
