@@ -55,13 +55,16 @@ typedef enum ha_layer_kind {
 typedef enum ha_dtype { HA_F32 = 0, HA_F16 = 1 } ha_dtype;
 
 typedef enum ha_recurrence {
-  HA_CHUNKED = 0,       /* prefill form: chunks of 64 rows at absolute positions, MFMA products (default; the
-                           engine picks one of the two implementations below from its batch and head count: the
-                           split form for at most 32 sequence-heads, the fused kernel otherwise) */
-  HA_SEQUENTIAL = 1,    /* token-by-token fp32 rule with the state in registers (decode / resume) */
-  HA_CHUNKED_FUSED = 2, /* the chunked form in one kernel per layer: one workgroup per (sequence, head) */
-  HA_CHUNKED_SPLIT = 3  /* the chunked form in two kernels: every chunk's state-independent part at once, then the
-                           recurrence over the chunks */
+  HA_CHUNKED = 0,        /* prefill form: chunks at absolute positions, MFMA products, the state stored at the last
+                            64-row boundary (default; the engine picks one of the implementations below from its batch
+                            and head count B*H: the split form up to 16, the paired form up to 128, the fused kernel
+                            beyond) */
+  HA_SEQUENTIAL = 1,     /* token-by-token fp32 rule with the state in registers (decode / resume) */
+  HA_CHUNKED_FUSED = 2,  /* the chunked form in one kernel per layer: one workgroup per (sequence, head), 64-row chunks */
+  HA_CHUNKED_SPLIT = 3,  /* the chunked form in two kernels: every chunk's state-independent part at once, then the
+                            recurrence over the chunks */
+  HA_CHUNKED_PAIRED = 4  /* the chunked form on two workgroups per (sequence, head), 32-row chunks: one prepares the
+                            chunks' tiles, the other runs the recurrence (B*H a multiple of 8, at most 128) */
 } ha_recurrence;
 
 /* Engine shape. Field names follow the manifest config keys (export_engine.py:83). */

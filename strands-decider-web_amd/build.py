@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libha.so")
 NAPI_OUT = os.path.join(HERE, "js", "ha_napi.node")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["engine.cpp", "gdn_seq.hip", "gdn_chunk.hip", "gdn_split.hip", "gqa.hip", "tail.hip", "mnb.hip", "torso.hip"]
+SOURCES = ["engine.cpp", "gdn_seq.hip", "gdn_chunk.hip", "gdn_duo.hip", "gdn_split.hip", "gqa.hip", "tail.hip", "mnb.hip", "torso.hip"]
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]

@@ -83,10 +83,11 @@ struct Scratch {
     size_t bytes = 0;
   };
   int device = 0;
-  Buf img, seq_raw, seq_cnt, gqa_part, zeros;
+  Buf img, seq_raw, seq_cnt, gqa_part, zeros, duo_ring, duo_flags;
+  unsigned duo_epoch = 0;  // the paired form's counter epoch of the last launch (the counters start at zero)
   ~Scratch() {
     (void)hipSetDevice(device);
-    for (Buf* b : {&img, &seq_raw, &seq_cnt, &gqa_part, &zeros})
+    for (Buf* b : {&img, &seq_raw, &seq_cnt, &gqa_part, &zeros, &duo_ring, &duo_flags})
       if (b->p) (void)hipFree(b->p);
   }
 };
@@ -123,7 +124,8 @@ struct ha_engine {
   // images [B][H][img_chunks] of the two-kernel form (allocated when a call can use that form), the sequential
   // form's raw outputs [B][H][kSegRows][DV] and counters [B][H], split-GQA partials [gqa_part_slots]
   std::shared_ptr<Scratch> scratch;
-  size_t need_zeros = 0, need_img = 0, need_seq_raw = 0, need_seq_cnt = 0, need_gqa = 0;
+  size_t need_zeros = 0, need_img = 0, need_seq_raw = 0, need_seq_cnt = 0, need_gqa = 0, need_duo_ring = 0,
+         need_duo_flags = 0;
   int img_chunks = 0;
   int gqa_split = 0, gqa_part_slots = 0;
   hipEvent_t ev[2] = {nullptr, nullptr};
@@ -166,9 +168,12 @@ const ha_engine* snapshot_owner(const ha_snapshot* s) {
   return (e && g_live.count(e) && e->id == s->owner_id) ? e : nullptr;
 }
 
-// HA_CHUNKED's choice of the two-kernel gated-delta form: few (sequence, head) recurrences for the 256 CUs (measured
-// crossover at T = 2048: B*H between 32 and 48). From the engine's shape alone, so every call rounds alike.
-bool split_by_shape(const ha_config& c) { return c.batch * c.H <= 32; }
+// HA_CHUNKED's choice of gated-delta prefill, from the engine's shape alone so that every call rounds alike: the
+// two-kernel form for one sequence's heads, the paired form while two workgroups per recurrence fit the 256 CUs, the
+// fused kernel beyond. Measured per layer at T = 2048 (split / paired / fused, us): B=1 186 / 196 / -, B=2 229 / 197 /
+// 280, B=4 - / 226 / 295, B=8 - / 292 / 313.
+bool split_by_shape(const ha_config& c) { return c.batch * c.H <= 16; }
+bool paired_by_shape(const ha_config& c) { return !split_by_shape(c) && ha::gdn_duo_fits(c.batch, c.H); }
 
 int check_config(const ha_config* c) {
   if (!c) return fail(HA_ERR_ARG, "config is NULL");
@@ -340,9 +345,14 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
     e->need_img = ha::gdn_split_image_bytes() * B * c.H * e->img_chunks;
     e->need_seq_raw = sizeof(float) * B * c.H * ha::kSegRows * c.DV;
     e->need_seq_cnt = sizeof(unsigned) * B * c.H;
+    // the paired form's tile-set ring and progress counters, likewise only where HA_CHUNKED picks that form
+    e->need_duo_ring = (size_t)ha::kDuoRing * ha::kDuoSetBytes * B * c.H;
+    e->need_duo_flags = sizeof(unsigned) * 64 * B * c.H;
     if ((rc = grow(e->scratch->zeros, e->need_zeros)) || (rc = grow(e->scratch->seq_raw, e->need_seq_raw)) ||
         (rc = grow(e->scratch->seq_cnt, e->need_seq_cnt)) ||
-        (split_by_shape(c) && (rc = grow(e->scratch->img, e->need_img))))
+        (split_by_shape(c) && (rc = grow(e->scratch->img, e->need_img))) ||
+        (paired_by_shape(c) && ((rc = grow(e->scratch->duo_ring, e->need_duo_ring)) ||
+                                (rc = grow(e->scratch->duo_flags, e->need_duo_flags)))))
       return bail(rc);
   }
   if (e->any_full) {
@@ -399,7 +409,9 @@ int ha_share_scratch(ha_engine* e, ha_engine* holder) {
   // images only where e had them (its shape picks the two-kernel form, or a call forced it)
   if ((rc = grow(to.zeros, e->need_zeros)) || (rc = grow(to.img, from.img.bytes ? e->need_img : 0)) ||
       (rc = grow(to.seq_raw, e->need_seq_raw)) ||
-      (rc = grow(to.seq_cnt, e->need_seq_cnt)) || (rc = grow(to.gqa_part, e->need_gqa)))
+      (rc = grow(to.seq_cnt, e->need_seq_cnt)) || (rc = grow(to.gqa_part, e->need_gqa)) ||
+      (rc = grow(to.duo_ring, from.duo_ring.bytes ? e->need_duo_ring : 0)) ||
+      (rc = grow(to.duo_flags, from.duo_flags.bytes ? e->need_duo_flags : 0)))
     return rc;
   e->scratch = holder->scratch;
   return HA_OK;
@@ -460,7 +472,9 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   if ((long)P + L > c.max_ctx)
     return fail(HA_ERR_CONTEXT, "context " + std::to_string((long)P + L) + " exceeds " + std::to_string(c.max_ctx));
   const int mode = opts ? opts->recurrence : HA_CHUNKED;
-  if (mode < HA_CHUNKED || mode > HA_CHUNKED_SPLIT) return fail(HA_ERR_ARG, "unknown recurrence mode");
+  if (mode < HA_CHUNKED || mode > HA_CHUNKED_PAIRED) return fail(HA_ERR_ARG, "unknown recurrence mode");
+  if (mode == HA_CHUNKED_PAIRED && !ha::gdn_duo_fits(c.batch, c.H))
+    return fail(HA_ERR_ARG, "the paired form needs batch * H a multiple of 8 and at most 128");
   const bool chunked = mode != HA_SEQUENTIAL;
   const bool timing = opts && (opts->timestamps || opts->layer_ms);
   HA_HIP(hipSetDevice(e->device));
@@ -480,15 +494,19 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
 
   const int end = P + L;
   const int s1 = chunked ? s0 + ha::kChunk * ((end - s0) / ha::kChunk) : end;  // new state position
-  // HA_CHUNKED picks the implementation from the engine's shape alone: the two-kernel form when there are few
-  // (sequence, head) recurrences for the 256 CUs (measured crossover at T = 2048: B*H between 32 and 48), the fused
-  // kernel otherwise. The two round differently, so the choice must not depend on the call (a resumed suffix must
-  // match the same rows of one longer forward bit for bit).
+  // HA_CHUNKED picks the implementation from the engine's shape alone (split_by_shape, paired_by_shape). The forms
+  // round differently, so the choice must not depend on the call: a resumed suffix must match the same rows of one
+  // longer forward bit for bit.
   const bool split = mode == HA_CHUNKED_SPLIT || (mode == HA_CHUNKED && split_by_shape(c));
+  const bool paired = mode == HA_CHUNKED_PAIRED || (mode == HA_CHUNKED && paired_by_shape(c));
   Scratch& sc = *e->scratch;
   if (e->any_linear && chunked && split && sc.img.bytes < e->need_img) {
     int rc = grow(sc.img, e->need_img);  // first call that forces the two-kernel form on a larger shape
     if (rc) return rc;
+  }
+  if (e->any_linear && chunked && paired && (sc.duo_ring.bytes < e->need_duo_ring || sc.duo_flags.bytes < e->need_duo_flags)) {
+    int rc;  // first call that forces the paired form on another shape
+    if ((rc = grow(sc.duo_ring, e->need_duo_ring)) || (rc = grow(sc.duo_flags, e->need_duo_flags))) return rc;
   }
   // raw-row tails: the copy reads only the call's input rows and the resumed tail, so the layers' copies are
   // gathered into one launch after the mixers (per layer when per-layer times are asked for, so that each layer's
@@ -518,9 +536,31 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.conv_w = l.conv; a.negA = l.negA; a.dtb = l.dtb; a.gnorm = c.lin_gnorm ? l.gnorm : nullptr;
       a.img = sc.img.p; a.img_chunks = e->img_chunks;
       a.seq_raw = static_cast<float*>(sc.seq_raw.p); a.seq_cnt = static_cast<unsigned*>(sc.seq_cnt.p);
-      hipError_t he = !chunked ? ha::launch_gdn_sequential(a, st)
-                      : split ? ha::launch_gdn_split(a, st)
-                              : ha::launch_gdn_chunked(a, st);
+      hipError_t he;
+      if (!chunked) {
+        he = ha::launch_gdn_sequential(a, st);
+      } else if (split) {
+        he = ha::launch_gdn_split(a, st);
+      } else if (paired) {
+        // a fresh counter epoch per launch; before the epoch field (24 bits) runs out, the counters are cleared
+        if (sc.duo_epoch + 1 >= (1u << 24)) {
+          HA_HIP(hipStreamSynchronize(st));
+          HA_HIP(hipMemset(sc.duo_flags.p, 0, sc.duo_flags.bytes));
+          sc.duo_epoch = 0;
+        }
+        a.duo_ring = sc.duo_ring.p; a.duo_flags = static_cast<unsigned*>(sc.duo_flags.p); a.duo_epoch = ++sc.duo_epoch;
+        he = ha::launch_gdn_duo(a, st);
+        // The device refuses a cooperative launch while another process holds its cooperative dispatch (it has made
+        // such launches and is still alive), or when the pairs do not fit the free CUs: the fused kernel runs instead.
+        // It rounds differently, so a resumed suffix matches one longer forward bit for bit only when both ran the
+        // same form.
+        if (he == hipErrorIllegalState || he == hipErrorCooperativeLaunchTooLarge) {
+          (void)hipGetLastError();
+          he = ha::launch_gdn_chunked(a, st);
+        }
+      } else {
+        he = ha::launch_gdn_chunked(a, st);
+      }
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " gated-delta launch: " + hipGetErrorString(he));
       t.in[t.n] = a.in; t.tail[t.n] = a.tail; t.tail_out[t.n] = l.tail; t.n++;
       if ((opts && opts->layer_ms) || t.n == ha::kTailLayers) {

@@ -1,0 +1,719 @@
+// Chunked gated-delta prefill on two CUs per (sequence, head) (ha_recurrence HA_CHUNKED for 32 < B*H <= 128,
+// HA_CHUNKED_PAIRED), gfx950.
+//
+// Same semantics as the sequential rule (reference web/public/engine/wgsl.js:124-187 + 252-268), evaluated in the
+// chunked WY/UT form (Yang et al. 2024, "Parallelizing Linear Transformers with the Delta Rule over Sequence
+// Length"; Yang, Kautz & Hatamizadeh, "Gated Delta Networks"). For a chunk of 32 rows with cumulative log-decay gc
+// and the state S at its start:
+//   A   = strictly_lower(beta_t (k^_t . k^_t') exp(gc_t - gc_t'))      T = (I + A)^-1
+//   V_new = T diag(beta) v - T diag(beta e^gc) (k^ S)
+//   o_t = exp(gc_t) q^_t S + sum_{t'<=t} (q^_t . k^_t') exp(gc_t - gc_t') V_new_t'
+//   S  <- exp(gc_31) S + k^T diag(exp(gc_31 - gc)) V_new
+//
+// One CU's VALU and latency chains bound a one-workgroup form at a period of about 10K cycles per 32 rows, and at
+// B = 8 half the CUs have no head. So each (sequence, head) gets two workgroups, both resident (cooperative launch):
+//   producer: everything that does not depend on the state, chunk by chunk: q/k conv + SiLU + l2 norm, the gates, the
+//     A and score tiles, T = (I + A)^-1, T diag(beta) and T diag(beta e^gc). In one period wave 0 runs chunk q's T
+//     chain, waves 1..2 its score tiles, wave 3 chunk q + 1's gates, waves 4..7 chunk q + 1's q/k conv, and waves
+//     1..3 copy chunk q - 1's finished tile set (36 KiB) into a ring of 6 slots in device memory.
+//   consumer: waves 0..3 own 32 value columns each of the fp32 state in MFMA accumulators and do the state work of
+//     chunk p; meanwhile waves 4..7 (helpers) DMA chunk p + 1's tile set from the ring into LDS, apply the gated
+//     RMSNorm to chunk p - 1's output and store it, and run chunk p + 1's v conv.
+// Each role passes one workgroup barrier per period.
+// The two exchange progress through counters: `produced` (tile sets in the ring) and `consumed` (sets copied into the
+// consumer's LDS, so their slots may be reused). Counter values carry a per-launch epoch (epoch * 256 + chunks), so
+// values left by earlier launches never satisfy a wait and nothing is cleared between launches. Data is written with
+// device-coherent (sc1) stores and waited for (vmcnt 0) before the counter store; readers load counters and data with
+// sc1. Every wait is bounded.
+//
+// Chunk boundaries sit at s0 + 32k and the state advances over every complete chunk. The state written out is the
+// one at the end of the call's last complete 64-row span (the position the engine stores it at); a resumed call
+// replays the rows from there with the same chunk boundaries, so prefix + suffix is bit-identical to one forward.
+//
+// MFMA operand conventions are those of gdn_common.h: lane l supplies row (l & 15) of A and column (l & 15) of B;
+// a D tile pair reused as a B operand is matched by A operands read in the permuted K order
+// {4 grp + e} U {16 + 4 grp + e}.
+#include "gdn_common.h"
+
+namespace ha {
+namespace {
+
+constexpr int kC = 32;          // chunk rows
+constexpr int kP = kC + 8;      // row pitch (halves) of [*][32] f16 tiles
+constexpr int kMP = kC + 4;     // row pitch (floats) of the fp32 A / T tile
+constexpr int kThreads = 512;   // 8 waves per workgroup
+constexpr int kOP = kDV + 4;    // row pitch (floats) of the consumer's output rows
+
+typedef int i4v __attribute__((ext_vector_type(4)));
+
+// One chunk's tiles, as the producer builds them in LDS and the consumer reads them; copied between the two as bytes.
+struct Set {
+  _Float16 Qs[kC * kQP];   // q^ / sqrt(DK), [t][i]
+  _Float16 Ks[kC * kQP];   // k^, [t][i]
+  _Float16 KT[kDK * kP];   // k^ transposed, [i][t], 8-column groups swizzled by kt32
+  _Float16 Tb[kC * kP];    // T diag(beta), [t][t'] (the block above the diagonal stays zero)
+  _Float16 Tw[kC * kP];    // T diag(beta e^gc)
+  _Float16 Att[kC * kP];   // decay-masked causal q^ k^T
+  float gc[kC];            // cumulative log decay inside the chunk
+  float eg[kC];            // e^gc
+  float bt[kC];            // beta
+  float ed[kC];            // e^(gc_31 - gc)
+  float rowf[kC];          // e^(gc_t - gc_16(t/16)), in (0, 1]
+  float brow[kC];          // beta_t rowf_t
+  float colf[kC];          // e^(gc_16 - gc_t') for t' < 16, in (0, 1]
+};
+static_assert(sizeof(Set) <= kDuoSetBytes, "a tile set fits one ring slot");
+static_assert(kDuoSetBytes % 1024 == 0, "ring slots are whole 1 KiB DMA instructions");
+union SetBuf {
+  Set s;
+  unsigned char raw[kDuoSetBytes];
+};
+
+struct ProducerLds {
+  SetBuf s[3];                 // chunk q (T chain), q + 1 (written by the conv waves), q - 1 (copied out), by c % 3
+  float Tm[kC * kMP];          // A, then T, fp32
+  float cwq[4][64][kKC];       // q/k conv taps: channel 4 g + c (g < 64: q then k) at cwq[c][g]
+};
+struct ConsumerLds {
+  SetBuf s[2];                 // chunk p (state waves) and chunk p + 1 (DMA target)
+  _Float16 VT[2][kDV * kP];    // v^ transposed, [j][t], by chunk parity
+  float osg[2][kC * kOP];      // output rows before the gated norm, by chunk parity
+  float red[2][kC * 4];        // gated-norm partial sums, [t][state wave], by chunk parity
+  float cwv[4][32][kKC];       // v conv taps: channel 4 g + c at cwv[c][g]
+};
+
+// k^T element (i, t) lives at i * kP + 8 * ((t / 8) ^ ((i / 16) % 4)) + t % 8: a producer lane writes 8 rows of one
+// channel (16 bytes) and the 32 lanes writing channels 4 l + c land on different banks
+__device__ __forceinline__ int kt32(int i, int g8) { return i * kP + 8 * (g8 ^ ((i >> 4) & 3)); }
+
+// perm_a for the swizzled k^T tile (one K block of 32 chunk rows)
+__device__ __forceinline__ h8 perm_a_kt32(const _Float16* kt, int r, int grp) {
+  const int sub = 4 * (grp & 1);
+  const h4 lo = *reinterpret_cast<const h4*>(kt + kt32(r, grp >> 1) + sub);
+  const h4 hi = *reinterpret_cast<const h4*>(kt + kt32(r, 2 + (grp >> 1)) + sub);
+  return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// sum over 32 lanes (0..31 or 32..63): the 16 lanes of a DPP row, then the paired row
+__device__ __forceinline__ float sum32(float v) {
+  v = row_sum16(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v), false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
+// Progress counters: device-coherent loads and stores (no release fence: the writer drains its data stores first)
+__device__ __forceinline__ unsigned ld_counter(const unsigned* c) {
+  return __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_counter(unsigned* c, unsigned v) {
+  __hip_atomic_store(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until the counter reaches v and returns the value read. Bounded (2^16 polls of about a microsecond; a partner
+// is normally a period or more ahead, a few microseconds): if the partner never gets there the caller goes on with
+// whatever the buffers hold, so the kernel still ends. Callers keep the value and poll again only when it falls short.
+__device__ __forceinline__ unsigned wait_counter(const unsigned* c, unsigned v) {
+  unsigned x = 0;
+  for (int i = 0; i < (1 << 16); i++) {
+    x = ld_counter(c);
+    if (x >= v) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return x;
+}
+
+// Loads rows cs + r0 - 3 .. cs + r0 + NR - 4 (NR = the rows x holds) at element column `col`, 4 channels. Uniform row
+// bases and 32-bit lane offsets when no row is a replay row or past the end; per-lane row pointers otherwise. Rows
+// past the end repeat the last row: they only feed conv outputs past the end, which are masked.
+template <typename T, int NR>
+__device__ __forceinline__ void fetch_rows(const GdnArgs& a, const RowSrc& src, int b, int cs, int r0, int col,
+                                           float (&x)[NR][4]) {
+  const int end = a.P + a.L;
+  const unsigned rowb = (unsigned)a.stride * sizeof(T);
+  if (cs - (kKC - 1) >= a.P && cs + kC <= end) {
+    const char* base = (const char*)a.in + ((size_t)b * a.L + (cs - (kKC - 1) - a.P)) * rowb;
+    const unsigned off = (unsigned)r0 * rowb + (unsigned)col * (unsigned)sizeof(T);
+#pragma unroll
+    for (int i = 0; i < NR; i++) load4(gp<T>(base + (size_t)i * rowb + off), x[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      const int r = cs + r0 - (kKC - 1) + i, rc = min(r, end - 1);
+      load4(row_of<T>(a, src, b, rc) + col, x[i]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Producer
+
+// One 16x16 tile of K K^T (-> A, fp32, in Tm) or Q K^T (-> decay-masked scores, f16) of the chunk in st; block row
+// ti, block column tj <= ti
+__device__ __forceinline__ void tile(Set& st, float* Tm, bool isq, int ti, int tj, int grp, int c16) {
+  const _Float16* ab = (isq ? st.Qs : st.Ks) + (16 * ti + c16) * kQP + 8 * grp;
+  const _Float16* bb = st.Ks + (16 * tj + c16) * kQP + 8 * grp;
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++)
+    acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
+  const int tp = 16 * tj + c16, t0 = 16 * ti + 4 * grp;
+  if (ti != tj) {
+    // below the diagonal blocks gc_t <= gc_16 <= gc_t', so e^(gc_t - gc_t') factors into two terms <= 1
+    const float cf = st.colf[tp];
+    if (!isq) {
+      const f4 bf = lds4(&st.brow[t0]);
+#pragma unroll
+      for (int e = 0; e < 4; e++) Tm[(t0 + e) * kMP + tp] = acc[e] * bf[e] * cf;
+    } else {
+      const f4 rf = lds4(&st.rowf[t0]);
+#pragma unroll
+      for (int e = 0; e < 4; e++) st.Att[(t0 + e) * kP + tp] = (_Float16)(acc[e] * rf[e] * cf);
+    }
+  } else {
+    const float gq = st.gc[tp];
+    const f4 gt = lds4(&st.gc[t0]), bt = lds4(&st.bt[t0]);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int t = t0 + e;
+      const float dec = __expf(fminf(gt[e] - gq, 0.0f));
+      if (!isq)
+        Tm[t * kMP + tp] = tp < t ? bt[e] * acc[e] * dec : 0.0f;
+      else
+        st.Att[t * kP + tp] = (_Float16)(tp <= t ? acc[e] * dec : 0.0f);
+    }
+  }
+}
+
+// The two diagonal blocks of T = (I + A)^-1 by forward substitution: lane group grp solves block grp % 2, lane c16
+// owning column c16. Right-looking: once entry r of the column is final, it is eliminated from the rows below, so each
+// step's updates are independent (column r of A read as broadcasts within the group). Groups 0 and 1 store their
+// block: T_bb in Tm, T diag(beta) and T diag(beta e^gc) in the f16 tiles.
+__device__ __forceinline__ void solve_diag(Set& st, float* Tm, int grp, int c16) {
+  const int base = 16 * (grp & 1);
+  float pc[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) pc[r] = r == c16 ? 1.0f : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 15; r++) {
+#pragma unroll
+    for (int r2 = r + 1; r2 < 16; r2++) pc[r2] = fmaf(-Tm[(base + r2) * kMP + base + r], pc[r], pc[r2]);
+  }
+  wave_sync();  // every lane has read A's block before it is overwritten
+  if (grp < 2) {
+    const float cb = st.bt[base + c16], cbw = cb * st.eg[base + c16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      Tm[(base + r) * kMP + base + c16] = pc[r];
+      st.Tb[(base + r) * kP + base + c16] = (_Float16)(pc[r] * cb);
+      st.Tw[(base + r) * kP + base + c16] = (_Float16)(pc[r] * cbw);
+    }
+  }
+}
+
+// The block below the diagonal: T_10 = -T_11 (A_10 T_00) on v_mfma_f32_16x16x4f32, D layout (rows 4 grp + e of the
+// block, column c16) used directly as the next product's B operand, the A operand read in the same K order
+__device__ __forceinline__ void solve_offdiag(Set& st, const float* Tm, int grp, int c16) {
+  f4 X = {0.0f, 0.0f, 0.0f, 0.0f}, Y = X;
+  const f4 av = lds4(&Tm[(16 + c16) * kMP + 4 * grp]);
+  f4 t0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) t0[e] = Tm[(4 * grp + e) * kMP + c16];
+#pragma unroll
+  for (int e = 0; e < 4; e++) X = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], t0[e], X, 0, 0, 0);
+  const f4 tv = lds4(&Tm[(16 + c16) * kMP + 16 + 4 * grp]);
+#pragma unroll
+  for (int e = 0; e < 4; e++) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(tv[e], X[e], Y, 0, 0, 0);
+  const float fb = st.bt[c16], fw = fb * st.eg[c16];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int t = 16 + 4 * grp + e;
+    st.Tb[t * kP + c16] = (_Float16)(-Y[e] * fb);
+    st.Tw[t * kP + c16] = (_Float16)(-Y[e] * fw);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, ProducerLds& sm, char* ring, unsigned* produced,
+                                        const unsigned* consumed, unsigned ep) {
+  const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  const int end = a.P + a.L;
+  const int n = (end - a.s0 + kC - 1) / kC;
+  const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
+  const unsigned rowb = (unsigned)a.stride * sizeof(T);
+  const char* const seq_in = (const char*)a.in + (size_t)b * a.L * rowb;
+
+  for (int i = tid0; i < 2 * 128 * kKC; i += kThreads) {
+    const int lc = i / kKC, j = i % kKC;
+    const int ch = lc < 128 ? h * kDK + lc : a.H * kDK + h * kDK + (lc - 128);
+    sm.cwq[lc & 3][lc >> 2][j] = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
+  }
+  // the block above the diagonal of every set's f16 T and score tiles is read by full K blocks and never written
+  for (int idx = tid0; idx < 3 * 16 * 16; idx += kThreads) {
+    const int st = idx >> 8, t = (idx >> 4) & 15, tp = 16 + (idx & 15);
+    sm.s[st].s.Tb[t * kP + tp] = (_Float16)0.0f;
+    sm.s[st].s.Tw[t * kP + tp] = (_Float16)0.0f;
+    sm.s[st].s.Att[t * kP + tp] = (_Float16)0.0f;
+  }
+  const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
+  const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
+  const RowSrc src = row_src(a);
+  const int last_cs = a.s0 + kC * (n - 1);
+
+  // conv waves 4..7: wave cw -> rows 8 cw .. 8 cw + 7 of a chunk; lane l -> channels 4 (l % 32) .. + 3 of q (l < 32)
+  // or k (l >= 32). Wave 3's lanes 0..31 hold rows 0..31's a/b inputs for the gates. Both are loaded a period ahead,
+  // every period (on clamped rows past the end): conditional loads would make the loop-carried registers a merge of
+  // old and new values, which the compiler resolves with copies that wait for the loads right after they are issued.
+  const bool conv = w >= 4;
+  const int cw = w - 4;
+  float xq[kKC + 7][4], ga = 0.0f, gb = 0.0f;
+  auto fetch_qk = [&](int cs) {
+    const int l = opaque(tid0) & 63;
+    fetch_rows<T>(a, src, b, min(cs, last_cs), 8 * cw, (l < 32 ? 0 : a.H * kDK) + h * kDK + 4 * (l & 31), xq);
+  };
+  auto fetch_ab = [&](int cs) {
+    const int lane = opaque(tid0) & 31;
+    cs = min(cs, last_cs);
+    // rows past the end: their gates are never used (the gate lanes mask them)
+    const gptr<T> grow = cs >= a.P && cs + kC <= end ? gp<T>(seq_in + (size_t)(cs - a.P + lane) * rowb)
+                                                     : row_of<T>(a, src, b, min(cs + lane, end - 1));
+    ga = (float)grow[aoff];
+    gb = (float)grow[boff];
+  };
+  if (conv) fetch_qk(a.s0);
+  if (w == 3) fetch_ab(a.s0);
+  unsigned seen = 0;  // the consumer's progress as last read (copy waves)
+  __syncthreads();  // conv taps and zero blocks visible
+
+  // Period q: wave 0 runs chunk q's T chain (set q % 3); waves 1..3 copy chunk q - 1's finished set (q - 1) % 3 into
+  // its ring slot, waves 1 and 2 also make chunk q's score tiles, wave 3 the gates of chunk q + 1; the conv waves
+  // write chunk q + 1 into set (q + 1) % 3. One barrier per period. The copy's stores are left to complete during
+  // the next period (the copy waves wait for them before issuing the next copy), so chunk q - 2 is published after
+  // period q's barrier.
+  for (int q = -1; q <= n + 1; q++) {
+    const int c1 = a.s0 + kC * (q + 1);  // chunk q + 1
+    const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
+    if (conv) {
+      if (q + 1 < n) {
+        const int isk = lane >> 5, l32 = lane & 31, m = min(kC, end - c1);
+        float uq[8][4], ss[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++) ss[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const f4 wc = lds4(sm.cwq[c][lane]);
+#pragma unroll
+          for (int r = 0; r < 8; r++) {
+            float sv = wc[0] * xq[r][c];
+            sv = fmaf(wc[1], xq[r + 1][c], sv);
+            sv = fmaf(wc[2], xq[r + 2][c], sv);
+            sv = fmaf(wc[3], xq[r + 3][c], sv);
+            uq[r][c] = 8 * cw + r < m ? silu(sv) : 0.0f;
+            ss[r] = fmaf(uq[r][c], uq[r][c], ss[r]);
+          }
+        }
+        fetch_qk(c1 + kC);
+        Set& st = sm.s[(q + 1) % 3].s;
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+          const float rs = rsqrtf(sum32(ss[r]) + 1e-6f) * (isk ? 1.0f : qscale);
+#pragma unroll
+          for (int c = 0; c < 4; c++) uq[r][c] *= rs;
+          const h4 hv = {(_Float16)uq[r][0], (_Float16)uq[r][1], (_Float16)uq[r][2], (_Float16)uq[r][3]};
+          *reinterpret_cast<h4*>((isk ? st.Ks : st.Qs) + (8 * cw + r) * kQP + 4 * l32) = hv;
+        }
+        if (isk) {
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            h8 kt;
+#pragma unroll
+            for (int r = 0; r < 8; r++) kt[r] = (_Float16)uq[r][c];
+            *reinterpret_cast<h8*>(st.KT + kt32(4 * l32 + c, cw)) = kt;
+          }
+        }
+      } else {
+        fetch_qk(c1 + kC);
+      }
+    } else {
+      if (w == 0) {
+        if (q >= 0 && q < n) {
+          Set& st = sm.s[q % 3].s;
+          tile(st, sm.Tm, false, 0, 0, grp, c16);
+          tile(st, sm.Tm, false, 1, 1, grp, c16);
+          tile(st, sm.Tm, false, 1, 0, grp, c16);
+          wave_sync();
+          solve_diag(st, sm.Tm, grp, c16);
+          wave_sync();
+          solve_offdiag(st, sm.Tm, grp, c16);
+        }
+      } else {
+        if (q >= 0 && q < n) {
+          Set& st = sm.s[q % 3].s;
+          if (w == 1) {
+            tile(st, sm.Tm, true, 0, 0, grp, c16);
+            tile(st, sm.Tm, true, 1, 0, grp, c16);
+          } else if (w == 2) {
+            tile(st, sm.Tm, true, 1, 1, grp, c16);
+          }
+        }
+        if (w == 3 && q + 1 < n) {
+          // beta and the cumulative log decay of row `lane` (lanes 0..31) of chunk q + 1
+          const int gl = lane & 31, m = min(kC, end - c1);
+          float gcr = 0.0f, btr = 0.0f;
+          if (lane < 32 && gl < m) {
+            btr = __builtin_amdgcn_rcpf(1.0f + __expf(-gb));
+            const float xs = ga + db;
+            gcr = na * (xs > 20.0f ? xs : log1pf(__expf(xs)));
+          }
+#pragma unroll
+          for (int d = 1; d < 32; d <<= 1) {
+            const float o = __shfl_up(gcr, d);
+            if (gl >= d) gcr += o;
+          }
+          const float glast = __shfl(gcr, 31), g16 = __shfl(gcr, 16);
+          const float rf = __expf(gcr - __shfl(gcr, lane & 16));
+          Set& st = sm.s[(q + 1) % 3].s;
+          if (lane < 32) {
+            st.gc[lane] = gcr;
+            st.eg[lane] = __expf(gcr);
+            st.bt[lane] = btr;
+            st.ed[lane] = __expf(glast - gcr);
+            st.rowf[lane] = rf;
+            st.brow[lane] = btr * rf;
+            st.colf[lane] = lane < 16 ? __expf(g16 - gcr) : 0.0f;
+          }
+        }
+        // the previous period's ring stores have reached the device-coherent level (they had a period to get there)
+        __builtin_amdgcn_s_waitcnt(0);
+        // chunk q - 1's set into slot (q - 1) % kDuoRing, once the consumer has taken chunk q - 1 - kDuoRing out of it
+        if (q >= 1 && q <= n) {
+          const int c = q - 1;
+          if (c >= kDuoRing && seen < ep + (unsigned)(c - kDuoRing + 1))
+            seen = wait_counter(consumed, ep + (unsigned)(c - kDuoRing + 1));
+          const __amdgpu_buffer_rsrc_t rs =
+              __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)(c % kDuoRing) * kDuoSetBytes, 0, kDuoSetBytes, 0x00020000);
+          const unsigned char* from = sm.s[c % 3].raw;
+          for (int i = tid - 64; i < kDuoSetBytes / 16; i += 192) {
+            const f4 v = lds4(reinterpret_cast<const float*>(from + 16 * i));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), rs, 16 * i, 0, 16);
+          }
+        }
+        if (w == 3) fetch_ab(c1 + kC);  // after the drain above, which would otherwise wait for these loads too
+      }
+    }
+    __syncthreads();
+    if (tid0 == 64 && q >= 2) st_counter(produced, ep + (unsigned)(q - 1));  // chunks 0 .. q - 2 are in the ring
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Consumer
+
+template <typename T>
+__device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, ConsumerLds& sm, const char* ring,
+                                        const unsigned* produced, unsigned* consumed, unsigned ep) {
+  const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  const int end = a.P + a.L;
+  const int n = (end - a.s0 + kC - 1) / kC;
+  const int s1 = a.s0 + 64 * ((end - a.s0) / 64);  // the stored state position
+  const unsigned orowb = (unsigned)(a.H * kDV) * sizeof(T);
+  const char* const seq_in = (const char*)a.in + (size_t)b * a.L * ((unsigned)a.stride * sizeof(T));
+  const size_t sbase = ((size_t)b * a.H + h) * kDK * kDV;
+  const bool state = w < 4;
+  const int hw = w - 4;  // helper wave
+  const int last_cs = a.s0 + kC * (n - 1);
+
+  for (int i = tid0; i < 128 * kKC; i += kThreads) {
+    const int lc = i / kKC, j = i % kKC;
+    sm.cwv[lc & 3][lc >> 2][j] = gp<float>(a.conv_w)[(size_t)(2 * a.H * kDK + h * kDV + lc) * kKC + j];
+  }
+
+  // Helper lanes: v conv of rows 4 vrg .. + 3, channels 4 cvg .. + 3; gated norm of row fr, columns fc .. fc + 15.
+  // They hold the raw v rows and the z rows of the chunks they work on next, loaded a period ahead (every period, on
+  // clamped rows past the end, so that the registers are never a merge of old and new loads) into second buffers.
+  const int ht0 = tid0 - 256;
+  const RowSrc src = row_src(a);
+  float xv[kKC + 3][4], xn[kKC + 3][4];
+  f4 zq[4], zn[4], gw[4] = {};
+  if (!state && a.gnorm)
+#pragma unroll
+    for (int q = 0; q < 4; q++) gw[q] = ld4(gp<float>(a.gnorm) + 16 * (ht0 & 7) + 4 * q);
+  unsigned seen = 0;  // the producer's progress as last read (helper waves); a read is issued every period, ahead of use
+  auto fetch_v = [&](int cs) {
+    const int ht = opaque(tid0) - 256, vrg = ht >> 5, cvg = ht & 31;
+    fetch_rows<T>(a, src, b, min(cs, last_cs), 4 * vrg, 2 * a.H * kDK + h * kDV + 4 * cvg, xn);
+  };
+  auto vconv = [&](int cs) {
+    const int ht = opaque(tid0) - 256, vrg = ht >> 5, cvg = ht & 31;
+    const int mv = min(kC, end - cs);
+    _Float16* VT = sm.VT[((cs - a.s0) / kC) & 1];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const f4 wc = lds4(sm.cwv[c][cvg]);
+      h4 vt;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float sv = wc[0] * xv[r][c];
+        sv = fmaf(wc[1], xv[r + 1][c], sv);
+        sv = fmaf(wc[2], xv[r + 2][c], sv);
+        sv = fmaf(wc[3], xv[r + 3][c], sv);
+        vt[r] = (_Float16)(4 * vrg + r < mv ? silu(sv) : 0.0f);
+      }
+      *reinterpret_cast<h4*>(VT + (4 * cvg + c) * kP + 4 * vrg) = vt;
+    }
+  };
+  auto fetch_z = [&](int c0) {
+    const int ht = opaque(tid0) - 256, fr = ht >> 3, fc = 16 * (ht & 7);
+    const int rr = min(max(min(c0, last_cs) + fr - a.P, 0), a.L - 1);
+    const gptr<T> zr = gp<T>(seq_in) + (size_t)rr * a.stride + a.C + h * kDV + fc;
+#pragma unroll
+    for (int q = 0; q < 4; q++) zn[q] = ld4(zr + 4 * q);
+  };
+  // chunk c's tile set from its ring slot into LDS: whole 1 KiB DMA instructions, helper wave wq issues every fourth
+  auto dma_set = [&](int c, int wq) {
+    if (seen < ep + (unsigned)(c + 1)) seen = max(seen, wait_counter(produced, ep + (unsigned)(c + 1)));
+    const char* from = ring + (size_t)(c % kDuoRing) * kDuoSetBytes;
+    unsigned char* to = sm.s[c & 1].raw;
+    const int ln = opaque(tid0) & 63;
+    for (int i = wq; i < kDuoSetBytes / 1024; i += 4)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(from + 1024 * (size_t)i + 16 * ln),
+                                       (__attribute__((address_space(3))) void*)(to + 1024 * i), 16, 0, 16);
+  };
+  f4 S[2][8];  // state waves: S[ct][it][e] = S[16 it + 4 grp + e][32 w + 16 ct + c16]
+  if (state) {
+    const int g0 = (tid0 & 63) >> 4, l16 = tid0 & 15;
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+      for (int it = 0; it < 8; it++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          S[ct][it][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16]
+                                : 0.0f;
+  } else {
+    fetch_v(a.s0);
+    dma_set(0, hw);
+    __syncthreads();  // v conv taps visible (the state waves pass this barrier below)
+#pragma unroll
+    for (int r = 0; r < kKC + 3; r++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
+    vconv(a.s0);
+    fetch_v(a.s0 + kC);
+    if (a.gnorm) fetch_z(a.s0);
+  }
+  // Drain the prologue's loads: the compiler's wait counting merges the loop's entry state into every period, so a load
+  // still outstanding at the loop head would make each period's first use of its registers wait for every global access
+  // issued before it.
+  __builtin_amdgcn_s_waitcnt(0);
+  if (state) __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; q++) zq[q] = zn[q];
+#pragma unroll
+  for (int r = 0; r < kKC + 3; r++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
+  __syncthreads();
+  if (tid0 == 256) st_counter(consumed, ep + 1u);
+
+  // Period p: the state waves run chunk p (its rows into osg[p % 2]); the helpers bring chunk p + 1's tile set, normalise
+  // and store chunk p - 1, run chunk p + 1's v conv and load the next rows. One barrier per period.
+  auto period = [&](int p) __attribute__((always_inline)) {
+    const int c0 = a.s0 + kC * p;  // chunk p
+    const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
+    if (state) {
+      if (p < n) {
+        const int m = min(kC, end - c0);
+        Set& st = sm.s[p & 1].s;
+        const _Float16* VT = sm.VT[p & 1];
+        float* osg = sm.osg[p & 1];
+        // k^ S and q^ S together, K block outermost (one f16 copy of that block of S at a time)
+        f4 KS[2][2], O[2][2], Vn[2][2];
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+          h8 S16[2];
+#pragma unroll
+          for (int ct = 0; ct < 2; ct++) S16[ct] = pack_b(S[ct][2 * kb], S[ct][2 * kb + 1]);
+#pragma unroll
+          for (int ti = 0; ti < 2; ti++) {
+            const h8 ka = perm_a(st.Ks, kQP, 16 * ti + c16, kb, grp);
+            const h8 qa = perm_a(st.Qs, kQP, 16 * ti + c16, kb, grp);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+              const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+              KS[ct][ti] = mfma16(ka, S16[ct], kb ? KS[ct][ti] : z4);
+              O[ct][ti] = mfma16(qa, S16[ct], kb ? O[ct][ti] : z4);
+            }
+          }
+        }
+        // V_new = T diag(beta) v - T diag(beta e^gc) (k^ S)
+        {
+          h8 KSb[2];
+#pragma unroll
+          for (int ct = 0; ct < 2; ct++) KSb[ct] = pack_b(KS[ct][0], KS[ct][1]);
+#pragma unroll
+          for (int ti = 0; ti < 2; ti++) {
+            const h8 tb = *reinterpret_cast<const h8*>(st.Tb + (16 * ti + c16) * kP + 8 * grp);
+            const h8 tw = perm_a(st.Tw, kP, 16 * ti + c16, 0, grp);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+              const int col = 32 * w + 16 * ct + c16;
+              const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+              const f4 u = mfma16(tb, *reinterpret_cast<const h8*>(VT + col * kP + 8 * grp), z4);
+              const f4 ws = mfma16(tw, KSb[ct], z4);
+              Vn[ct][ti] = u - ws;
+            }
+          }
+        }
+        // o = e^gc (q^ S) + scores V_new
+        {
+          h8 Vb[2];
+#pragma unroll
+          for (int ct = 0; ct < 2; ct++) Vb[ct] = pack_b(Vn[ct][0], Vn[ct][1]);
+#pragma unroll
+          for (int ti = 0; ti < 2; ti++) {
+            const f4 eg = lds4(&st.eg[16 * ti + 4 * grp]);
+            const h8 at = perm_a(st.Att, kP, 16 * ti + c16, 0, grp);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) O[ct][ti] = mfma16(at, Vb[ct], O[ct][ti] * eg);
+          }
+        }
+        if (m == kC) {
+          // rows of V_new scaled by e^(gc_31 - gc_t), then S <- e^gc_31 S + k^T (scaled V_new)
+          h8 Vd[2];
+#pragma unroll
+          for (int ti = 0; ti < 2; ti++) {
+            const f4 ed = lds4(&st.ed[16 * ti + 4 * grp]);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) Vn[ct][ti] *= ed;
+          }
+#pragma unroll
+          for (int ct = 0; ct < 2; ct++) Vd[ct] = pack_b(Vn[ct][0], Vn[ct][1]);
+          const float el = st.eg[kC - 1];
+#pragma unroll
+          for (int it = 0; it < 8; it++) {
+            const h8 k = perm_a_kt32(st.KT, 16 * it + c16, grp);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) S[ct][it] = mfma16(k, Vd[ct], S[ct][it] * el);
+          }
+        }
+        // O (D layout) -> the output rows; this wave's gated-norm partial sums over its 32 columns
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+          for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) osg[(16 * ti + 4 * grp + e) * kOP + 32 * w + 16 * ct + c16] = O[ct][ti][e];
+        if (a.gnorm) {
+          wave_sync();
+          const int er = lane >> 3, ec = 32 * w + 4 * (lane & 7);
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const f4 y = lds4(&osg[(8 * q + er) * kOP + ec]);
+            const float sq = sum8((y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]));
+            if ((lane & 7) == 0) sm.red[p & 1][(8 * q + er) * 4 + w] = sq;
+          }
+        }
+      }
+    } else {
+      // the tile set's DMA first, so that it lands behind this period's work; then the small loads (vector memory
+      // instructions issue in order, so these queue behind the DMA but are not waited for until the period's end)
+      if (p + 1 < n) dma_set(p + 1, hw);
+      fetch_v(c0 + 2 * kC);
+      if (a.gnorm) fetch_z(c0);
+      const unsigned ahead = ld_counter(produced);  // for the next period's check
+      if (p >= 1) {
+        // chunk p - 1's gated norm and store
+        const int cp = c0 - kC, mp = min(kC, end - cp), fr = ht0 >> 3, fc = 16 * (ht0 & 7);
+        const float* osg = sm.osg[(p - 1) & 1];
+        f4 y[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) y[q] = lds4(&osg[fr * kOP + fc + 4 * q]);
+        if (a.gnorm) {
+          const f4 r = lds4(&sm.red[(p - 1) & 1][fr * 4]);
+          const float iv = rsqrtf(((r[0] + r[1]) + (r[2] + r[3])) / kDV + 1e-6f);
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) y[q][c] = y[q][c] * iv * (gw[q][c] * silu(zq[q][c]));
+        }
+        if (fr < mp && cp + fr >= a.P) {
+          __attribute__((address_space(1))) T* orow =
+              gpw<T>((char*)a.out + ((size_t)b * a.L + (cp + fr - a.P)) * (size_t)orowb) + (size_t)h * kDV + fc;
+#pragma unroll
+          for (int q = 0; q < 4; q++) store4(orow + 4 * q, y[q]);
+        }
+      }
+      if (p + 1 < n) vconv(c0 + kC);
+      __builtin_amdgcn_s_waitcnt(0);  // chunk p + 1's tile set has landed in LDS; the next rows are in registers
+      seen = max(seen, ahead);
+#pragma unroll
+      for (int r = 0; r < kKC + 3; r++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
+#pragma unroll
+      for (int q = 0; q < 4; q++) zq[q] = zn[q];
+    }
+    __syncthreads();
+    if (tid0 == 256 && p + 1 < n) st_counter(consumed, ep + (unsigned)(p + 2));
+  };
+
+  // the stored state is the one at s1: the periods before chunk (s1 - s0) / 32 advance it up to there, it is written
+  // out, and the rest of the call continues from it (a separate loop, so the store is not inside the periods); one
+  // period past the last chunk stores its output
+  const int k1 = (s1 - a.s0) / kC;
+  int p = 0;
+  for (; p < k1; p++) period(p);
+  if (state) {
+    const int g0 = (tid0 & 63) >> 4, l16 = tid0 & 15;
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+      for (int it = 0; it < 8; it++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16] = S[ct][it][e];
+  }
+  for (; p <= n; p++) period(p);
+}
+
+// Blocks 16 i + r (r < 8) and 16 i + 8 + r form pair 8 i + r: the dispatcher hands consecutive blocks to the XCDs in
+// turn, so both members of a pair share an XCD and its L2.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gdn_duo_kernel(GdnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  const int blk = blockIdx.x;
+  const int pair = (blk >> 4) * 8 + (blk & 7);
+  const int b = pair / a.H, h = pair % a.H;
+  unsigned* const produced = a.duo_flags + (size_t)pair * 64;  // each counter on its own 128-byte line
+  unsigned* const consumed = produced + 32;
+  char* const ring = (char*)a.duo_ring + (size_t)pair * kDuoRing * kDuoSetBytes;
+  const unsigned ep = a.duo_epoch * 256u;
+  if ((blk >> 3) & 1)
+    produce<T>(a, b, h, *reinterpret_cast<ProducerLds*>(lds_raw), ring, produced, consumed, ep);
+  else
+    consume<T>(a, b, h, *reinterpret_cast<ConsumerLds*>(lds_raw), ring, produced, consumed, ep);
+}
+
+template <typename T>
+hipError_t launch(const GdnArgs& a, hipStream_t s) {
+  auto k = gdn_duo_kernel<T>;
+  const int lds = (int)(sizeof(ConsumerLds) > sizeof(ProducerLds) ? sizeof(ConsumerLds) : sizeof(ProducerLds));
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e != hipSuccess) return e;
+  GdnArgs arg = a;
+  void* params[] = {&arg};
+  return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k), dim3(2 * a.B * a.H), dim3(kThreads), params,
+                                    (unsigned)lds, s);
+}
+
+}  // namespace
+
+bool gdn_duo_fits(int B, int H) { return (B * H) % 8 == 0 && 2 * B * H <= 256; }
+
+hipError_t launch_gdn_duo(const GdnArgs& a, hipStream_t s) {
+  if (a.DK != kDK || a.DV != kDV || a.KC != kKC) return hipErrorInvalidValue;
+  if (a.P - a.s0 >= 64 || a.P < a.s0) return hipErrorInvalidValue;  // at most one open 64-row span is replayed
+  if (!gdn_duo_fits(a.B, a.H) || !a.duo_ring || !a.duo_flags) return hipErrorInvalidValue;
+  return a.dtype == 0 ? launch<float>(a, s) : launch<_Float16>(a, s);
+}
+
+}  // namespace ha

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(HERE, "libha.so")
 HA_OK, HA_ERR_ARG, HA_ERR_CONTEXT, HA_ERR_HANDLE, HA_ERR_DEVICE, HA_ERR_NOMEM, HA_ERR_PARAM = 0, -1, -2, -3, -4, -5, -6
 LINEAR, FULL, ADAPTER = 0, 1, 2  # ADAPTER: no token mixer (engine.js:256-261); its forward buffers may be None
 F32, F16 = 0, 1
-CHUNKED, SEQUENTIAL, CHUNKED_FUSED, CHUNKED_SPLIT = 0, 1, 2, 3
+CHUNKED, SEQUENTIAL, CHUNKED_FUSED, CHUNKED_SPLIT, CHUNKED_PAIRED = 0, 1, 2, 3, 4
 KIND_NAMES = {"linear_attention": LINEAR, "full_attention": FULL, "adapter": ADAPTER}
 
 

@@ -19,10 +19,11 @@ const native = require(path.join(__dirname, 'ha_napi.node'));
 
 const F32 = 0;
 const F16 = 1;
-const CHUNKED = 0;  // the engine picks CHUNKED_SPLIT or CHUNKED_FUSED from the batch shape
+const CHUNKED = 0;  // the engine picks CHUNKED_SPLIT, CHUNKED_PAIRED or CHUNKED_FUSED from the batch shape
 const SEQUENTIAL = 1;
 const CHUNKED_FUSED = 2;
 const CHUNKED_SPLIT = 3;
+const CHUNKED_PAIRED = 4;
 // adapter: a projection stand-in with no token mixer (engine.js:256-261); its forward buffers may be null
 const LAYER_KIND = { linear_attention: 0, full_attention: 1, adapter: 2 };
 
@@ -183,7 +184,7 @@ class Engine {
    * One forward over L new rows of every sequence (engine.js:313). inputs / outputs: one device buffer per layer.
    * options: {cache: Snapshot to resume from, keepCache: return a snapshot of the context after this call,
    *           timestamps: report gpu_ms, layerMs: per-layer GPU ms,
-   *           recurrence: CHUNKED | SEQUENTIAL | CHUNKED_FUSED | CHUNKED_SPLIT}
+   *           recurrence: CHUNKED | SEQUENTIAL | CHUNKED_FUSED | CHUNKED_SPLIT | CHUNKED_PAIRED}
    * Throws (as the reference does at engine.js:316) when the cached plus new rows exceed maxCtx.
    */
   forward(L, inputs, outputs, options) {
@@ -504,5 +505,6 @@ module.exports = {
   SEQUENTIAL: SEQUENTIAL,
   CHUNKED_FUSED: CHUNKED_FUSED,
   CHUNKED_SPLIT: CHUNKED_SPLIT,
+  CHUNKED_PAIRED: CHUNKED_PAIRED,
   abiVersion: native.abiVersion,
 };

@@ -2,7 +2,7 @@
 // Drives the Node host API (strands-decider-web_amd/js/engine.js) the way the reference's callers drive
 // Engine.forward: a prefix forward that keeps its cache, then a suffix forward resumed from that snapshot, then
 // release(). Inputs and outputs are raw little-endian files in a directory named by the first argument:
-//   spec.json {kinds, batch, maxCtx, T0, T1, params: [{name: file}...]}
+//   spec.json {kinds, batch, maxCtx, T0, T1, params: [{name: file}...], recurrence (optional)}
 //   in_<layer>_<part>.bin  rows in the layer kind's dtype; out_<layer>_<part>.bin written back the same way
 //   state_<layer>.bin      snapshot state of linear layers after the prefix
 const fs = require('fs');
@@ -40,7 +40,8 @@ function run(part, L, cache, keep) {
     outs.push(engine.alloc(spec.batch * L * (lin ? c.H * c.DV : c.HQ * c.HD) * e));
     esz.push(e);
   });
-  const r = engine.forward(L, ins, outs, { cache: cache, keepCache: keep, timestamps: true });
+  const r = engine.forward(L, ins, outs, { cache: cache, keepCache: keep, timestamps: true,
+    recurrence: spec.recurrence === undefined ? ha.CHUNKED : spec.recurrence });
   outs.forEach(function (o, i) {
     const host = esz[i] === 4 ? new Float32Array(o.bytes / 4) : new Uint16Array(o.bytes / 2);
     o.download(host);

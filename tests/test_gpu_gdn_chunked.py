@@ -13,7 +13,7 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3  # north-star bar for the recurrence (max |err| / max |ref|)
 
 
-@pytest.fixture(params=[ha.CHUNKED_FUSED, ha.CHUNKED_SPLIT], ids=["fused", "split"])
+@pytest.fixture(params=[ha.CHUNKED_FUSED, ha.CHUNKED_SPLIT, ha.CHUNKED_PAIRED], ids=["fused", "split", "paired"])
 def mode(request):
     return request.param
 

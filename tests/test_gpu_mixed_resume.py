@@ -18,7 +18,9 @@ pytestmark = pytest.mark.gpu
     (ha.CHUNKED_SPLIT, ha.SEQUENTIAL, 64 * 3 + 5, 1),
     (ha.SEQUENTIAL, ha.CHUNKED, 100, 150),
     (ha.SEQUENTIAL, ha.CHUNKED_FUSED, 37, 64),
-    (ha.SEQUENTIAL, ha.CHUNKED_SPLIT, 129, 70)])
+    (ha.SEQUENTIAL, ha.CHUNKED_SPLIT, 129, 70),
+    (ha.CHUNKED_PAIRED, ha.SEQUENTIAL, 64 * 2 + 33, 9),
+    (ha.SEQUENTIAL, ha.CHUNKED_PAIRED, 71, 100)])
 def test_mixed_mode_resume(first, second, P, L):
     print("mixed resume: mode %d for %d rows, then mode %d for %d rows" % (first, P, second, L), flush=True)
     r = Runner(["linear_attention"], batch=2)

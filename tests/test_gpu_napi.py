@@ -11,6 +11,7 @@ import sys
 import numpy as np
 import pytest
 
+import hybrid_attention as ha
 import synth
 from harness import Runner, oracle_gdn, oracle_gqa, rel_err
 
@@ -33,7 +34,11 @@ def _params():
 def test_node_forward_resume_release(tmp_path):
     d = str(tmp_path)
     params = _params()
-    spec = {"kinds": KINDS, "batch": B, "maxCtx": 4096, "T0": T0, "T1": T1, "params": []}
+    # one form in both hosts: the default for B * H = 32 (the paired form) needs a cooperative launch, which the device
+    # refuses to the Node child while this process, which has made such launches, is alive (the engine then falls back
+    # to the fused kernel; tests/test_gpu_paired_fallback.py covers that)
+    rec = ha.CHUNKED_FUSED
+    spec = {"kinds": KINDS, "batch": B, "maxCtx": 4096, "T0": T0, "T1": T1, "params": [], "recurrence": rec}
     for i, p in enumerate(params):
         names = {}
         for k, v in p.items():
@@ -60,8 +65,8 @@ def test_node_forward_resume_release(tmp_path):
     run = Runner(KINDS, batch=B)
     for i, p in enumerate(params):
         run.set_params(i, p)
-    out0, snap = run.forward(ins[0], keep=True)
-    out1, _ = run.forward(ins[1], cache=snap)
+    out0, snap = run.forward(ins[0], keep=True, recurrence=rec)
+    out1, _ = run.forward(ins[1], cache=snap, recurrence=rec)
     for i in range(2):
         assert np.array_equal(js_out(i, 0, T0), out0[i]), "prefix layer %d differs from the C ABI run" % i
         assert np.array_equal(js_out(i, 1, T1), out1[i]), "suffix layer %d differs from the C ABI run" % i

@@ -70,7 +70,7 @@ def test_config4_stack(T):
     e2 = _engine(sub, 2, 2048)
     ins2 = [ins[i][pick].contiguous() for i in range(5)]
     outs2 = [torch.full_like(outs[i][pick], float("nan")) for i in range(5)]
-    rec = ha.CHUNKED_FUSED  # the form HA_CHUNKED picks for 8 x 16 sequence-heads
+    rec = ha.CHUNKED_PAIRED  # the form HA_CHUNKED picks for 8 x 16 sequence-heads
     torch.cuda.synchronize()
     e2.forward(T, ins2, outs2, recurrence=rec, sync=True)
     torch.cuda.synchronize()
