@@ -44,8 +44,8 @@ def gqa_flops(T, P=0):
 
 
 COPY_BYTES = 512 << 20
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gdn_chunk_B8_T2048_hbm_traffic.md")
-GDN_SOURCE = os.path.join(ROOT, "strands-decider-web_amd", "csrc", "gdn_chunk.hip")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gdn_duo_B8_T2048_hbm_traffic.md")
+GDN_SOURCE = os.path.join(ROOT, "strands-decider-web_amd", "csrc", "gdn_duo.hip")
 
 
 def measured_traffic():
@@ -528,9 +528,10 @@ def main():
                 "kind's layers), conv taps ~N(0,0.5^2), unit q/k norm gain",
         "config": {"workload": "24-layer hybrid stack (18 gated-delta + 6 GQA, 3:1), "
                                "B=8 sequences, T=2048, projections excluded",
-                   "batch": B, "seq_len": T, "layers": len(KINDS), "gdn_recurrence": "chunked (64)"},
+                   "batch": B, "seq_len": T, "layers": len(KINDS),
+                   "gdn_recurrence": "chunked, paired form (32-row chunks, 2 workgroups per sequence-head)"},
         "per_kind_ms": {"gated_delta_18": round(gdn_ms, 4), "gqa_6": round(gqa_ms, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gdn_chunk_kernel (+ its 3-row tail copy)",
+        "roofline": {"bound": "hbm", "kernel": "gdn_duo_kernel (+ its 3-row tail copy)",
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": gdn_bytes, "bytes_per_token": gdn_bytes_per_token(),
