@@ -1,4 +1,4 @@
-// Chunked gated-delta prefill on two CUs per (sequence, head) (ha_recurrence HA_CHUNKED for 32 < B*H <= 128,
+// Chunked gated-delta prefill on two CUs per (sequence, head) (ha_recurrence HA_CHUNKED for 16 < B*H <= 128,
 // HA_CHUNKED_PAIRED), gfx950.
 //
 // Same semantics as the sequential rule (reference web/public/engine/wgsl.js:124-187 + 252-268), evaluated in the
