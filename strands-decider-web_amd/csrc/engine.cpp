@@ -126,7 +126,7 @@ struct ha_engine {
   std::shared_ptr<Scratch> scratch;
   size_t need_zeros = 0, need_img = 0, need_seq_raw = 0, need_seq_cnt = 0, need_gqa = 0, need_duo_ring = 0,
          need_duo_flags = 0;
-  int img_chunks = 0;
+  int img_chunks = 0, duo_slots = 0;
   int gqa_split = 0, gqa_part_slots = 0;
   hipEvent_t ev[2] = {nullptr, nullptr};
   std::vector<hipEvent_t> lev;
@@ -345,8 +345,10 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
     e->need_img = ha::gdn_split_image_bytes() * B * c.H * e->img_chunks;
     e->need_seq_raw = sizeof(float) * B * c.H * ha::kSegRows * c.DV;
     e->need_seq_cnt = sizeof(unsigned) * B * c.H;
-    // the paired form's tile-set ring and progress counters, likewise only where HA_CHUNKED picks that form
-    e->need_duo_ring = (size_t)ha::kDuoRing * ha::kDuoSetBytes * B * c.H;
+    // the paired form's tile sets (a slot for every 32-row chunk a call can have) and progress counters, likewise
+    // only where HA_CHUNKED picks that form
+    e->duo_slots = (c.max_ctx + 31) / 32;
+    e->need_duo_ring = (size_t)e->duo_slots * ha::kDuoSetBytes * B * c.H;
     e->need_duo_flags = sizeof(unsigned) * 64 * B * c.H;
     if ((rc = grow(e->scratch->zeros, e->need_zeros)) || (rc = grow(e->scratch->seq_raw, e->need_seq_raw)) ||
         (rc = grow(e->scratch->seq_cnt, e->need_seq_cnt)) ||
@@ -542,22 +544,15 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       } else if (split) {
         he = ha::launch_gdn_split(a, st);
       } else if (paired) {
-        // a fresh counter epoch per launch; before the epoch field (24 bits) runs out, the counters are cleared
-        if (sc.duo_epoch + 1 >= (1u << 24)) {
+        // a fresh counter epoch per launch; before the epoch field runs out, the counters are cleared
+        if (sc.duo_epoch + 1 >= (1u << (32 - ha::kDuoEpochShift))) {
           HA_HIP(hipStreamSynchronize(st));
           HA_HIP(hipMemset(sc.duo_flags.p, 0, sc.duo_flags.bytes));
           sc.duo_epoch = 0;
         }
-        a.duo_ring = sc.duo_ring.p; a.duo_flags = static_cast<unsigned*>(sc.duo_flags.p); a.duo_epoch = ++sc.duo_epoch;
+        a.duo_ring = sc.duo_ring.p; a.duo_slots = e->duo_slots;
+        a.duo_flags = static_cast<unsigned*>(sc.duo_flags.p); a.duo_epoch = ++sc.duo_epoch;
         he = ha::launch_gdn_duo(a, st);
-        // The device refuses a cooperative launch while another process holds its cooperative dispatch (it has made
-        // such launches and is still alive), or when the pairs do not fit the free CUs: the fused kernel runs instead.
-        // It rounds differently, so a resumed suffix matches one longer forward bit for bit only when both ran the
-        // same form.
-        if (he == hipErrorIllegalState || he == hipErrorCooperativeLaunchTooLarge) {
-          (void)hipGetLastError();
-          he = ha::launch_gdn_chunked(a, st);
-        }
       } else {
         he = ha::launch_gdn_chunked(a, st);
       }

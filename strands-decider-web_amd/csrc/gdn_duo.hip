@@ -11,20 +11,23 @@
 //   S  <- exp(gc_31) S + k^T diag(exp(gc_31 - gc)) V_new
 //
 // One CU's VALU and latency chains bound a one-workgroup form at a period of about 10K cycles per 32 rows, and at
-// B = 8 half the CUs have no head. So each (sequence, head) gets two workgroups, both resident (cooperative launch):
+// B = 8 half the CUs have no head. So each (sequence, head) gets two workgroups:
 //   producer: everything that does not depend on the state, chunk by chunk: q/k conv + SiLU + l2 norm, the gates, the
 //     A and score tiles, T = (I + A)^-1, T diag(beta) and T diag(beta e^gc). In one period wave 0 runs chunk q's T
 //     chain, waves 1..2 its score tiles, wave 3 chunk q + 1's gates, waves 4..7 chunk q + 1's q/k conv, and waves
-//     1..3 copy chunk q - 1's finished tile set (36 KiB) into a ring of 6 slots in device memory.
+//     1..3 copy chunk q - 1's finished tile set (36 KiB) into that chunk's slot in device memory.
 //   consumer: waves 0..3 own 32 value columns each of the fp32 state in MFMA accumulators and do the state work of
-//     chunk p; meanwhile waves 4..7 (helpers) DMA chunk p + 1's tile set from the ring into LDS, apply the gated
+//     chunk p; meanwhile waves 4..7 (helpers) DMA chunk p + 1's tile set from its slot into LDS, apply the gated
 //     RMSNorm to chunk p - 1's output and store it, and run chunk p + 1's v conv.
 // Each role passes one workgroup barrier per period.
-// The two exchange progress through counters: `produced` (tile sets in the ring) and `consumed` (sets copied into the
-// consumer's LDS, so their slots may be reused). Counter values carry a per-launch epoch (epoch * 256 + chunks), so
-// values left by earlier launches never satisfy a wait and nothing is cleared between launches. Data is written with
-// device-coherent (sc1) stores and waited for (vmcnt 0) before the counter store; readers load counters and data with
-// sc1. Every wait is bounded.
+// The two exchange progress through counters: `produced` (tile sets in their slots) and `consumed` (sets copied into
+// the consumer's LDS). Counter values carry a per-launch epoch (epoch << kDuoEpochShift | chunks), so values left by
+// earlier launches never satisfy a wait and nothing is cleared between launches. Data is written with device-coherent
+// (sc1) stores and waited for (vmcnt 0) before the counter store; readers load counters and data with sc1.
+// Ordinary launch, no co-residency guarantee: every chunk has its own slot, so the producer never needs the consumer
+// (it only holds back, for a bounded time, while it is more than kLead chunks ahead, which keeps the sets it writes
+// in the caches), and it is dispatched first (see the block mapping at the kernel). A consumer that is resident
+// therefore waits only for a producer that is resident or finished. Every wait is bounded.
 //
 // Chunk boundaries sit at s0 + 32k and the state advances over every complete chunk. The state written out is the
 // one at the end of the call's last complete 64-row span (the position the engine stores it at); a resumed call
@@ -43,6 +46,7 @@ constexpr int kP = kC + 8;      // row pitch (halves) of [*][32] f16 tiles
 constexpr int kMP = kC + 4;     // row pitch (floats) of the fp32 A / T tile
 constexpr int kThreads = 512;   // 8 waves per workgroup
 constexpr int kOP = kDV + 4;    // row pitch (floats) of the consumer's output rows
+constexpr int kLead = 6;        // chunks the producer may run ahead of the consumer before it holds back
 
 typedef int i4v __attribute__((ext_vector_type(4)));
 
@@ -108,12 +112,11 @@ __device__ __forceinline__ unsigned ld_counter(const unsigned* c) {
 __device__ __forceinline__ void st_counter(unsigned* c, unsigned v) {
   __hip_atomic_store(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Waits until the counter reaches v and returns the value read. Bounded (2^16 polls of about a microsecond; a partner
-// is normally a period or more ahead, a few microseconds): if the partner never gets there the caller goes on with
-// whatever the buffers hold, so the kernel still ends. Callers keep the value and poll again only when it falls short.
-__device__ __forceinline__ unsigned wait_counter(const unsigned* c, unsigned v) {
+// Waits until the counter reaches v and returns the value read, for at most `polls` polls of about a microsecond.
+// Callers keep the value and poll again only when it falls short.
+__device__ __forceinline__ unsigned wait_counter(const unsigned* c, unsigned v, int polls) {
   unsigned x = 0;
-  for (int i = 0; i < (1 << 16); i++) {
+  for (int i = 0; i < polls; i++) {
     x = ld_counter(c);
     if (x >= v) break;
     __builtin_amdgcn_s_sleep(2);
@@ -383,13 +386,14 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
         }
         // the previous period's ring stores have reached the device-coherent level (they had a period to get there)
         __builtin_amdgcn_s_waitcnt(0);
-        // chunk q - 1's set into slot (q - 1) % kDuoRing, once the consumer has taken chunk q - 1 - kDuoRing out of it
+        // chunk q - 1's set into its slot; while the consumer has not yet taken chunk q - 1 - kLead, hold back for up
+        // to 64 polls (the slot is this chunk's alone, so going on is always safe)
         if (q >= 1 && q <= n) {
           const int c = q - 1;
-          if (c >= kDuoRing && seen < ep + (unsigned)(c - kDuoRing + 1))
-            seen = wait_counter(consumed, ep + (unsigned)(c - kDuoRing + 1));
+          if (c >= kLead && seen < ep + (unsigned)(c - kLead + 1))
+            seen = wait_counter(consumed, ep + (unsigned)(c - kLead + 1), 64);
           const __amdgpu_buffer_rsrc_t rs =
-              __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)(c % kDuoRing) * kDuoSetBytes, 0, kDuoSetBytes, 0x00020000);
+              __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)c * kDuoSetBytes, 0, kDuoSetBytes, 0x00020000);
           const unsigned char* from = sm.s[c % 3].raw;
           for (int i = tid - 64; i < kDuoSetBytes / 16; i += 192) {
             const f4 v = lds4(reinterpret_cast<const float*>(from + 16 * i));
@@ -400,7 +404,7 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
       }
     }
     __syncthreads();
-    if (tid0 == 64 && q >= 2) st_counter(produced, ep + (unsigned)(q - 1));  // chunks 0 .. q - 2 are in the ring
+    if (tid0 == 64 && q >= 2) st_counter(produced, ep + (unsigned)(q - 1));  // chunks 0 .. q - 2 are in their slots
   }
 }
 
@@ -467,10 +471,12 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
 #pragma unroll
     for (int q = 0; q < 4; q++) zn[q] = ld4(zr + 4 * q);
   };
-  // chunk c's tile set from its ring slot into LDS: whole 1 KiB DMA instructions, helper wave wq issues every fourth
+  // chunk c's tile set from its slot into LDS: whole 1 KiB DMA instructions, helper wave wq issues every fourth. The
+  // producer is resident or done (it is dispatched first and waits for nothing), so the wait ends; its bound (2^16
+  // polls) only keeps the kernel finite.
   auto dma_set = [&](int c, int wq) {
-    if (seen < ep + (unsigned)(c + 1)) seen = max(seen, wait_counter(produced, ep + (unsigned)(c + 1)));
-    const char* from = ring + (size_t)(c % kDuoRing) * kDuoSetBytes;
+    if (seen < ep + (unsigned)(c + 1)) seen = max(seen, wait_counter(produced, ep + (unsigned)(c + 1), 1 << 16));
+    const char* from = ring + (size_t)c * kDuoSetBytes;
     unsigned char* to = sm.s[c & 1].raw;
     const int ln = opaque(tid0) & 63;
     for (int i = wq; i < kDuoSetBytes / 1024; i += 4)
@@ -675,8 +681,9 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
   for (; p <= n; p++) period(p);
 }
 
-// Blocks 16 i + r (r < 8) and 16 i + 8 + r form pair 8 i + r: the dispatcher hands consecutive blocks to the XCDs in
-// turn, so both members of a pair share an XCD and its L2.
+// Blocks 16 i + r (r < 8, the producer) and 16 i + 8 + r (the consumer) form pair 8 i + r. The dispatcher hands
+// consecutive blocks to the XCDs in turn and each XCD takes its blocks in order, so both members of a pair share an
+// XCD (and its L2), and the producer comes first.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void gdn_duo_kernel(GdnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
@@ -685,12 +692,12 @@ __global__ __launch_bounds__(kThreads) void gdn_duo_kernel(GdnArgs a) {
   const int b = pair / a.H, h = pair % a.H;
   unsigned* const produced = a.duo_flags + (size_t)pair * 64;  // each counter on its own 128-byte line
   unsigned* const consumed = produced + 32;
-  char* const ring = (char*)a.duo_ring + (size_t)pair * kDuoRing * kDuoSetBytes;
-  const unsigned ep = a.duo_epoch * 256u;
+  char* const ring = (char*)a.duo_ring + (size_t)pair * a.duo_slots * kDuoSetBytes;
+  const unsigned ep = a.duo_epoch << kDuoEpochShift;
   if ((blk >> 3) & 1)
-    produce<T>(a, b, h, *reinterpret_cast<ProducerLds*>(lds_raw), ring, produced, consumed, ep);
-  else
     consume<T>(a, b, h, *reinterpret_cast<ConsumerLds*>(lds_raw), ring, produced, consumed, ep);
+  else
+    produce<T>(a, b, h, *reinterpret_cast<ProducerLds*>(lds_raw), ring, produced, consumed, ep);
 }
 
 template <typename T>
@@ -699,10 +706,8 @@ hipError_t launch(const GdnArgs& a, hipStream_t s) {
   const int lds = (int)(sizeof(ConsumerLds) > sizeof(ProducerLds) ? sizeof(ConsumerLds) : sizeof(ProducerLds));
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;
-  GdnArgs arg = a;
-  void* params[] = {&arg};
-  return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k), dim3(2 * a.B * a.H), dim3(kThreads), params,
-                                    (unsigned)lds, s);
+  hipLaunchKernelGGL(k, dim3(2 * a.B * a.H), dim3(kThreads), (unsigned)lds, s, a);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -713,6 +718,9 @@ hipError_t launch_gdn_duo(const GdnArgs& a, hipStream_t s) {
   if (a.DK != kDK || a.DV != kDV || a.KC != kKC) return hipErrorInvalidValue;
   if (a.P - a.s0 >= 64 || a.P < a.s0) return hipErrorInvalidValue;  // at most one open 64-row span is replayed
   if (!gdn_duo_fits(a.B, a.H) || !a.duo_ring || !a.duo_flags) return hipErrorInvalidValue;
+  const int n = (a.P + a.L - a.s0 + kC - 1) / kC;  // chunks of the call: one slot each, and the counters' chunk field
+  if (n > a.duo_slots || n + 2 >= (1 << kDuoEpochShift) || a.duo_epoch >= (1u << (32 - kDuoEpochShift)))
+    return hipErrorInvalidValue;
   return a.dtype == 0 ? launch<float>(a, s) : launch<_Float16>(a, s);
 }
 

@@ -28,13 +28,14 @@ struct GdnArgs {
   int img_chunks;                   // image slots per (sequence, head)
   float* seq_raw;                   // sequential form: raw outputs [B][H][kSegRows][DV] fp32 awaiting the gated norm
   unsigned* seq_cnt;                // sequential form: [B][H] arrival counters (zero between launches)
-  void* duo_ring;                   // paired form: [B*H][kDuoRing] tile-set slots of kDuoSetBytes
+  void* duo_ring;                   // paired form: [B*H][duo_slots] tile-set slots of kDuoSetBytes, one per chunk
+  int duo_slots;                    // paired form: slots per (sequence, head), at least the call's 32-row chunks
   unsigned* duo_flags;              // paired form: [B*H][64] progress counters (produced at 0, consumed at 32)
   unsigned duo_epoch;               // paired form: this launch's counter epoch, >= 1 and increasing per flag buffer
 };
 constexpr int kSegRows = 64;        // output rows per launch of the sequential form
-constexpr int kDuoRing = 6;               // tile-set slots per (sequence, head) of the paired form
-constexpr int kDuoSetBytes = 36 * 1024;   // bytes per slot
+constexpr int kDuoSetBytes = 36 * 1024;   // bytes per tile-set slot of the paired form
+constexpr int kDuoEpochShift = 12;        // paired-form counter value: epoch << kDuoEpochShift | chunks (< 4096)
 
 // Full-attention prep (q/k RMSNorm, partial RoPE, K/V cache write) and attention for rows [P, P + L).
 struct GqaArgs {
@@ -74,7 +75,7 @@ struct TailArgs {
 
 hipError_t launch_gdn_sequential(const GdnArgs& a, hipStream_t s);
 hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t s);
-// paired form: a producer and a consumer workgroup per (sequence, head), cooperative launch of 2*B*H workgroups
+// paired form: a producer and a consumer workgroup per (sequence, head), 2*B*H workgroups
 bool gdn_duo_fits(int B, int H);
 hipError_t launch_gdn_duo(const GdnArgs& a, hipStream_t s);
 hipError_t launch_gdn_split(const GdnArgs& a, hipStream_t s);  // chunk-parallel preparation + recurrence

@@ -34,10 +34,9 @@ def _params():
 def test_node_forward_resume_release(tmp_path):
     d = str(tmp_path)
     params = _params()
-    # one form in both hosts: the default for B * H = 32 (the paired form) needs a cooperative launch, which the device
-    # refuses to the Node child while this process, which has made such launches, is alive (the engine then falls back
-    # to the fused kernel; tests/test_gpu_paired_fallback.py covers that)
-    rec = ha.CHUNKED_FUSED
+    # the engine's default form for B * H = 32 (the paired form) in both hosts, while this process is alive and has
+    # run that form itself
+    rec = ha.CHUNKED
     spec = {"kinds": KINDS, "batch": B, "maxCtx": 4096, "T0": T0, "T1": T1, "params": [], "recurrence": rec}
     for i, p in enumerate(params):
         names = {}
