@@ -57,8 +57,8 @@ typedef enum ha_dtype { HA_F32 = 0, HA_F16 = 1 } ha_dtype;
 typedef enum ha_recurrence {
   HA_CHUNKED = 0,        /* prefill form: chunks at absolute positions, MFMA products, the state stored at the last
                             64-row boundary (default; the engine picks one of the implementations below from its batch
-                            and head count B*H: the split form up to 16, the paired form up to 128, the fused kernel
-                            beyond) */
+                            and head count B*H: the paired form for a multiple of 8 up to 128, the split form for
+                            another count up to 16, the fused kernel beyond) */
   HA_SEQUENTIAL = 1,     /* token-by-token fp32 rule with the state in registers (decode / resume) */
   HA_CHUNKED_FUSED = 2,  /* the chunked form in one kernel per layer: one workgroup per (sequence, head), 64-row chunks */
   HA_CHUNKED_SPLIT = 3,  /* the chunked form in two kernels: every chunk's state-independent part at once, then the

@@ -169,11 +169,12 @@ const ha_engine* snapshot_owner(const ha_snapshot* s) {
 }
 
 // HA_CHUNKED's choice of gated-delta prefill, from the engine's shape alone so that every call rounds alike: the
-// two-kernel form for one sequence's heads, the paired form while two workgroups per recurrence fit the 256 CUs, the
-// fused kernel beyond. Measured per layer at T = 2048 (split / paired / fused, us): B=1 186 / 196 / -, B=2 229 / 197 /
-// 280, B=4 - / 226 / 295, B=8 - / 292 / 313.
-bool split_by_shape(const ha_config& c) { return c.batch * c.H <= 16; }
-bool paired_by_shape(const ha_config& c) { return !split_by_shape(c) && ha::gdn_duo_fits(c.batch, c.H); }
+// paired form while its two workgroups per recurrence fit the 256 CUs in one round (B*H a multiple of 8, at most 128),
+// the two-kernel form for fewer sequence-heads of another count, the fused kernel beyond. Measured per layer at
+// T = 2048, 18 forwards back to back (split / paired / fused, us): B=1 182 / 176 / -, B=2 223 / 177 / -,
+// B=8 - / 271 / 303, B=16 - / - / 350.
+bool paired_by_shape(const ha_config& c) { return ha::gdn_duo_fits(c.batch, c.H); }
+bool split_by_shape(const ha_config& c) { return !paired_by_shape(c) && c.batch * c.H <= 16; }
 
 int check_config(const ha_config* c) {
   if (!c) return fail(HA_ERR_ARG, "config is NULL");

@@ -1,9 +1,9 @@
 """Call-time device buffers held by several engines (ha_share_scratch) and allocated on demand:
-- engines holding one set (a one-sequence gated-delta engine using chunk images, a four-sequence one forced to the
-  two-kernel form, and a one-sequence full-attention engine with split key ranges), called one after another on one
-  stream, give bit for bit what engines with their own sets give, through every form (fused, two-kernel, paired,
+- engines holding one set (a one-sequence and a four-sequence gated-delta engine, each also forced to the two-kernel
+  form, and a one-sequence full-attention engine with split key ranges), called one after another on one stream,
+  give bit for bit what engines with their own sets give, through every form (fused, two-kernel, paired,
   sequential, split GQA) and again on a second round of calls;
-- the four-sequence engine's shape does not pick the two-kernel form, so its images come from the first call that
+- neither gated-delta engine's shape picks the two-kernel form, so the chunk images come from the first call that
   forces it: those outputs also match the fp64 oracle."""
 import numpy as np
 import pytest
@@ -37,7 +37,8 @@ def _calls(lin1, lin4, full):
     q = synth.gqa_rows(300, seed=5).astype(np.float16)
     out = []
     for _ in range(2):
-        out.append(lin1.forward([x1])[0][0])                                # two-kernel form by shape
+        out.append(lin1.forward([x1])[0][0])                                # paired form by shape
+        out.append(lin1.forward([x1], recurrence=ha.CHUNKED_SPLIT)[0][0])   # images from a forced call
         out.append(full.forward([q])[0][0])                                 # split key ranges
         out.append(lin4.forward([x4], recurrence=ha.CHUNKED_SPLIT)[0][0])   # images from a forced call
         out.append(lin4.forward([x4[:, :40]], recurrence=ha.SEQUENTIAL)[0][0])
@@ -52,12 +53,13 @@ def test_shared_scratch_is_bit_identical_and_lazy_images_match_the_oracle():
     own, x4 = _calls(*_engines(torch, share=False))
     print("one shared set", flush=True)
     shared, _ = _calls(*_engines(torch, share=True))
-    names = ["split B=1", "GQA split", "forced split B=4", "sequential B=4", "paired B=4", "fused B=4"] * 2
+    names = ["paired B=1", "forced split B=1", "GQA split", "forced split B=4", "sequential B=4", "paired B=4",
+             "fused B=4"] * 2
     for n, a, b in zip(names, own, shared):
         assert np.array_equal(a, b), n
-    for a, b in zip(own[:6], own[6:]):  # a second round of calls on the same buffers
+    for a, b in zip(own[:7], own[7:]):  # a second round of calls on the same buffers
         assert np.array_equal(a, b)
     ref, _ = oracle_gdn(x4, synth.gdn_params(seed=4))
-    e = rel_err(own[2], ref)
+    e = rel_err(own[3], ref)
     print("forced two-kernel form at B=4 vs fp64: %.2e" % e)
     assert e < 2e-3
