@@ -47,6 +47,11 @@ constexpr int kMP = kC + 4;     // row pitch (floats) of the fp32 A / T tile
 constexpr int kThreads = 512;   // 8 waves per workgroup
 constexpr int kOP = kDV + 4;    // row pitch (floats) of the consumer's output rows
 constexpr int kLead = 6;        // chunks the producer may run ahead of the consumer before it holds back
+// Vector memory instructions a helper wave issues after its tile-set DMA in every period: the v rows (kKC + 3 loads), the
+// z rows (4) and the counter (1). s_waitcnt with vmcnt = kAfterDma (expcnt and lgkmcnt not waited for) then covers
+// the DMA alone.
+constexpr int kAfterDma = kKC + 3 + 4 + 1;
+constexpr int kWaitDma = (kAfterDma & 15) | ((kAfterDma >> 4) << 14) | (7 << 4) | (15 << 8);
 
 typedef int i4v __attribute__((ext_vector_type(4)));
 
@@ -440,7 +445,8 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
   if (!state && a.gnorm)
 #pragma unroll
     for (int q = 0; q < 4; q++) gw[q] = ld4(gp<float>(a.gnorm) + 16 * (ht0 & 7) + 4 * q);
-  unsigned seen = 0;  // the producer's progress as last read (helper waves); a read is issued every period, ahead of use
+  unsigned seen = 0;   // the producer's progress as last read (helper waves)
+  unsigned ahead = 0;  // the read issued in the previous period, taken into `seen` at the next period's start
   auto fetch_v = [&](int cs) {
     const int ht = opaque(tid0) - 256, vrg = ht >> 5, cvg = ht & 31;
     fetch_rows<T>(a, src, b, min(cs, last_cs), 4 * vrg, 2 * a.H * kDK + h * kDV + 4 * cvg, xn);
@@ -504,19 +510,13 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
       for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
     vconv(a.s0);
     fetch_v(a.s0 + kC);
-    if (a.gnorm) fetch_z(a.s0);
+    fetch_z(a.s0);
   }
   // Drain the prologue's loads: the compiler's wait counting merges the loop's entry state into every period, so a load
   // still outstanding at the loop head would make each period's first use of its registers wait for every global access
   // issued before it.
   __builtin_amdgcn_s_waitcnt(0);
   if (state) __syncthreads();
-#pragma unroll
-  for (int q = 0; q < 4; q++) zq[q] = zn[q];
-#pragma unroll
-  for (int r = 0; r < kKC + 3; r++)
-#pragma unroll
-    for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
   __syncthreads();
   if (tid0 == 256) st_counter(consumed, ep + 1u);
 
@@ -620,12 +620,25 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
         }
       }
     } else {
-      // the tile set's DMA first, so that it lands behind this period's work; then the small loads (vector memory
-      // instructions issue in order, so these queue behind the DMA but are not waited for until the period's end)
+      // the rows loaded during the previous period (their loads had that period and its barrier to land)
+      seen = max(seen, ahead);
+#pragma unroll
+      for (int r = 0; r < kKC + 3; r++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
+#pragma unroll
+      for (int q = 0; q < 4; q++) zq[q] = zn[q];
+      // the tile set's DMA first, so that it lands behind this period's work; then exactly kAfterDma loads, none of
+      // them conditional (z too: its columns exist with or without the gated norm), which the period's end does not
+      // wait for
       if (p + 1 < n) dma_set(p + 1, hw);
+      asm volatile("" ::: "memory");  // the loads below stay behind the DMA, in the compiler and the scheduler
+      __builtin_amdgcn_sched_barrier(0);
       fetch_v(c0 + 2 * kC);
-      if (a.gnorm) fetch_z(c0);
-      const unsigned ahead = ld_counter(produced);  // for the next period's check
+      fetch_z(c0);
+      ahead = ld_counter(produced);  // for the next period's check
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
       if (p >= 1) {
         // chunk p - 1's gated norm and store
         const int cp = c0 - kC, mp = min(kC, end - cp), fr = ht0 >> 3, fc = 16 * (ht0 & 7);
@@ -649,14 +662,9 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
         }
       }
       if (p + 1 < n) vconv(c0 + kC);
-      __builtin_amdgcn_s_waitcnt(0);  // chunk p + 1's tile set has landed in LDS; the next rows are in registers
-      seen = max(seen, ahead);
-#pragma unroll
-      for (int r = 0; r < kKC + 3; r++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
-#pragma unroll
-      for (int q = 0; q < 4; q++) zq[q] = zn[q];
+      // chunk p + 1's tile set has landed in LDS: at most the kAfterDma loads issued after the DMA (and the stores
+      // after them) may still be in flight (vmcnt counts in issue order)
+      __builtin_amdgcn_s_waitcnt(kWaitDma);
     }
     __syncthreads();
     if (tid0 == 256 && p + 1 < n) st_counter(consumed, ep + (unsigned)(p + 2));

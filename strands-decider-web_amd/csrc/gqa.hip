@@ -22,6 +22,7 @@
 //   a score exceeds it by 2^8, so the 128 O accumulators are rarely rescaled; the decision is per row, which keeps
 //   every row's arithmetic independent of the other rows in its block (prefix + suffix stays bit-identical).
 #include <algorithm>
+#include <type_traits>
 
 #include "ha_kernels.h"
 
@@ -269,15 +270,15 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
                                        (__attribute__((address_space(3))) void*)(vb + (size_t)ins * 512), 16, 0, 0);
     }
   };
-  issue(kt0, lane);
 
   // Q as the B operand of S^T = K Q^T (32x32x16): qreg[ks] = q[q0 + c32][16 ks + 8 half .. +7], prepared here:
   // RMSNorm (the two halves of a row sit in lanes l and l + 32), RoPE (dim i < 32 in ks 0/1 pairs with i + 32 in
   // ks 2/3 of the same lane and element), then f16(f16(.) / sqrt(HD)). A row past the end (t >= L) repeats row
   // L - 1: rows are independent and such a row is never stored, so every load here is unconditional.
-  // qw (the stored 1 + w) is staged in LDS (tile buffer 1, unused until the loop): every lane needs 128 of the 256
-  // weights, the same ones as every other lane of its half.
-  float* qw_l = reinterpret_cast<float*>(lds_raw + 2 * (size_t)kTileBytes);
+  // qw (the stored 1 + w) is staged in LDS, in the tile buffer the first tile does not use (nothing is loaded into it
+  // before the loop): every lane needs 128 of the 256 weights, the same ones as every other lane of its half.
+  // The first tile's K/V copy is issued once the lane's Q loads are out, so that those return first.
+  float* qw_l = reinterpret_cast<float*>(lds_raw + (size_t)(((kt0 & 1) ^ 1) * 2) * kTileBytes);
   if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = *(gptr<f4>)(gp<float>(a.qw) + 4 * tid);
   h8 qreg[16];
   {
@@ -315,6 +316,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
       h8 raw[16];
 #pragma unroll
       for (int ks = 0; ks < 16; ks++) raw[ks] = *(gptr<h8>)(src + 16 * ks + 8 * half);
+      issue(kt0, lane);
 #pragma unroll
       for (int ks = 0; ks < 16; ks++)
 #pragma unroll
@@ -351,6 +353,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
 #pragma unroll
           for (int e = 0; e < 8; e++) ss += qv[k][e] * qv[k][e];
         asm volatile("" : "+v"(ss)::"memory");
+        if (bt == 0) issue(kt0, lane);
       }
       const float inv = rsqrtf(sum_halves(ss) / kHD + 1e-6f);
       __syncthreads();  // qw staged
@@ -518,16 +521,26 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   // epilogue: out[t][h][d] = O / l * sigmoid(gate), through LDS (free after the loop's last barrier). Each wave
   // stages 32 rows x 128 dims of O / l at a time; then a lane handles 4 consecutive dims of a row (rows 2 i + er),
   // so gate loads and output stores are 8- or 16-byte accesses, all issued before they are needed.
+  // The gate loads of f16 rows (both passes, 64 VGPRs once Q is dead) are all issued first; f32 rows load each pass's
+  // at its start.
+  typedef typename std::conditional<sizeof(T) == 2, h4, f4>::type G4;
+  G4 graw[2][16];
+  auto load_gates = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int tc = min(q0 + 2 * i + er, a.L - 1);
+      graw[p][i] = *(gptr<G4>)(gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD + 128 * p + ec);
+    }
+  };
+  load_gates(0);
+  if constexpr (sizeof(T) == 2) load_gates(1);
   float linv[16];
 #pragma unroll
   for (int v = 0; v < 16; v++) linv[v] = 1.0f / __shfl(lsum, 8 * (v >> 2) + 4 * half + (v & 3));
 #pragma unroll
   for (int p = 0; p < 2; p++) {
-    f4 g[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int tc = min(q0 + 2 * i + er, a.L - 1);
-      g[i] = ld4(gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD + 128 * p + ec);
+    if constexpr (sizeof(T) == 4) {
+      if (p == 1) load_gates(1);
     }
 #pragma unroll
     for (int j = 0; j < 4; j++)
@@ -540,7 +553,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
       const f4 o = lds4(ep + (2 * i + er) * kEP + ec);
       f4 r;
 #pragma unroll
-      for (int c = 0; c < 4; c++) r[c] = o[c] * sigmoid(g[i][c]);
+      for (int c = 0; c < 4; c++) r[c] = o[c] * sigmoid((float)graw[p][i][c]);
       if (t < a.L) store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + 128 * p + ec, r);
     }
     wave_sync();
