@@ -435,7 +435,8 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     sm.cwv[lc & 3][lc >> 2][j] = gp<float>(a.conv_w)[(size_t)(2 * a.H * kDK + h * kDV + lc) * kKC + j];
   }
 
-  // Helper lanes: v conv of rows 4 vrg .. + 3, channels 4 cvg .. + 3; gated norm of row fr, columns fc .. fc + 15.
+  // Helper lanes: v conv of rows 4 vrg .. + 3, channels 4 cvg .. + 3; gated norm of row fr, columns fc + 32 q .. + 3
+  // (q < 4), so that the 8 lanes of a row cover one contiguous 128-byte span per z load and output store.
   // They hold the raw v rows and the z rows of the chunks they work on next, loaded a period ahead (every period, on
   // clamped rows past the end, so that the registers are never a merge of old and new loads) into second buffers.
   const int ht0 = tid0 - 256;
@@ -444,7 +445,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
   f4 zq[4], zn[4], gw[4] = {};
   if (!state && a.gnorm)
 #pragma unroll
-    for (int q = 0; q < 4; q++) gw[q] = ld4(gp<float>(a.gnorm) + 16 * (ht0 & 7) + 4 * q);
+    for (int q = 0; q < 4; q++) gw[q] = ld4(gp<float>(a.gnorm) + 4 * (ht0 & 7) + 32 * q);
   unsigned seen = 0;   // the producer's progress as last read (helper waves)
   unsigned ahead = 0;  // the read issued in the previous period, taken into `seen` at the next period's start
   auto fetch_v = [&](int cs) {
@@ -471,11 +472,11 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     }
   };
   auto fetch_z = [&](int c0) {
-    const int ht = opaque(tid0) - 256, fr = ht >> 3, fc = 16 * (ht & 7);
+    const int ht = opaque(tid0) - 256, fr = ht >> 3, fc = 4 * (ht & 7);
     const int rr = min(max(min(c0, last_cs) + fr - a.P, 0), a.L - 1);
     const gptr<T> zr = gp<T>(seq_in) + (size_t)rr * a.stride + a.C + h * kDV + fc;
 #pragma unroll
-    for (int q = 0; q < 4; q++) zn[q] = ld4(zr + 4 * q);
+    for (int q = 0; q < 4; q++) zn[q] = ld4(zr + 32 * q);
   };
   // chunk c's tile set from its slot into LDS: whole 1 KiB DMA instructions, helper wave wq issues every fourth. The
   // producer is resident or done (it is dispatched first and waits for nothing), so the wait ends; its bound (2^16
@@ -641,11 +642,11 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
       __builtin_amdgcn_sched_barrier(0);
       if (p >= 1) {
         // chunk p - 1's gated norm and store
-        const int cp = c0 - kC, mp = min(kC, end - cp), fr = ht0 >> 3, fc = 16 * (ht0 & 7);
+        const int cp = c0 - kC, mp = min(kC, end - cp), fr = ht0 >> 3, fc = 4 * (ht0 & 7);
         const float* osg = sm.osg[(p - 1) & 1];
         f4 y[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) y[q] = lds4(&osg[fr * kOP + fc + 4 * q]);
+        for (int q = 0; q < 4; q++) y[q] = lds4(&osg[fr * kOP + fc + 32 * q]);
         if (a.gnorm) {
           const f4 r = lds4(&sm.red[(p - 1) & 1][fr * 4]);
           const float iv = rsqrtf(((r[0] + r[1]) + (r[2] + r[3])) / kDV + 1e-6f);
@@ -658,7 +659,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
           __attribute__((address_space(1))) T* orow =
               gpw<T>((char*)a.out + ((size_t)b * a.L + (cp + fr - a.P)) * (size_t)orowb) + (size_t)h * kDV + fc;
 #pragma unroll
-          for (int q = 0; q < 4; q++) store4(orow + 4 * q, y[q]);
+          for (int q = 0; q < 4; q++) store4(orow + 32 * q, y[q]);
         }
       }
       if (p + 1 < n) vconv(c0 + kC);
