@@ -47,10 +47,10 @@ constexpr int kMP = kC + 4;     // row pitch (floats) of the fp32 A / T tile
 constexpr int kThreads = 512;   // 8 waves per workgroup
 constexpr int kOP = kDV + 4;    // row pitch (floats) of the consumer's output rows
 constexpr int kLead = 6;        // chunks the producer may run ahead of the consumer before it holds back
-// Vector memory instructions a helper wave issues after its tile-set DMA in every period: the v rows (kKC + 3 loads), the
+// Vector memory instructions a helper wave issues after its tile-set DMA in every period: the v rows (kKC + 7 loads), the
 // z rows (4) and the counter (1). s_waitcnt with vmcnt = kAfterDma (expcnt and lgkmcnt not waited for) then covers
 // the DMA alone.
-constexpr int kAfterDma = kKC + 3 + 4 + 1;
+constexpr int kAfterDma = kKC + 7 + 4 + 1;
 constexpr int kWaitDma = (kAfterDma & 15) | ((kAfterDma >> 4) << 14) | (7 << 4) | (15 << 8);
 
 typedef int i4v __attribute__((ext_vector_type(4)));
@@ -85,7 +85,7 @@ struct ProducerLds {
 };
 struct ConsumerLds {
   SetBuf s[2];                 // chunk p (state waves) and chunk p + 1 (DMA target)
-  _Float16 VT[2][kDV * kP];    // v^ transposed, [j][t], by chunk parity
+  _Float16 VT[2][kDV * kP];    // v^ transposed, [j][t] (8-row groups swizzled by vt32), by chunk parity
   float osg[2][kC * kOP];      // output rows before the gated norm, by chunk parity
   float red[2][kC * 4];        // gated-norm partial sums, [t][state wave], by chunk parity
   float cwv[4][32][kKC];       // v conv taps: channel 4 g + c at cwv[c][g]
@@ -94,6 +94,11 @@ struct ConsumerLds {
 // k^T element (i, t) lives at i * kP + 8 * ((t / 8) ^ ((i / 16) % 4)) + t % 8: a producer lane writes 8 rows of one
 // channel (16 bytes) and the 32 lanes writing channels 4 l + c land on different banks
 __device__ __forceinline__ int kt32(int i, int g8) { return i * kP + 8 * (g8 ^ ((i >> 4) & 3)); }
+
+// v^T element (j, t) lives at j * kP + 8 * ((t / 8) ^ ((j / 16) % 4)) + t % 8: the state waves read 8 rows of one
+// channel (16 bytes, a B operand) and the helpers write 4 rows of channels 4 cvg + c, which without the swizzle
+// would put every fourth lane on the same banks
+__device__ __forceinline__ int vt32(int j, int g8) { return j * kP + 8 * (g8 ^ ((j >> 4) & 3)); }
 
 // perm_a for the swizzled k^T tile (one K block of 32 chunk rows)
 __device__ __forceinline__ h8 perm_a_kt32(const _Float16* kt, int r, int grp) {
@@ -129,24 +134,38 @@ __device__ __forceinline__ unsigned wait_counter(const unsigned* c, unsigned v, 
   return x;
 }
 
-// Loads rows cs + r0 - 3 .. cs + r0 + NR - 4 (NR = the rows x holds) at element column `col`, 4 channels. Uniform row
-// bases and 32-bit lane offsets when no row is a replay row or past the end; per-lane row pointers otherwise. Rows
-// past the end repeat the last row: they only feed conv outputs past the end, which are masked.
-template <typename T, int NR>
+// NC consecutive channels of one row (one 8- or 16-byte load)
+__device__ __forceinline__ void loadc(gptr<float> p, float (&o)[4]) { load4(p, o); }
+__device__ __forceinline__ void loadc(gptr<_Float16> p, float (&o)[4]) { load4(p, o); }
+__device__ __forceinline__ void loadc(gptr<float> p, float (&o)[2]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 x = *(gptr<f2>)(p);
+  o[0] = x[0]; o[1] = x[1];
+}
+__device__ __forceinline__ void loadc(gptr<_Float16> p, float (&o)[2]) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 x = *(gptr<h2>)(p);
+  o[0] = (float)x[0]; o[1] = (float)x[1];
+}
+
+// Loads rows cs + r0 - 3 .. cs + r0 + NR - 4 (NR = the rows x holds) at element column `col`, NC channels. Uniform
+// row bases and 32-bit lane offsets when no row is a replay row or past the end; per-lane row pointers otherwise.
+// Rows past the end repeat the last row: they only feed conv outputs past the end, which are masked.
+template <typename T, int NR, int NC>
 __device__ __forceinline__ void fetch_rows(const GdnArgs& a, const RowSrc& src, int b, int cs, int r0, int col,
-                                           float (&x)[NR][4]) {
+                                           float (&x)[NR][NC]) {
   const int end = a.P + a.L;
   const unsigned rowb = (unsigned)a.stride * sizeof(T);
   if (cs - (kKC - 1) >= a.P && cs + kC <= end) {
     const char* base = (const char*)a.in + ((size_t)b * a.L + (cs - (kKC - 1) - a.P)) * rowb;
     const unsigned off = (unsigned)r0 * rowb + (unsigned)col * (unsigned)sizeof(T);
 #pragma unroll
-    for (int i = 0; i < NR; i++) load4(gp<T>(base + (size_t)i * rowb + off), x[i]);
+    for (int i = 0; i < NR; i++) loadc(gp<T>(base + (size_t)i * rowb + off), x[i]);
   } else {
 #pragma unroll
     for (int i = 0; i < NR; i++) {
       const int r = cs + r0 - (kKC - 1) + i, rc = min(r, end - 1);
-      load4(row_of<T>(a, src, b, rc) + col, x[i]);
+      loadc(row_of<T>(a, src, b, rc) + col, x[i]);
     }
   }
 }
@@ -435,13 +454,15 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     sm.cwv[lc & 3][lc >> 2][j] = gp<float>(a.conv_w)[(size_t)(2 * a.H * kDK + h * kDV + lc) * kKC + j];
   }
 
-  // Helper lanes: v conv of rows 4 vrg .. + 3, channels 4 cvg .. + 3; gated norm of row fr, columns fc + 32 q .. + 3
+  // Helper lanes: v conv of rows 8 vrg .. + 7 (vrg = the helper wave), channels 2 cvg, 2 cvg + 1 (a row's 128 channels
+  // are one 512-byte load across the wave, and the 11 rows a lane loads for its 8 outputs overlap the next wave's by
+  // only 3); gated norm of row fr, columns fc + 32 q .. + 3
   // (q < 4), so that the 8 lanes of a row cover one contiguous 128-byte span per z load and output store.
   // They hold the raw v rows and the z rows of the chunks they work on next, loaded a period ahead (every period, on
   // clamped rows past the end, so that the registers are never a merge of old and new loads) into second buffers.
   const int ht0 = tid0 - 256;
   const RowSrc src = row_src(a);
-  float xv[kKC + 3][4], xn[kKC + 3][4];
+  float xv[kKC + 7][2], xn[kKC + 7][2];
   f4 zq[4], zn[4], gw[4] = {};
   if (!state && a.gnorm)
 #pragma unroll
@@ -449,26 +470,27 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
   unsigned seen = 0;   // the producer's progress as last read (helper waves)
   unsigned ahead = 0;  // the read issued in the previous period, taken into `seen` at the next period's start
   auto fetch_v = [&](int cs) {
-    const int ht = opaque(tid0) - 256, vrg = ht >> 5, cvg = ht & 31;
-    fetch_rows<T>(a, src, b, min(cs, last_cs), 4 * vrg, 2 * a.H * kDK + h * kDV + 4 * cvg, xn);
+    const int ht = opaque(tid0) - 256, vrg = ht >> 6, cvg = ht & 63;
+    fetch_rows<T>(a, src, b, min(cs, last_cs), 8 * vrg, 2 * a.H * kDK + h * kDV + 2 * cvg, xn);
   };
   auto vconv = [&](int cs) {
-    const int ht = opaque(tid0) - 256, vrg = ht >> 5, cvg = ht & 31;
+    const int ht = opaque(tid0) - 256, vrg = ht >> 6, cvg = ht & 63;
     const int mv = min(kC, end - cs);
     _Float16* VT = sm.VT[((cs - a.s0) / kC) & 1];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const f4 wc = lds4(sm.cwv[c][cvg]);
-      h4 vt;
+    for (int c = 0; c < 2; c++) {
+      const int j = 2 * cvg + c;
+      const f4 wc = lds4(sm.cwv[j & 3][j >> 2]);
+      h8 vt;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
+      for (int r = 0; r < 8; r++) {
         float sv = wc[0] * xv[r][c];
         sv = fmaf(wc[1], xv[r + 1][c], sv);
         sv = fmaf(wc[2], xv[r + 2][c], sv);
         sv = fmaf(wc[3], xv[r + 3][c], sv);
-        vt[r] = (_Float16)(4 * vrg + r < mv ? silu(sv) : 0.0f);
+        vt[r] = (_Float16)(8 * vrg + r < mv ? silu(sv) : 0.0f);
       }
-      *reinterpret_cast<h4*>(VT + (4 * cvg + c) * kP + 4 * vrg) = vt;
+      *reinterpret_cast<h8*>(VT + vt32(j, vrg)) = vt;
     }
   };
   auto fetch_z = [&](int c0) {
@@ -506,9 +528,9 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     dma_set(0, hw);
     __syncthreads();  // v conv taps visible (the state waves pass this barrier below)
 #pragma unroll
-    for (int r = 0; r < kKC + 3; r++)
+    for (int r = 0; r < kKC + 7; r++)
 #pragma unroll
-      for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
+      for (int c = 0; c < 2; c++) xv[r][c] = xn[r][c];
     vconv(a.s0);
     fetch_v(a.s0 + kC);
     fetch_z(a.s0);
@@ -564,7 +586,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
             for (int ct = 0; ct < 2; ct++) {
               const int col = 32 * w + 16 * ct + c16;
               const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
-              const f4 u = mfma16(tb, *reinterpret_cast<const h8*>(VT + col * kP + 8 * grp), z4);
+              const f4 u = mfma16(tb, *reinterpret_cast<const h8*>(VT + vt32(col, grp)), z4);
               const f4 ws = mfma16(tw, KSb[ct], z4);
               Vn[ct][ti] = u - ws;
             }
@@ -624,9 +646,9 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
       // the rows loaded during the previous period (their loads had that period and its barrier to land)
       seen = max(seen, ahead);
 #pragma unroll
-      for (int r = 0; r < kKC + 3; r++)
+      for (int r = 0; r < kKC + 7; r++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) xv[r][c] = xn[r][c];
+        for (int c = 0; c < 2; c++) xv[r][c] = xn[r][c];
 #pragma unroll
       for (int q = 0; q < 4; q++) zq[q] = zn[q];
       // the tile set's DMA first, so that it lands behind this period's work; then exactly kAfterDma loads, none of
