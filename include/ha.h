@@ -57,12 +57,13 @@ typedef enum ha_dtype { HA_F32 = 0, HA_F16 = 1 } ha_dtype;
 typedef enum ha_recurrence {
   HA_CHUNKED = 0,        /* prefill form: chunks at absolute positions, MFMA products, the state stored at the last
                             64-row boundary (default; the engine picks one of the implementations below from its batch
-                            and head count B*H: the paired form for a multiple of 8 up to 128, the split form for
-                            another count up to 16, the fused kernel beyond) */
+                            and head count B*H: the split form up to 32, the paired form for a multiple of 8 up to 128,
+                            the fused kernel beyond) */
   HA_SEQUENTIAL = 1,     /* token-by-token fp32 rule with the state in registers (decode / resume) */
   HA_CHUNKED_FUSED = 2,  /* the chunked form in one kernel per layer: one workgroup per (sequence, head), 64-row chunks */
-  HA_CHUNKED_SPLIT = 3,  /* the chunked form in two kernels: every chunk's state-independent part at once, then the
-                            recurrence over the chunks */
+  HA_CHUNKED_SPLIT = 3,  /* the chunked form in three kernels, 64-row chunks: every chunk's state-independent part at
+                            once, the state alone through the chunks (four workgroups per (sequence, head)), then
+                            every chunk's outputs at once */
   HA_CHUNKED_PAIRED = 4  /* the chunked form on two workgroups per (sequence, head), 32-row chunks: one prepares the
                             chunks' tiles, the other runs the recurrence (B*H a multiple of 8, at most 128) */
 } ha_recurrence;

@@ -21,6 +21,9 @@ SOURCES = ["engine.cpp", "gdn_seq.hip", "gdn_chunk.hip", "gdn_duo.hip", "gdn_spl
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
+# Per-source additions. -amdgpu-mfma-vgpr-form keeps MFMA accumulators in VGPRs: the state passes scale their fp32
+# accumulators on the VALU every chunk, which with AGPR accumulators costs a read and a write-back per element.
+FILE_FLAGS = {"gdn_split.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd, verbose):
@@ -42,7 +45,7 @@ def build_lib(verbose=False):
         obj = os.path.join(BUILD, src.replace(".", "_") + ".o")
         objs.append(obj)
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        jobs.append([HIPCC] + HIP_FLAGS + lang + ["-c", os.path.join(CSRC, src), "-o", obj])
+        jobs.append([HIPCC] + HIP_FLAGS + FILE_FLAGS.get(src, []) + lang + ["-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         list(ex.map(lambda c: _run(c, verbose), jobs))
     tmp = LIB + ".tmp"

@@ -73,7 +73,7 @@ struct Layer {
 
 size_t dtype_size(int dt) { return dt == HA_F16 ? 2 : 4; }
 
-// Device memory an engine's kernels use only inside a call: the two-kernel form's chunk images, the sequential
+// Device memory an engine's kernels use only inside a call: the split form's chunk images, the sequential
 // form's raw outputs and per-head arrival counters (zero between calls), split-GQA partial results, and the zero
 // history of an empty context. Engines whose calls never overlap may hold one set between them (ha_share_scratch);
 // it is freed with the last engine holding it. Every buffer only has to be large enough for each holder's shape.
@@ -121,7 +121,7 @@ struct ha_engine {
   std::vector<Layer> layers;
   float* rope = nullptr;
   // call-time buffers, possibly held with other engines: zeros [B][3][lin_stride] (the history of an empty context),
-  // images [B][H][img_chunks] of the two-kernel form (allocated when a call can use that form), the sequential
+  // images [B][H][img_chunks] of the split form (allocated when a call can use that form), the sequential
   // form's raw outputs [B][H][kSegRows][DV] and counters [B][H], split-GQA partials [gqa_part_slots]
   std::shared_ptr<Scratch> scratch;
   size_t need_zeros = 0, need_img = 0, need_seq_raw = 0, need_seq_cnt = 0, need_gqa = 0, need_duo_ring = 0,
@@ -169,12 +169,13 @@ const ha_engine* snapshot_owner(const ha_snapshot* s) {
 }
 
 // HA_CHUNKED's choice of gated-delta prefill, from the engine's shape alone so that every call rounds alike: the
-// paired form while its two workgroups per recurrence fit the 256 CUs in one round (B*H a multiple of 8, at most 128),
-// the two-kernel form for fewer sequence-heads of another count, the fused kernel beyond. Measured per layer at
-// T = 2048, 18 forwards back to back (split / paired / fused, us): B=1 182 / 176 / -, B=2 223 / 177 / -,
-// B=8 - / 271 / 303, B=16 - / - / 350.
-bool paired_by_shape(const ha_config& c) { return ha::gdn_duo_fits(c.batch, c.H); }
-bool split_by_shape(const ha_config& c) { return !paired_by_shape(c) && c.batch * c.H <= 16; }
+// three-kernel form (every chunk's preparation and output work spread over the chip, only the state pass sequential)
+// up to 32 sequence-heads, the paired form above that while its two workgroups per recurrence fit the 256 CUs in one
+// round (B*H a multiple of 8, at most 128), the fused kernel beyond. Measured per layer at T = 2048, 18 forwards back
+// to back (split / paired / fused, us): B=1 90 / 175 / -, B=2 148 / 176 / -, B=4 290 / 194 / -, B=8 - / 271 / 303,
+// B=16 - / - / 350.
+bool split_by_shape(const ha_config& c) { return c.batch * c.H <= 32; }
+bool paired_by_shape(const ha_config& c) { return !split_by_shape(c) && ha::gdn_duo_fits(c.batch, c.H); }
 
 int check_config(const ha_config* c) {
   if (!c) return fail(HA_ERR_ARG, "config is NULL");
@@ -341,7 +342,7 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
   if (e->any_linear) {
     e->need_zeros = dtype_size(c.lin_dtype) * B * (kKC - 1) * c.lin_stride;
     // chunk images: every chunk a call can touch (max_ctx / 64, plus the replayed open chunk); allocated here only
-    // when HA_CHUNKED picks the two-kernel form for this shape, else by the first call that forces that form
+    // when HA_CHUNKED picks the split form for this shape, else by the first call that forces that form
     e->img_chunks = (c.max_ctx + ha::kChunk - 1) / ha::kChunk + 1;
     e->need_img = ha::gdn_split_image_bytes() * B * c.H * e->img_chunks;
     e->need_seq_raw = sizeof(float) * B * c.H * ha::kSegRows * c.DV;
@@ -409,7 +410,7 @@ int ha_share_scratch(ha_engine* e, ha_engine* holder) {
   Scratch& to = *holder->scratch;
   const Scratch& from = *e->scratch;
   int rc;
-  // images only where e had them (its shape picks the two-kernel form, or a call forced it)
+  // images only where e had them (its shape picks the split form, or a call forced it)
   if ((rc = grow(to.zeros, e->need_zeros)) || (rc = grow(to.img, from.img.bytes ? e->need_img : 0)) ||
       (rc = grow(to.seq_raw, e->need_seq_raw)) ||
       (rc = grow(to.seq_cnt, e->need_seq_cnt)) || (rc = grow(to.gqa_part, e->need_gqa)) ||
@@ -504,7 +505,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   const bool paired = mode == HA_CHUNKED_PAIRED || (mode == HA_CHUNKED && paired_by_shape(c));
   Scratch& sc = *e->scratch;
   if (e->any_linear && chunked && split && sc.img.bytes < e->need_img) {
-    int rc = grow(sc.img, e->need_img);  // first call that forces the two-kernel form on a larger shape
+    int rc = grow(sc.img, e->need_img);  // first call that forces the split form on a larger shape
     if (rc) return rc;
   }
   if (e->any_linear && chunked && paired && (sc.duo_ring.bytes < e->need_duo_ring || sc.duo_flags.bytes < e->need_duo_flags)) {

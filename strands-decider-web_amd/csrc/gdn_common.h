@@ -1,5 +1,5 @@
 // Helpers shared by the chunked gated-delta kernels (gdn_chunk.hip: one fused kernel; gdn_split.hip: the
-// chunk-parallel preparation kernel and the recurrence kernel). Chunk geometry, the swizzled LDS tile layouts,
+// chunk-parallel preparation, state and output kernels). Chunk geometry, the swizzled LDS tile layouts,
 // the DPP reductions, global-pointer loads/stores and the MFMA operand conventions are described where they are
 // defined. Everything is in an anonymous namespace: each translation unit gets its own copy.
 #pragma once

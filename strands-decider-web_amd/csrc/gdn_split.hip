@@ -1,4 +1,4 @@
-// Chunked gated-delta prefill in two kernels, gfx950.
+// Chunked gated-delta prefill in three kernels, gfx950 (HA_CHUNKED_SPLIT; HA_CHUNKED for few sequence-heads).
 //
 // Same semantics and chunk geometry as gdn_chunk.hip (the sequential rule of reference
 // web/public/engine/wgsl.js:124-187 + 252-268 in the chunked WY/UT form, chunk 64, chunk boundaries at s0 + 64 k),
@@ -7,22 +7,18 @@
 //   W = T diag(beta e^gc) k^      U = T diag(beta) v^      V_new = U - W S
 //   o = diag(e^gc) q^ S + Att V_new,  Att = causal(q^ k^T e^(gc_t - gc_t'))   (t' <= t)
 //   S <- e^(gc_63) S + (diag(e^(gc_63 - gc)) k^)^T V_new                       (complete chunks only)
-// Everything except the three products with S depends only on the chunk's own rows, so
+// Everything except the products with S depends only on the chunk's own rows, and of those only the state update is
+// sequential, so
 //   gdn_prep_kernel  runs one workgroup per (chunk, sequence, head), all chunks at once over the whole chip, and
 //                    writes each chunk's "image": the MFMA A operands q~ = diag(e^gc) q^, W, K~^T and Att and the
-//                    matrix U, every operand block in lane order (64 lanes x 16 bytes), so that the recurrence
-//                    reads each with one conflict-free 16-byte LDS load and no lane moves;
-//   gdn_chain_kernel runs one workgroup per (sequence, head) through the chunks in order: 4 waves, each holding 32
-//                    value columns of the fp32 state in MFMA accumulators. Per chunk its dependent chain is
-//                    W S -> V_new -> state update; q~ S, Att V_new, the gated norm (GNORM) and the output are off
-//                    that chain. It DMAs image p+1 into the other of two LDS buffers while it works on chunk p.
-//
-// MFMA operand convention (v_mfma_f32_16x16x32_f16): lane l supplies row l & 15 of A and column l & 15 of B, with
-// K indices assigned per (lane group l >> 4, element); D holds rows 4 (l >> 4) + e of column l & 15. A D tile pair
-// (rows 32 kb .. 32 kb + 31 of a column) is reused as a B operand with the permuted K order
-// {32 kb + 4 grp + e} U {32 kb + 16 + 4 grp + e}; the image's A operands are stored in that same order. The prep
-// kernel obtains most of them as D tiles of transposed products (W^T = k^T (T diag(beta e^gc))^T and
-// Att^T = k^ q^T), whose lanes already hold exactly those K indices.
+//                    matrix U, every operand block in lane order (64 lanes x 16 bytes), so that the later kernels read
+//                    each with one conflict-free 16-byte LDS load and no lane moves;
+//   gdn_state_kernel carries the state through the chunks in order: four workgroups per (sequence, head) on 32 value
+//                    columns each, X = W S -> V_new -> S <- e^(gc_63) S + K~^T V_new per chunk, and leaves the packed
+//                    state at every chunk's start in that chunk's scratch;
+//   gdn_out_kernel   runs every chunk's outputs at once from its image and that packed state: o^T = S^T q~^T +
+//                    V_new^T Att^T, the gated norm (GNORM), the stores.
+
 #include <stddef.h>
 
 #include "gdn_common.h"
@@ -43,7 +39,12 @@ constexpr int kImg = 73 * kBlk;       // whole 1 KiB DMA instructions
 // the recurrence's transposed output: block (w, tb, jj) of 64 lanes x 4 floats holds, for lane (grp, c16),
 // columns 32 w + 16 jj + 4 grp .. + 3 of chunk row 16 tb + c16.
 constexpr int kGate = 32 * kBlk;
-constexpr int kChunkScratch = kImg + kGate;
+// After those, the scan schedule's state at the chunk's start, packed as the products with S read it (f16 B operands):
+// the h8 Sb[kb][jj] of lane l of wave w (state rows {32 kb + 4 grp + e} U {32 kb + 16 + 4 grp + e} of value column
+// 32 w + 16 jj + (l & 15)) at byte ((w * 4 + kb) * 2 + jj) * 1024 + 16 l.
+constexpr int kOffSnap = kImg + kGate;
+constexpr int kSnap = 32 * kBlk;
+constexpr int kChunkScratch = kImg + kGate + kSnap;
 
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i2v __attribute__((ext_vector_type(2)));
@@ -439,23 +440,7 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// gdn_chain_kernel: 4 waves; wave w owns value columns 32 w .. 32 w + 31 of the fp32 state (MFMA D layout:
-// S[ib][jj][e] = S[16 ib + 4 grp + e][32 w + 16 jj + c16]). Per period p (chunk p, image in LDS buffer p & 1):
-//   the DMA of image p+1 into the other buffer and the z rows of chunk p+1, issued first;
-//   X = W S (eight accumulator chains) and the first half of o^T = S^T q~^T, both from the packed state Sb;
-//   V_new = U - X; the state update S <- e^(gc_63) S + K~^T V_new (complete chunks), the dependent chain into the
-//   next chunk; o^T += V_new^T Att^T; the gated norm's factors w SiLU(z) in the shadow of those MFMAs;
-//   the 32-column row partials of the gated norm to LDS; barrier; 1/rms per row, output; wait for this wave's loads;
-//   barrier.
-// o is computed transposed (o^T = S^T q~^T + V_new^T Att^T: the packed state and V_new serve as A operands with the
-// same permuted K order in which they serve as B operands, and the image blocks of q~ and Att as B operands), so a
-// lane holds 4 consecutive value columns of one row: z loads and output stores are 16-byte accesses.
-constexpr int kCW = 4, kCT = 64 * kCW;
-
-struct ChainLds {
-  unsigned char img[2][kImg];  // chunk images; chunk p in img[p & 1]
-  float red[kCH * kCW];        // gated-norm partial sums, [t][wave]
-};
+constexpr int kCW = 4, kCT = 64 * kCW;  // output pass: 4 waves, wave w on value columns 32 w .. + 31
 
 __device__ __forceinline__ h8 lds16(const unsigned char* p) { return *reinterpret_cast<const h8*>(p); }
 
@@ -468,220 +453,275 @@ __device__ __forceinline__ float sum_col4(float x) {
   return __builtin_bit_cast(float, (unsigned)q[0]) + __builtin_bit_cast(float, (unsigned)q[1]);
 }
 
+// The sequential part is the state pass alone: per chunk four K blocks of MFMA products per wave, spread over four
+// CUs per (sequence, head). The output work runs afterwards on the whole chip.
+
+// gdn_state_kernel: kSG workgroups per (sequence, head), workgroup g on value columns 32 g .. + 31, its two waves on
+// 16 columns each (wave v: columns 32 g + 16 v + c16), so that a head's products spread over kSG CUs; each wave
+// reads the whole of W and K~^T every chunk, which with more waves per CU would make LDS reads the bound. Each chunk's
+// W and K~^T (image blocks 16..47), the workgroup's 32 columns of U (one 1 KiB block per row block) and e^(gc_63),
+// plus one block of padding so that both waves issue the same number of DMA instructions, arrive in one of four LDS
+// buffers three chunks ahead.
+constexpr int kSG = 4, kSV = 2, kSVT = 64 * kSV;
+constexpr int kStBlocks = 38;
+constexpr int kStBufs = 4;
+constexpr int kStDma = kStBlocks / kSV;  // DMA instructions per wave per chunk
+constexpr int kStW = 0, kStK = 16 * kBlk, kStU = 32 * kBlk, kStS = 36 * kBlk;  // LDS offsets in a buffer
+static_assert(kStBlocks % kSV == 0 && kOffS / kBlk + 1 < kChunkScratch / kBlk, "state-pass DMA blocks");
+// Vector memory instructions a wave issues after the DMA of chunk p + 1 (issued kStBufs - 1 periods before the end of
+// period p) up to that end: the four stores of the packed state of its own period, then kStBufs - 2 periods of a DMA
+// and four stores. s_waitcnt with that vmcnt and lgkmcnt 0 (expcnt not waited for) covers that DMA and this wave's
+// LDS reads.
+constexpr int kStAfter = 4 + (kStBufs - 2) * (kStDma + 4);
+constexpr int kStWait = (kStAfter & 15) | ((kStAfter >> 4) << 14) | (7 << 4);
+
+struct StateLds {
+  unsigned char buf[kStBufs][kStBlocks * kBlk];  // chunk p in buf[p % kStBufs]
+};
+
 template <typename T>
-__global__ __launch_bounds__(kCT) void gdn_chain_kernel(GdnArgs a) {
+__global__ __launch_bounds__(kSVT) void gdn_state_kernel(GdnArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[];
-  ChainLds& sm = *reinterpret_cast<ChainLds*>(lds_raw);
-  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
-  const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  StateLds& sm = *reinterpret_cast<StateLds*>(lds_raw);
+  const int g = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int tid0 = threadIdx.x, v = __builtin_amdgcn_readfirstlane(tid0 >> 6);
   const int end = a.P + a.L;
   const int nchunks = (a.L + (a.P - a.s0) + kCH - 1) / kCH;
-  const char* const imgs = (const char*)a.img + (size_t)bh * a.img_chunks * kChunkScratch;
+  char* const imgs = (char*)a.img + (size_t)bh * a.img_chunks * kChunkScratch;
   const size_t sbase = ((size_t)b * a.H + h) * kDK * kDV;
-  const int ostride = a.H * kDV;
+  const int col0 = 32 * g + 16 * v;  // this wave's first value column
 
-  // this wave's share of one chunk image, 1 KiB DMA instructions w, w + 4, ..., issued in three groups spread over
-  // the period (a wave that issues them all at once stalls until the memory pipeline has taken them)
-  auto issue_img = [&](int p, int part) {
-    const char* src = imgs + (size_t)p * kChunkScratch;
-    unsigned char* dst = sm.img[p & 1];
+  // chunk q's blocks into buf[d]: DMA instructions v, v + 2, ... (16 bytes per lane, whole 1 KiB blocks)
+  auto issue = [&](int q, int d) {
+    const char* src = imgs + (size_t)q * kChunkScratch;
+    unsigned char* dst = sm.buf[d];
     const int ln = opaque(tid0) & 63;
-    constexpr int kPer = (kImg / kBlk + 3 * kCW - 1) / (3 * kCW);
-    for (int k = part * kPer; k < (part + 1) * kPer; k++) {
-      const int i = w + kCW * k;
-      if (i < kImg / kBlk)
-        __builtin_amdgcn_global_load_lds(
-            (const __attribute__((address_space(1))) void*)(src + kBlk * (size_t)i + 16 * ln),
-            (__attribute__((address_space(3))) void*)(dst + kBlk * i), 16, 0, 0);
+#pragma unroll
+    for (int k = 0; k < kStDma; k++) {
+      const int i = v + kSV * k;
+      const int sb = i < 32 ? kOffW / kBlk + i : i < 36 ? kOffU / kBlk + 4 * (i - 32) + g : kOffS / kBlk + (i - 36);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + kBlk * (size_t)sb + 16 * ln),
+                                       (__attribute__((address_space(3))) void*)(dst + kBlk * i), 16, 0, 0);
     }
-  };
-  // the gate factors of chunk q at this lane's (transposed) output positions, straight into registers
-  f4 zq[4][2], zn[4][2];
-  auto fetch_z = [&](f4 (*z)[2], int q) {
-    const int lane = opaque(tid0) & 63;
-    const gptr<float> g = gp<float>(imgs + (size_t)q * kChunkScratch + kImg) + (size_t)(w * 8) * (kBlk / 4) + 4 * lane;
-#pragma unroll
-    for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-      for (int jj = 0; jj < 2; jj++) z[tb][jj] = ld4(g + (size_t)(tb * 2 + jj) * (kBlk / 4));
   };
 
   const int lane0 = tid0 & 63, grp0 = lane0 >> 4, c160 = lane0 & 15;
-  f4 S[8][2];
+  f4 S[8];
 #pragma unroll
   for (int ib = 0; ib < 8; ib++)
 #pragma unroll
-    for (int jj = 0; jj < 2; jj++)
+    for (int e = 0; e < 4; e++)
+      S[ib][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * ib + 4 * grp0 + e) * kDV + col0 + c160] : 0.0f;
 #pragma unroll
-      for (int e = 0; e < 4; e++)
-        S[ib][jj][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * ib + 4 * grp0 + e) * kDV + 32 * w + 16 * jj + c160]
-                              : 0.0f;
-  issue_img(0, 0);
-  issue_img(0, 1);
-  issue_img(0, 2);
-  if (a.gnorm) fetch_z(zq, 0);
-  // Drain the prologue's loads: the compiler's wait counting merges the loop's entry state into every iteration,
-  // so a load still outstanding at the loop head would make each period's first use of it wait for the DMA issued
-  // just before.
-  __builtin_amdgcn_s_waitcnt(0);
+  for (int q = 0; q < kStBufs - 1; q++) issue(min(q, nchunks - 1), q);
+  __builtin_amdgcn_s_waitcnt(0);  // the prologue's loads drained (else every period's first use would wait for them)
   __syncthreads();
-
-  for (int p = 0; p < nchunks; p++) {
-    const int c0 = a.s0 + kCH * p;
-    const int m = min(kCH, end - c0);
-    const bool full = m == kCH;
-    const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
-    const int lo16 = 16 * lane;
-    const bool more = p + 1 < nchunks;
-    if (more) issue_img(p + 1, 0);
-    // z of the next chunk, every period (past the last chunk on the last chunk's rows, never used): conditional
-    // loads would make the loop-carried registers a merge of old and new values, resolved with early waits
-    if (a.gnorm) fetch_z(zn, min(p + 1, nchunks - 1));
-    const unsigned char* im = sm.img[p & 1];
-
-    // the state as f16 operands: Sb[kb][jj] holds state rows {32 kb + 4 grp + e} U {32 kb + 16 + 4 grp + e} of
-    // column 32 w + 16 jj + c16 (B operand of W S; A operand, as S^T, of S^T q~^T)
-    h8 Sb[4][2];
+  // W of the period's chunk, read during the previous period (the first from the prologue)
+  h8 wa[4][4];
+  auto read_w = [&](int q) {
+    const unsigned char* im = sm.buf[q % kStBufs];
+    const int lo16 = 16 * (opaque(tid0) & 63);
 #pragma unroll
     for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-      for (int jj = 0; jj < 2; jj++) Sb[kb][jj] = pack_b(S[2 * kb][jj], S[2 * kb + 1][jj]);
-    // X = W S first (it feeds the dependent chain), then o^T = S^T q~^T; each K block's operands are read while
-    // the previous block's MFMAs issue
-    f4 X[4][2], O[2][4];
+      for (int tb = 0; tb < 4; tb++) wa[kb][tb] = lds16(im + kStW + (tb * 4 + kb) * kBlk + lo16);
+  };
+  read_w(0);
+
+  // Period p: the DMA of chunk p + kStBufs - 1; the packed state and its snapshot; K~^T of chunk p into registers
+  // while X = W S runs; the wait for chunk p + 1 and the barrier; W of chunk p + 1 into registers while V_new and the
+  // state update run. Every LDS read of a period's chunk thus has a stretch of MFMA work to land behind.
+  for (int p = 0; p < nchunks; p++) {
+    const int c0 = a.s0 + kCH * p;
+    const bool full = end - c0 >= kCH;
+    const int tid = opaque(tid0), lane = tid & 63;
+    const int lo16 = 16 * lane;
+    // every period (the last chunk again past the end, into a buffer nobody reads): the wait below counts a fixed
+    // number of instructions
+    issue(min(p + kStBufs - 1, nchunks - 1), (p + kStBufs - 1) % kStBufs);
+    const unsigned char* im = sm.buf[p % kStBufs];
+    h8 Sb[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++) Sb[kb] = pack_b(S[2 * kb], S[2 * kb + 1]);
+    {
+      __attribute__((address_space(1))) h8* snap = gpw<h8>(imgs + (size_t)p * kChunkScratch + kOffSnap) + lane;
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) snap[((g * 4 + kb) * 2 + v) * 64] = Sb[kb];
+    }
+    h8 kt[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int ib = 0; ib < 8; ib++) kt[kb][ib] = lds16(im + kStK + (ib * 2 + kb) * kBlk + lo16);
+    f4 X[4];
     const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    {
-      h8 wa[2][4];
-      auto read_w = [&](int s, int kb) {
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) wa[s][tb] = lds16(im + kOffW + (tb * 4 + kb) * kBlk + lo16);
-      };
-      read_w(0, 0);
+    for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++) {
-        if (kb < 3) read_w((kb + 1) & 1, kb + 1);
-        asm volatile("" : "+v"(Sb[kb][0]), "+v"(Sb[kb][1])::"memory");
+      for (int tb = 0; tb < 4; tb++) X[tb] = mfma16(wa[kb][tb], Sb[kb], kb ? X[tb] : z4);
+    h4 u[4];
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-          for (int jj = 0; jj < 2; jj++) X[tb][jj] = mfma16(wa[kb & 1][tb], Sb[kb][jj], kb ? X[tb][jj] : z4);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (more) issue_img(p + 1, 1);
-      h8 qa[2][4];
-      auto read_q = [&](int s, int kb) {
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++) qa[s][tb] = lds16(im + kOffQ + (tb * 4 + kb) * kBlk + lo16);
-      };
-      read_q(0, 0);
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++) {
-        if (kb < 3) read_q((kb + 1) & 1, kb + 1);
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++)
-#pragma unroll
-          for (int tb = 0; tb < 4; tb++) O[jj][tb] = mfma16(Sb[kb][jj], qa[kb & 1][tb], kb ? O[jj][tb] : z4);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    if (more) issue_img(p + 1, 2);
-    // V_new = U - X, kept in fp32 in the D layout and rounded once as an operand (K = chunk rows)
-    h8 Vb[2][2];
-    {
-      f4 Vn[4][2];
-#pragma unroll
-      for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-          const h4 u = *reinterpret_cast<const h4*>(im + kOffU + (tb * 8 + 2 * w + jj) * 512 + 8 * lane);
-          Vn[tb][jj] = f4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]} - X[tb][jj];
-        }
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) Vb[kb][jj] = pack_b(Vn[2 * kb][jj], Vn[2 * kb + 1][jj]);
-    }
-    // the state update (the dependent chain into the next chunk)
+    for (int tb = 0; tb < 4; tb++) u[tb] = *reinterpret_cast<const h4*>(im + kStU + tb * kBlk + v * 512 + 8 * lane);
+    const float eL = *reinterpret_cast<const float*>(im + kStS);
+    // This wave's part of chunk p + 1 has landed and its reads of chunk p are done; after the barrier both waves'
+    // parts have, and no wave reads chunk p's buffer again before the next period's DMA into it. A bare s_barrier:
+    // __syncthreads() would also wait for the DMAs just issued for later chunks (a workgroup-scope fence waits for every
+    // LDS DMA in flight). The empty asm statements keep the compiler from moving memory accesses across it.
+    __builtin_amdgcn_s_waitcnt(kStWait);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // every period (a conditional read would make wa a merge that waits at once), issued here: the empty asm keeps
+    // the compiler from sinking the reads below the state update
+    read_w(min(p + 1, nchunks - 1));
+    asm volatile("" ::: "memory");
     if (full) {
-      // all sixteen first-block products before any second-block one, so that no MFMA waits for its predecessor
-      const float eL = *reinterpret_cast<const float*>(im + kOffS);
-      h8 kt[8];
+      h8 Vb[2];
+      {
+        f4 Vn[4];
 #pragma unroll
-      for (int ib = 0; ib < 8; ib++) kt[ib] = lds16(im + kOffK + (ib * 2 + 0) * kBlk + lo16);
+        for (int tb = 0; tb < 4; tb++) Vn[tb] = f4{(float)u[tb][0], (float)u[tb][1], (float)u[tb][2], (float)u[tb][3]} - X[tb];
 #pragma unroll
-      for (int ib = 0; ib < 8; ib++)
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) S[ib][jj] = mfma16(kt[ib], Vb[0][jj], S[ib][jj] * eL);
-#pragma unroll
-      for (int ib = 0; ib < 8; ib++) kt[ib] = lds16(im + kOffK + (ib * 2 + 1) * kBlk + lo16);
-#pragma unroll
-      for (int ib = 0; ib < 8; ib++)
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) S[ib][jj] = mfma16(kt[ib], Vb[1][jj], S[ib][jj]);
-    }
-    // o^T += V_new^T Att^T (causal: the second K block only for row blocks 2 and 3)
-#pragma unroll
-    for (int tb = 0; tb < 4; tb++) {
-      const h8 a0 = lds16(im + kOffA + (tb * 2 + 0) * kBlk + lo16);
-#pragma unroll
-      for (int jj = 0; jj < 2; jj++) O[jj][tb] = mfma16(Vb[0][jj], a0, O[jj][tb]);
-      if (tb >= 2) {
-        const h8 a1 = lds16(im + kOffA + (tb * 2 + 1) * kBlk + lo16);
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) O[jj][tb] = mfma16(Vb[1][jj], a1, O[jj][tb]);
+        for (int kb = 0; kb < 2; kb++) Vb[kb] = pack_b(Vn[2 * kb], Vn[2 * kb + 1]);
       }
+#pragma unroll
+      for (int ib = 0; ib < 8; ib++) S[ib] = mfma16(kt[0][ib], Vb[0], S[ib] * eL);
+#pragma unroll
+      for (int ib = 0; ib < 8; ib++) S[ib] = mfma16(kt[1][ib], Vb[1], S[ib]);
     }
-    if (a.gnorm) {
-      // row 16 tb + c16: this wave's 32-column sum of squares (8 values here, 4 lanes c16 + 16 g)
-#pragma unroll
-      for (int tb = 0; tb < 4; tb++) {
-        float v = 0.0f;
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) v = fmaf(O[jj][tb][e], O[jj][tb][e], v);
-        v = sum_col4(v);
-        if (grp == tb) sm.red[(16 * tb + c16) * kCW + w] = v;
-      }
-    }
-    __syncthreads();
-    if (a.gnorm) {
-#pragma unroll
-      for (int tb = 0; tb < 4; tb++) {
-        const f4 r = lds4(&sm.red[(16 * tb + c16) * kCW]);
-        const float iv = rsqrtf(((r[0] + r[1]) + (r[2] + r[3])) / kDV + 1e-6f);
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) O[jj][tb] = O[jj][tb] * iv * zq[tb][jj];
-      }
-    }
-    {
-      __attribute__((address_space(1))) T* ob =
-          gpw<T>(a.out) + (size_t)b * a.L * ostride + (size_t)h * kDV + 32 * w + 4 * grp;
-#pragma unroll
-      for (int tb = 0; tb < 4; tb++) {
-        const int t = 16 * tb + c16, r = c0 + t;
-        if (t < m && r >= a.P) {
-          __attribute__((address_space(1))) T* orow = ob + (size_t)(r - a.P) * ostride;
-          store4(orow, O[0][tb]);
-          store4(orow + 16, O[1][tb]);
-        }
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next image and the next z rows have landed
-#pragma unroll
-    for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-      for (int jj = 0; jj < 2; jj++) zq[tb][jj] = zn[tb][jj];
-    __syncthreads();
   }
 #pragma unroll
   for (int ib = 0; ib < 8; ib++)
 #pragma unroll
+    for (int e = 0; e < 4; e++)
+      gpw<float>(a.S_out)[sbase + (size_t)(16 * ib + 4 * grp0 + e) * kDV + col0 + c160] = S[ib][e];
+}
+
+// gdn_out_kernel: one 4-wave workgroup per (chunk, sequence, head), wave w on value columns 32 w .. + 31: the chunk's
+// image in LDS and the packed state at its start from the state pass; X = W S and the first half of o^T = S^T q~^T
+// from the packed state, V_new = U - X, o^T += V_new^T Att^T, the gated norm and the stores. o is computed transposed
+// (the packed state and V_new serve as A operands with the same permuted K order in which they serve as B operands,
+// and the image blocks of q~ and Att as B operands), so a lane holds 4 consecutive value columns of one row: the gate
+// factors arrive and the outputs leave as 16-byte accesses. The state pass computes X from the same operands in the
+// same order, so V_new here is bit for bit the one the state update used.
+struct OutLds {
+  unsigned char img[kImg];
+  float red[kCH * kCW];  // gated-norm partial sums, [t][wave]
+};
+
+template <typename T>
+__global__ __launch_bounds__(kCT) void gdn_out_kernel(GdnArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[];
+  OutLds& sm = *reinterpret_cast<OutLds*>(lds_raw);
+  const int p = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, grp = lane >> 4, c16 = lane & 15, lo16 = 16 * lane;
+  const int end = a.P + a.L;
+  const int c0 = a.s0 + kCH * p;
+  const int m = min(kCH, end - c0);
+  const char* const src = (const char*)a.img + ((size_t)bh * a.img_chunks + p) * kChunkScratch;
+  for (int i = w; i < kImg / kBlk; i += kCW)
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + kBlk * (size_t)i + 16 * lane),
+                                     (__attribute__((address_space(3))) void*)(sm.img + kBlk * i), 16, 0, 0);
+  h8 Sb[4][2];
+  {
+    const gptr<h8> snap = gp<h8>(src + kOffSnap) + w * 8 * 64 + lane;
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) Sb[kb][jj] = snap[(kb * 2 + jj) * 64];
+  }
+  f4 zq[4][2];
+  if (a.gnorm) {
+    const gptr<float> g = gp<float>(src + kImg) + (size_t)(w * 8) * (kBlk / 4) + 4 * lane;
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) zq[tb][jj] = ld4(g + (size_t)(tb * 2 + jj) * (kBlk / 4));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const unsigned char* im = sm.img;
+
+  f4 X[4][2], O[2][4];
+  const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++) {
+    h8 wa[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) wa[tb] = lds16(im + kOffW + (tb * 4 + kb) * kBlk + lo16);
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) X[tb][jj] = mfma16(wa[tb], Sb[kb][jj], kb ? X[tb][jj] : z4);
+  }
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++) {
+    h8 qa[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) qa[tb] = lds16(im + kOffQ + (tb * 4 + kb) * kBlk + lo16);
+#pragma unroll
     for (int jj = 0; jj < 2; jj++)
 #pragma unroll
-      for (int e = 0; e < 4; e++)
-        gpw<float>(a.S_out)[sbase + (size_t)(16 * ib + 4 * grp0 + e) * kDV + 32 * w + 16 * jj + c160] = S[ib][jj][e];
+      for (int tb = 0; tb < 4; tb++) O[jj][tb] = mfma16(Sb[kb][jj], qa[tb], kb ? O[jj][tb] : z4);
+  }
+  h8 Vb[2][2];
+  {
+    f4 Vn[4][2];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) {
+        const h4 u = *reinterpret_cast<const h4*>(im + kOffU + (tb * 8 + 2 * w + jj) * 512 + 8 * lane);
+        Vn[tb][jj] = f4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]} - X[tb][jj];
+      }
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) Vb[kb][jj] = pack_b(Vn[2 * kb][jj], Vn[2 * kb + 1][jj]);
+  }
+#pragma unroll
+  for (int tb = 0; tb < 4; tb++) {
+    const h8 a0 = lds16(im + kOffA + (tb * 2 + 0) * kBlk + lo16);
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++) O[jj][tb] = mfma16(Vb[0][jj], a0, O[jj][tb]);
+    if (tb >= 2) {
+      const h8 a1 = lds16(im + kOffA + (tb * 2 + 1) * kBlk + lo16);
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) O[jj][tb] = mfma16(Vb[1][jj], a1, O[jj][tb]);
+    }
+  }
+  if (a.gnorm) {
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) {
+      float v = 0.0f;
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) v = fmaf(O[jj][tb][e], O[jj][tb][e], v);
+      v = sum_col4(v);
+      if (grp == tb) sm.red[(16 * tb + c16) * kCW + w] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) {
+      const f4 r = lds4(&sm.red[(16 * tb + c16) * kCW]);
+      const float iv = rsqrtf(((r[0] + r[1]) + (r[2] + r[3])) / kDV + 1e-6f);
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++) O[jj][tb] = O[jj][tb] * iv * zq[tb][jj];
+    }
+  }
+  const int ostride = a.H * kDV;
+  __attribute__((address_space(1))) T* ob = gpw<T>(a.out) + (size_t)b * a.L * ostride + (size_t)h * kDV + 32 * w + 4 * grp;
+#pragma unroll
+  for (int tb = 0; tb < 4; tb++) {
+    const int t = 16 * tb + c16, r = c0 + t;
+    if (t < m && r >= a.P) {
+      __attribute__((address_space(1))) T* orow = ob + (size_t)(r - a.P) * ostride;
+      store4(orow, O[0][tb]);
+      store4(orow + 16, O[1][tb]);
+    }
+  }
 }
 
 template <typename T>
@@ -694,11 +734,17 @@ hipError_t launch(const GdnArgs& a, hipStream_t s) {
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kp, dim3(nchunks, a.B * a.H), dim3(kPT), sizeof(PrepLds), s, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  auto kr = gdn_chain_kernel<T>;
-  e = hipFuncSetAttribute(reinterpret_cast<const void*>(kr), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)sizeof(ChainLds));
+  auto ks = gdn_state_kernel<T>;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(ks), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)sizeof(StateLds));
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kr, dim3(a.B * a.H), dim3(kCT), sizeof(ChainLds), s, a);
+  hipLaunchKernelGGL(ks, dim3(kSG, a.B * a.H), dim3(kSVT), sizeof(StateLds), s, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  auto ko = gdn_out_kernel<T>;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(ko), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)sizeof(OutLds));
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(ko, dim3(nchunks, a.B * a.H), dim3(kCT), sizeof(OutLds), s, a);
   return hipGetLastError();
 }
 

@@ -24,7 +24,7 @@ struct GdnArgs {
   const float* negA;                // [H]
   const float* dtb;                 // [H]
   const float* gnorm;               // [DV], or nullptr to output the raw core output
-  void* img;                        // chunk-image scratch of the two-kernel form: [B][H][img_chunks] images
+  void* img;                        // chunk scratch of the split form: [B][H][img_chunks] images
   int img_chunks;                   // image slots per (sequence, head)
   float* seq_raw;                   // sequential form: raw outputs [B][H][kSegRows][DV] fp32 awaiting the gated norm
   unsigned* seq_cnt;                // sequential form: [B][H] arrival counters (zero between launches)
@@ -78,8 +78,8 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t s);
 // paired form: a producer and a consumer workgroup per (sequence, head), 2*B*H workgroups
 bool gdn_duo_fits(int B, int H);
 hipError_t launch_gdn_duo(const GdnArgs& a, hipStream_t s);
-hipError_t launch_gdn_split(const GdnArgs& a, hipStream_t s);  // chunk-parallel preparation + recurrence
-size_t gdn_split_image_bytes();                                // bytes of one chunk image
+hipError_t launch_gdn_split(const GdnArgs& a, hipStream_t s);  // chunk-parallel preparation, state pass, outputs
+size_t gdn_split_image_bytes();                                // scratch bytes of one chunk
 hipError_t launch_gqa(const GqaArgs& a, hipStream_t s);
 
 // MatMulNBits projection: y[M][N] (f16) = a[M][K] (f16) x W^T, W in packed blocks of 32 (`bits` u32 words each) with

@@ -1,5 +1,5 @@
 """The reference's context cap (engine.js:92,316: LT = 4096) on a one-sequence engine, where the gated-delta layer
-runs the two-kernel chunked form and the GQA layer splits key ranges over workgroups: a 4000-row prefix kept as a
+runs the split chunked form (chunk-parallel preparation and output, a sequential state pass) and the GQA layer splits key ranges over workgroups: a 4000-row prefix kept as a
 snapshot plus a 96-row suffix equals one 4096-row forward bit for bit, both match the fp64 oracle, and one row more
 is refused with HA_ERR_CONTEXT."""
 import numpy as np

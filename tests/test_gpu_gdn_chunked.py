@@ -1,7 +1,7 @@
 """GPU parity of the chunked (MFMA) gated-delta prefill against the fp64 sequential oracle and against the GPU's own
-fp32 sequential kernel, plus bit-exact prefix + suffix for aligned and unaligned splits. Every test runs both
-implementations of the chunked form: the single fused kernel and the two-kernel split (chunk images, then the
-recurrence)."""
+fp32 sequential kernel, plus bit-exact prefix + suffix for aligned and unaligned splits. Every test runs the three
+implementations of the chunked form: the single fused kernel, the split form (chunk images, a sequential state pass,
+then every chunk's outputs at once) and the paired form."""
 import numpy as np
 import pytest
 
@@ -110,3 +110,15 @@ def test_three_way_split_and_decode_steps(mode):
         (o,), s = r.forward([x[:, a:bnd]], cache=s, keep=True, recurrence=mode)
         outs.append(o)
     np.testing.assert_array_equal(np.concatenate(outs, 1), full)
+
+
+@pytest.mark.parametrize("B,form", [(1, ha.CHUNKED_SPLIT), (2, ha.CHUNKED_SPLIT), (4, ha.CHUNKED_PAIRED)])
+def test_default_form_by_shape(B, form):
+    # HA_CHUNKED picks by batch x heads (16 heads here): the split form up to 32 sequence-heads, the paired form above
+    x = gdn_inputs(200, B, seed=12)
+    r = Runner(["linear_attention"], batch=B)
+    r.set_params(0, synth.gdn_params(seed=12))
+    (auto,), sa = r.forward([x], keep=True)
+    (forced,), sf = r.forward([x], keep=True, recurrence=form)
+    np.testing.assert_array_equal(auto, forced)
+    np.testing.assert_array_equal(_state(sa, B), _state(sf, B))

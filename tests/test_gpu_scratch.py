@@ -1,10 +1,11 @@
 """Call-time device buffers held by several engines (ha_share_scratch) and allocated on demand:
-- engines holding one set (a one-sequence and a four-sequence gated-delta engine, each also forced to the two-kernel
-  form, and a one-sequence full-attention engine with split key ranges), called one after another on one stream,
-  give bit for bit what engines with their own sets give, through every form (fused, two-kernel, paired,
-  sequential, split GQA) and again on a second round of calls;
-- neither gated-delta engine's shape picks the two-kernel form, so the chunk images come from the first call that
-  forces it: those outputs also match the fp64 oracle."""
+- engines holding one set (a one-sequence gated-delta engine, also forced to the paired form, a four-sequence one,
+  also forced to the split and fused forms, and a one-sequence full-attention engine with split key ranges), called
+  one after another on one stream, give bit for bit what engines with their own sets give, through every form
+  (split, paired, fused, sequential, split GQA) and again on a second round of calls;
+- the one-sequence shape picks the split form and the four-sequence shape the paired form, so the one-sequence
+  engine's paired tile sets and the four-sequence engine's chunk images come from the first calls that force those
+  forms: the latter's outputs also match the fp64 oracle."""
 import numpy as np
 import pytest
 
@@ -37,8 +38,8 @@ def _calls(lin1, lin4, full):
     q = synth.gqa_rows(300, seed=5).astype(np.float16)
     out = []
     for _ in range(2):
-        out.append(lin1.forward([x1])[0][0])                                # paired form by shape
-        out.append(lin1.forward([x1], recurrence=ha.CHUNKED_SPLIT)[0][0])   # images from a forced call
+        out.append(lin1.forward([x1])[0][0])                                # split form by shape
+        out.append(lin1.forward([x1], recurrence=ha.CHUNKED_PAIRED)[0][0])  # tile sets from a forced call
         out.append(full.forward([q])[0][0])                                 # split key ranges
         out.append(lin4.forward([x4], recurrence=ha.CHUNKED_SPLIT)[0][0])   # images from a forced call
         out.append(lin4.forward([x4[:, :40]], recurrence=ha.SEQUENTIAL)[0][0])
@@ -53,7 +54,7 @@ def test_shared_scratch_is_bit_identical_and_lazy_images_match_the_oracle():
     own, x4 = _calls(*_engines(torch, share=False))
     print("one shared set", flush=True)
     shared, _ = _calls(*_engines(torch, share=True))
-    names = ["paired B=1", "forced split B=1", "GQA split", "forced split B=4", "sequential B=4", "paired B=4",
+    names = ["split B=1", "forced paired B=1", "GQA split", "forced split B=4", "sequential B=4", "paired B=4",
              "fused B=4"] * 2
     for n, a, b in zip(names, own, shared):
         assert np.array_equal(a, b), n
@@ -61,5 +62,5 @@ def test_shared_scratch_is_bit_identical_and_lazy_images_match_the_oracle():
         assert np.array_equal(a, b)
     ref, _ = oracle_gdn(x4, synth.gdn_params(seed=4))
     e = rel_err(own[3], ref)
-    print("forced two-kernel form at B=4 vs fp64: %.2e" % e)
+    print("forced split form at B=4 vs fp64: %.2e" % e)
     assert e < 2e-3
