@@ -73,21 +73,31 @@ constexpr int kPW = 4, kPT = 64 * kPW;
 constexpr int kPRG = 8;  // rows per conv lane
 constexpr int kPG = kPW - 1;
 
+// 80,128 bytes, so that two workgroups share a CU (one's row loads overlap the other's arithmetic). The arrays share
+// storage by lifetime: q^ until Att and q~ are written, then A and T (fp32); k^ and the conv taps until A is formed,
+// then T diag(beta) and T diag(beta e^gc).
 struct PrepLds {
-  _Float16 Qs[kCH * kQP];   // q^ / sqrt(DK), [t][i]
-  _Float16 Ks[kCH * kQP];   // k^, [t][i]
+  union {
+    _Float16 Qs[kCH * kQP];   // q^ / sqrt(DK), [t][i]
+    float Tm[kCH * kAP];      // A, then T (fp32)
+  };
+  union {
+    struct {
+      _Float16 Ks[kCH * kQP];   // k^, [t][i]
+      float cw[12][32][kKC];    // conv taps: channel 4 g + c of q (c < 4), k (4 <= c < 8), v (c >= 8) at cw[c][g]
+    };
+    struct {
+      _Float16 Tb[kCH * kTP];   // T diag(beta), [t][t'] (blocks above the diagonal zero)
+      _Float16 Tw[kCH * kTP];   // T diag(beta e^gc)
+    };
+  };
   _Float16 KT[kDK * kTP];   // k^ transposed, [i][t], swizzled by kt16
   _Float16 VT[kDV * kTP];   // v^ transposed, [j][t], swizzled by vt16
-  _Float16 Tb[kCH * kTP];   // T diag(beta), [t][t'] (blocks above the diagonal zero)
-  _Float16 Tw[kCH * kTP];   // T diag(beta e^gc)
   float eg[kCH], ed[kCH], gc[kCH], rowf[kCH], colf[3][kCH];
   float bt[kCH];            // beta
   float brow[kCH];          // beta_t rowf_t
-  union {
-    float cw[12][32][kKC];  // conv taps: channel 4 g + c of q (c < 4), k (4 <= c < 8), v (c >= 8) at cw[c][g]
-    float Tm[kCH * kAP];    // A, then T (fp32), after the conv
-  };
 };
+static_assert(sizeof(PrepLds) <= 80 * 1024, "two preparation workgroups per CU");
 
 template <typename T>
 __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
@@ -154,14 +164,6 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
     const int lc = i / kKC, j = i % kKC, part = lc >> 7;
     const int ch = part * a.H * kDK + h * kDK + (lc & 127);
     sm.cw[(lc & 3) + 4 * part][(lc & 127) >> 2][j] = gp<float>(a.conv_w)[(size_t)ch * kKC + j];
-  }
-  // blocks above the diagonal of T diag(beta) and T diag(beta e^gc) are read by full 32-wide K blocks and never
-  // written otherwise: row block rb (< 3) has 6 - 2 rb such 8-column groups per row, from column 16 (rb + 1)
-  if (tid0 < 192) {
-    const int k = tid0, rb = k < 96 ? 0 : k < 160 ? 1 : 2, k2 = k - (rb == 0 ? 0 : rb == 1 ? 96 : 160);
-    const int ng = 6 - 2 * rb, t = 16 * rb + k2 / ng, g = k2 % ng + 2 * (rb + 1);
-    *reinterpret_cast<h8*>(sm.Tb + t * kTP + 8 * g) = h8{};
-    *reinterpret_cast<h8*>(sm.Tw + t * kTP + 8 * g) = h8{};
   }
   __syncthreads();  // conv taps visible
 
@@ -241,122 +243,10 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
       sm.colf[i - 1][lane] = lane < 16 * i ? __expf(gi - gcr) : 0.0f;
     }
   }
-  __syncthreads();  // q^, k^, k^T, v^T, gates; the taps are dead (Tm reuses them)
+  __syncthreads();  // q^, k^, k^T, v^T, gates
 
   const int lane = tid0 & 63, grp = lane >> 4, c16 = lane & 15;
-  if (w == kPG) {
-    // the four diagonal blocks of A: k^ k^T (A and B operands are the same rows), beta and decay, strictly lower
-    f4 dg[4];
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-      const _Float16* kr = sm.Ks + (16 * d + c16) * kQP + 8 * grp;
-      dg[d] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ks++) {
-        const h8 kv = *reinterpret_cast<const h8*>(kr + 32 * ks);
-        dg[d] = mfma16(kv, kv, dg[d]);
-      }
-    }
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-      const int tp = 16 * d + c16, t0 = 16 * d + 4 * grp;
-      const float gp_ = sm.gc[tp];
-      const f4 gt = lds4(&sm.gc[t0]), bv = lds4(&sm.bt[t0]);
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int t = t0 + e;
-        const float dec = __expf(fminf(gt[e] - gp_, 0.0f));
-        sm.Tm[t * kAP + tp] = tp < t ? bv[e] * dg[d][e] * dec : 0.0f;
-      }
-    }
-    wave_sync();
-    // lane (grp, c16): column c16 of diagonal block grp, rows in order (left-looking)
-    const int base = 16 * grp;
-    float pc[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float* ar = &sm.Tm[(base + r) * kAP + base];
-      float acc = r == c16 ? 1.0f : 0.0f;
-#pragma unroll
-      for (int j = 0; j < r; j++) acc = fmaf(-ar[j], pc[j], acc);
-      pc[r] = acc;
-    }
-    const float cb = sm.bt[base + c16], cw = cb * sm.eg[base + c16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      sm.Tm[(base + r) * kAP + base + c16] = pc[r];
-      sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cb);
-      sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cw);
-    }
-  } else {
-    // below-diagonal blocks of A: tiles 1,3,4,6,7,8 of the 10 on or below the diagonal, two per wave
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int jt = w == 0 ? (k ? 3 : 1) : w == 1 ? (k ? 6 : 4) : (k ? 8 : 7);
-      const int ti = jt >= 6 ? 3 : jt >= 3 ? 2 : 1, tj = jt - ti * (ti + 1) / 2;
-      const _Float16* ab = sm.Ks + (16 * ti + c16) * kQP + 8 * grp;
-      const _Float16* bb = sm.Ks + (16 * tj + c16) * kQP + 8 * grp;
-      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ks++)
-        acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
-      // e^(gc_t - gc_t') factors into two terms <= 1 below the diagonal blocks
-      const int tp = 16 * tj + c16, t0 = 16 * ti + 4 * grp;
-      const float cf = sm.colf[ti - 1][tp];
-      const f4 bf = lds4(&sm.brow[t0]);
-#pragma unroll
-      for (int e = 0; e < 4; e++) sm.Tm[(t0 + e) * kAP + tp] = acc[e] * bf[e] * cf;
-    }
-  }
-  __syncthreads();
-  if (w == 0)
-    t_column<0, true>(sm, grp, c16);
-  else if (w == 1)
-    t_column<1, true>(sm, grp, c16);
-  else if (w == 2)
-    t_column<2, true>(sm, grp, c16);
-  __syncthreads();  // T diag(beta), T diag(beta e^gc) complete
-
   const int lo16 = 16 * lane;
-  // W^T = k^T (T diag(beta e^gc))^T: tiles (ib, tb), ib in {2w, 2w+1}: lane holds W[16 tb + c16][16 ib + 4 grp + e],
-  // so the tile pair (2w, 2w+1) of one tb is W's A-operand block (tb, kb = w). T is lower triangular: the second
-  // K block (chunk rows 32..63) only contributes to tb >= 2.
-#pragma unroll
-  for (int tb = 0; tb < 4; tb++) {
-    f4 d[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int i = 16 * (2 * w + k) + c16;
-      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        if (kb == 1 && tb < 2) continue;
-        const h8 av = *reinterpret_cast<const h8*>(sm.KT + kt16(i, 4 * kb + grp));
-        const h8 bv = *reinterpret_cast<const h8*>(sm.Tw + (16 * tb + c16) * kTP + 32 * kb + 8 * grp);
-        acc = mfma16(av, bv, acc);
-      }
-      d[k] = acc;
-    }
-    img.st16(kOffW + (tb * 4 + w) * kBlk + lo16, join(d[0], d[1]));
-  }
-  // U = T diag(beta) v^: tiles (tb, jt), jt in {2w, 2w+1}, in the D layout
-#pragma unroll
-  for (int tb = 0; tb < 4; tb++) {
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int jt = 2 * w + k;
-      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        if (kb == 1 && tb < 2) continue;
-        const h8 av = *reinterpret_cast<const h8*>(sm.Tb + (16 * tb + c16) * kTP + 32 * kb + 8 * grp);
-        const h8 bv = *reinterpret_cast<const h8*>(sm.VT + vt16(16 * jt + c16, 4 * kb + grp));
-        acc = mfma16(av, bv, acc);
-      }
-      img.st8(kOffU + (tb * 8 + jt) * 512 + 8 * lane,
-              h4{(_Float16)acc[0], (_Float16)acc[1], (_Float16)acc[2], (_Float16)acc[3]});
-    }
-  }
   // Att^T = k^ q^T, decay-masked: tile (a, tb) holds Att[16 tb + c16][16 a + 4 grp + e]; Att block (tb, kb) is the
   // tile pair a = 2 kb, 2 kb + 1 (a tile above the diagonal, a > tb, is zero). The six blocks that are read:
   // wave 0: (0,0) and (2,1); wave 1: (1,0); wave 2: (2,0); wave 3: (3,0) and (3,1).
@@ -404,6 +294,129 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; e++) o[e] = (_Float16)((float)q[e] * eg);
       img.st16(kOffQ + (w * 4 + kb) * kBlk + lo16, o);
+    }
+  }
+  __syncthreads();  // q^ is dead: A and T reuse its storage
+  if (w == kPG) {
+    // the four diagonal blocks of A: k^ k^T (A and B operands are the same rows), beta and decay, strictly lower
+    f4 dg[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      const _Float16* kr = sm.Ks + (16 * d + c16) * kQP + 8 * grp;
+      dg[d] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) {
+        const h8 kv = *reinterpret_cast<const h8*>(kr + 32 * ks);
+        dg[d] = mfma16(kv, kv, dg[d]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      const int tp = 16 * d + c16, t0 = 16 * d + 4 * grp;
+      const float gp_ = sm.gc[tp];
+      const f4 gt = lds4(&sm.gc[t0]), bv = lds4(&sm.bt[t0]);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int t = t0 + e;
+        const float dec = __expf(fminf(gt[e] - gp_, 0.0f));
+        sm.Tm[t * kAP + tp] = tp < t ? bv[e] * dg[d][e] * dec : 0.0f;
+      }
+    }
+  } else {
+    // below-diagonal blocks of A: tiles 1,3,4,6,7,8 of the 10 on or below the diagonal, two per wave
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int jt = w == 0 ? (k ? 3 : 1) : w == 1 ? (k ? 6 : 4) : (k ? 8 : 7);
+      const int ti = jt >= 6 ? 3 : jt >= 3 ? 2 : 1, tj = jt - ti * (ti + 1) / 2;
+      const _Float16* ab = sm.Ks + (16 * ti + c16) * kQP + 8 * grp;
+      const _Float16* bb = sm.Ks + (16 * tj + c16) * kQP + 8 * grp;
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++)
+        acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
+      // e^(gc_t - gc_t') factors into two terms <= 1 below the diagonal blocks
+      const int tp = 16 * tj + c16, t0 = 16 * ti + 4 * grp;
+      const float cf = sm.colf[ti - 1][tp];
+      const f4 bf = lds4(&sm.brow[t0]);
+#pragma unroll
+      for (int e = 0; e < 4; e++) sm.Tm[(t0 + e) * kAP + tp] = acc[e] * bf[e] * cf;
+    }
+  }
+  __syncthreads();  // A complete; k^ and the taps are dead: T diag(beta), T diag(beta e^gc) reuse their storage
+  // blocks above the diagonal of T diag(beta) and T diag(beta e^gc) are read by full 32-wide K blocks and never
+  // written otherwise: row block rb (< 3) has 6 - 2 rb such 8-column groups per row, from column 16 (rb + 1)
+  if (tid0 < 192) {
+    const int k = tid0, rb = k < 96 ? 0 : k < 160 ? 1 : 2, k2 = k - (rb == 0 ? 0 : rb == 1 ? 96 : 160);
+    const int ng = 6 - 2 * rb, t = 16 * rb + k2 / ng, g = k2 % ng + 2 * (rb + 1);
+    *reinterpret_cast<h8*>(sm.Tb + t * kTP + 8 * g) = h8{};
+    *reinterpret_cast<h8*>(sm.Tw + t * kTP + 8 * g) = h8{};
+  }
+  if (w == kPG) {
+    // lane (grp, c16): column c16 of diagonal block grp, rows in order (left-looking)
+    const int base = 16 * grp;
+    float pc[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float* ar = &sm.Tm[(base + r) * kAP + base];
+      float acc = r == c16 ? 1.0f : 0.0f;
+#pragma unroll
+      for (int j = 0; j < r; j++) acc = fmaf(-ar[j], pc[j], acc);
+      pc[r] = acc;
+    }
+    const float cb = sm.bt[base + c16], cw = cb * sm.eg[base + c16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      sm.Tm[(base + r) * kAP + base + c16] = pc[r];
+      sm.Tb[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cb);
+      sm.Tw[(base + r) * kTP + base + c16] = (_Float16)(pc[r] * cw);
+    }
+  }
+  __syncthreads();
+  if (w == 0)
+    t_column<0, true>(sm, grp, c16);
+  else if (w == 1)
+    t_column<1, true>(sm, grp, c16);
+  else if (w == 2)
+    t_column<2, true>(sm, grp, c16);
+  __syncthreads();  // T diag(beta), T diag(beta e^gc) complete
+
+  // W^T = k^T (T diag(beta e^gc))^T: tiles (ib, tb), ib in {2w, 2w+1}: lane holds W[16 tb + c16][16 ib + 4 grp + e],
+  // so the tile pair (2w, 2w+1) of one tb is W's A-operand block (tb, kb = w). T is lower triangular: the second
+  // K block (chunk rows 32..63) only contributes to tb >= 2.
+#pragma unroll
+  for (int tb = 0; tb < 4; tb++) {
+    f4 d[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int i = 16 * (2 * w + k) + c16;
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        if (kb == 1 && tb < 2) continue;
+        const h8 av = *reinterpret_cast<const h8*>(sm.KT + kt16(i, 4 * kb + grp));
+        const h8 bv = *reinterpret_cast<const h8*>(sm.Tw + (16 * tb + c16) * kTP + 32 * kb + 8 * grp);
+        acc = mfma16(av, bv, acc);
+      }
+      d[k] = acc;
+    }
+    img.st16(kOffW + (tb * 4 + w) * kBlk + lo16, join(d[0], d[1]));
+  }
+  // U = T diag(beta) v^: tiles (tb, jt), jt in {2w, 2w+1}, in the D layout
+#pragma unroll
+  for (int tb = 0; tb < 4; tb++) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int jt = 2 * w + k;
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        if (kb == 1 && tb < 2) continue;
+        const h8 av = *reinterpret_cast<const h8*>(sm.Tb + (16 * tb + c16) * kTP + 32 * kb + 8 * grp);
+        const h8 bv = *reinterpret_cast<const h8*>(sm.VT + vt16(16 * jt + c16, 4 * kb + grp));
+        acc = mfma16(av, bv, acc);
+      }
+      img.st8(kOffU + (tb * 8 + jt) * 512 + 8 * lane,
+              h4{(_Float16)acc[0], (_Float16)acc[1], (_Float16)acc[2], (_Float16)acc[3]});
     }
   }
   // K~^T blocks (ib in {2w, 2w+1}, kb 0..1): k^ columns with chunk row t scaled by e^(gc_63 - gc_t)
