@@ -61,9 +61,9 @@ typedef enum ha_recurrence {
                             the fused kernel beyond) */
   HA_SEQUENTIAL = 1,     /* token-by-token fp32 rule with the state in registers (decode / resume) */
   HA_CHUNKED_FUSED = 2,  /* the chunked form in one kernel per layer: one workgroup per (sequence, head), 64-row chunks */
-  HA_CHUNKED_SPLIT = 3,  /* the chunked form in three kernels, 64-row chunks: every chunk's state-independent part at
-                            once, the state alone through the chunks (four workgroups per (sequence, head)), then
-                            every chunk's outputs at once */
+  HA_CHUNKED_SPLIT = 3,  /* the chunked form in two launches, 64-row chunks: every chunk's state-independent part at
+                            once, then the state alone through the chunks (four workgroups per (sequence, head))
+                            with every chunk's outputs on the other CUs as soon as its state is known */
   HA_CHUNKED_PAIRED = 4  /* the chunked form on two workgroups per (sequence, head), 32-row chunks: one prepares the
                             chunks' tiles, the other runs the recurrence (B*H a multiple of 8, at most 128) */
 } ha_recurrence;

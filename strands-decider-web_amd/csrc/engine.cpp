@@ -83,11 +83,11 @@ struct Scratch {
     size_t bytes = 0;
   };
   int device = 0;
-  Buf img, seq_raw, seq_cnt, gqa_part, zeros, duo_ring, duo_flags;
-  unsigned duo_epoch = 0;  // the paired form's counter epoch of the last launch (the counters start at zero)
+  Buf img, seq_raw, seq_cnt, gqa_part, zeros, duo_ring, sync_flags;
+  unsigned sync_epoch = 0;  // the progress counters' epoch of the last launch that used them (they start at zero)
   ~Scratch() {
     (void)hipSetDevice(device);
-    for (Buf* b : {&img, &seq_raw, &seq_cnt, &gqa_part, &zeros, &duo_ring, &duo_flags})
+    for (Buf* b : {&img, &seq_raw, &seq_cnt, &gqa_part, &zeros, &duo_ring, &sync_flags})
       if (b->p) (void)hipFree(b->p);
   }
 };
@@ -125,7 +125,7 @@ struct ha_engine {
   // form's raw outputs [B][H][kSegRows][DV] and counters [B][H], split-GQA partials [gqa_part_slots]
   std::shared_ptr<Scratch> scratch;
   size_t need_zeros = 0, need_img = 0, need_seq_raw = 0, need_seq_cnt = 0, need_gqa = 0, need_duo_ring = 0,
-         need_duo_flags = 0;
+         need_sync_flags = 0;
   int img_chunks = 0, duo_slots = 0;
   int gqa_split = 0, gqa_part_slots = 0;
   hipEvent_t ev[2] = {nullptr, nullptr};
@@ -172,7 +172,7 @@ const ha_engine* snapshot_owner(const ha_snapshot* s) {
 // three-kernel form (every chunk's preparation and output work spread over the chip, only the state pass sequential)
 // up to 32 sequence-heads, the paired form above that while its two workgroups per recurrence fit the 256 CUs in one
 // round (B*H a multiple of 8, at most 128), the fused kernel beyond. Measured per layer at T = 2048, 18 forwards back
-// to back (split / paired / fused, us): B=1 79 / 175 / -, B=2 127 / 176 / -, B=4 249 / 196 / -, B=8 - / 271 / 303,
+// to back (split / paired / fused, us): B=1 71 / 175 / -, B=2 122 / 176 / -, B=4 252 / 196 / -, B=8 - / 271 / 303,
 // B=16 - / - / 350.
 bool split_by_shape(const ha_config& c) { return c.batch * c.H <= 32; }
 bool paired_by_shape(const ha_config& c) { return !split_by_shape(c) && ha::gdn_duo_fits(c.batch, c.H); }
@@ -351,12 +351,11 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
     // only where HA_CHUNKED picks that form
     e->duo_slots = (c.max_ctx + 31) / 32;
     e->need_duo_ring = (size_t)e->duo_slots * ha::kDuoSetBytes * B * c.H;
-    e->need_duo_flags = sizeof(unsigned) * 64 * B * c.H;
+    e->need_sync_flags = sizeof(unsigned) * 64 * B * c.H;
     if ((rc = grow(e->scratch->zeros, e->need_zeros)) || (rc = grow(e->scratch->seq_raw, e->need_seq_raw)) ||
-        (rc = grow(e->scratch->seq_cnt, e->need_seq_cnt)) ||
+        (rc = grow(e->scratch->seq_cnt, e->need_seq_cnt)) || (rc = grow(e->scratch->sync_flags, e->need_sync_flags)) ||
         (split_by_shape(c) && (rc = grow(e->scratch->img, e->need_img))) ||
-        (paired_by_shape(c) && ((rc = grow(e->scratch->duo_ring, e->need_duo_ring)) ||
-                                (rc = grow(e->scratch->duo_flags, e->need_duo_flags)))))
+        (paired_by_shape(c) && (rc = grow(e->scratch->duo_ring, e->need_duo_ring))))
       return bail(rc);
   }
   if (e->any_full) {
@@ -415,7 +414,7 @@ int ha_share_scratch(ha_engine* e, ha_engine* holder) {
       (rc = grow(to.seq_raw, e->need_seq_raw)) ||
       (rc = grow(to.seq_cnt, e->need_seq_cnt)) || (rc = grow(to.gqa_part, e->need_gqa)) ||
       (rc = grow(to.duo_ring, from.duo_ring.bytes ? e->need_duo_ring : 0)) ||
-      (rc = grow(to.duo_flags, from.duo_flags.bytes ? e->need_duo_flags : 0)))
+      (rc = grow(to.sync_flags, e->need_sync_flags)))
     return rc;
   e->scratch = holder->scratch;
   return HA_OK;
@@ -508,9 +507,9 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
     int rc = grow(sc.img, e->need_img);  // first call that forces the split form on a larger shape
     if (rc) return rc;
   }
-  if (e->any_linear && chunked && paired && (sc.duo_ring.bytes < e->need_duo_ring || sc.duo_flags.bytes < e->need_duo_flags)) {
+  if (e->any_linear && chunked && paired && sc.duo_ring.bytes < e->need_duo_ring) {
     int rc;  // first call that forces the paired form on another shape
-    if ((rc = grow(sc.duo_ring, e->need_duo_ring)) || (rc = grow(sc.duo_flags, e->need_duo_flags))) return rc;
+    if ((rc = grow(sc.duo_ring, e->need_duo_ring))) return rc;
   }
   // raw-row tails: the copy reads only the call's input rows and the resumed tail, so the layers' copies are
   // gathered into one launch after the mixers (per layer when per-layer times are asked for, so that each layer's
@@ -543,18 +542,16 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       hipError_t he;
       if (!chunked) {
         he = ha::launch_gdn_sequential(a, st);
-      } else if (split) {
-        he = ha::launch_gdn_split(a, st);
-      } else if (paired) {
-        // a fresh counter epoch per launch; before the epoch field runs out, the counters are cleared
-        if (sc.duo_epoch + 1 >= (1u << (32 - ha::kDuoEpochShift))) {
+      } else if (split || paired) {
+        // a fresh progress-counter epoch per launch; before the epoch field runs out, the counters are cleared
+        if (sc.sync_epoch + 1 >= (1u << (32 - ha::kDuoEpochShift))) {
           HA_HIP(hipStreamSynchronize(st));
-          HA_HIP(hipMemset(sc.duo_flags.p, 0, sc.duo_flags.bytes));
-          sc.duo_epoch = 0;
+          HA_HIP(hipMemset(sc.sync_flags.p, 0, sc.sync_flags.bytes));
+          sc.sync_epoch = 0;
         }
+        a.sync_flags = static_cast<unsigned*>(sc.sync_flags.p); a.sync_epoch = ++sc.sync_epoch;
         a.duo_ring = sc.duo_ring.p; a.duo_slots = e->duo_slots;
-        a.duo_flags = static_cast<unsigned*>(sc.duo_flags.p); a.duo_epoch = ++sc.duo_epoch;
-        he = ha::launch_gdn_duo(a, st);
+        he = split ? ha::launch_gdn_split(a, st) : ha::launch_gdn_duo(a, st);
       } else {
         he = ha::launch_gdn_chunked(a, st);
       }

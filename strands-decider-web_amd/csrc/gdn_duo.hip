@@ -721,10 +721,10 @@ __global__ __launch_bounds__(kThreads) void gdn_duo_kernel(GdnArgs a) {
   const int blk = blockIdx.x;
   const int pair = (blk >> 4) * 8 + (blk & 7);
   const int b = pair / a.H, h = pair % a.H;
-  unsigned* const produced = a.duo_flags + (size_t)pair * 64;  // each counter on its own 128-byte line
+  unsigned* const produced = a.sync_flags + (size_t)pair * 64;  // each counter on its own 128-byte line
   unsigned* const consumed = produced + 32;
   char* const ring = (char*)a.duo_ring + (size_t)pair * a.duo_slots * kDuoSetBytes;
-  const unsigned ep = a.duo_epoch << kDuoEpochShift;
+  const unsigned ep = a.sync_epoch << kDuoEpochShift;
   if ((blk >> 3) & 1)
     consume<T>(a, b, h, *reinterpret_cast<ConsumerLds*>(lds_raw), ring, produced, consumed, ep);
   else
@@ -748,9 +748,9 @@ bool gdn_duo_fits(int B, int H) { return (B * H) % 8 == 0 && 2 * B * H <= 256; }
 hipError_t launch_gdn_duo(const GdnArgs& a, hipStream_t s) {
   if (a.DK != kDK || a.DV != kDV || a.KC != kKC) return hipErrorInvalidValue;
   if (a.P - a.s0 >= 64 || a.P < a.s0) return hipErrorInvalidValue;  // at most one open 64-row span is replayed
-  if (!gdn_duo_fits(a.B, a.H) || !a.duo_ring || !a.duo_flags) return hipErrorInvalidValue;
+  if (!gdn_duo_fits(a.B, a.H) || !a.duo_ring || !a.sync_flags) return hipErrorInvalidValue;
   const int n = (a.P + a.L - a.s0 + kC - 1) / kC;  // chunks of the call: one slot each, and the counters' chunk field
-  if (n > a.duo_slots || n + 2 >= (1 << kDuoEpochShift) || a.duo_epoch >= (1u << (32 - kDuoEpochShift)))
+  if (n > a.duo_slots || n + 2 >= (1 << kDuoEpochShift) || a.sync_epoch >= (1u << (32 - kDuoEpochShift)))
     return hipErrorInvalidValue;
   return a.dtype == 0 ? launch<float>(a, s) : launch<_Float16>(a, s);
 }

@@ -13,11 +13,12 @@
 //                    writes each chunk's "image": the MFMA A operands q~ = diag(e^gc) q^, W, K~^T and Att and the
 //                    matrix U, every operand block in lane order (64 lanes x 16 bytes), so that the later kernels read
 //                    each with one conflict-free 16-byte LDS load and no lane moves;
-//   gdn_state_kernel carries the state through the chunks in order: four workgroups per (sequence, head) on 32 value
-//                    columns each, X = W S -> V_new -> S <- e^(gc_63) S + K~^T V_new per chunk, and leaves the packed
-//                    state at every chunk's start in that chunk's scratch;
-//   gdn_out_kernel   runs every chunk's outputs at once from its image and that packed state: o^T = S^T q~^T +
-//                    V_new^T Att^T, the gated norm (GNORM), the stores.
+//   gdn_scan_kernel  runs two roles in one launch. The state pass carries the state through the chunks in order
+//                    (four workgroups per (sequence, head) on 32 value columns each, X = W S -> V_new ->
+//                    S <- e^(gc_63) S + K~^T V_new per chunk) and leaves the packed state at every chunk's start in
+//                    that chunk's scratch. The output pass, one workgroup per (chunk, sequence, head) on the other
+//                    CUs, takes each chunk as soon as its packed state is published: o^T = S^T q~^T + V_new^T Att^T,
+//                    the gated norm (GNORM), the stores.
 
 #include <stddef.h>
 
@@ -467,9 +468,24 @@ __device__ __forceinline__ float sum_col4(float x) {
 }
 
 // The sequential part is the state pass alone: per chunk four K blocks of MFMA products per wave, spread over four
-// CUs per (sequence, head). The output work runs afterwards on the whole chip.
+// CUs per (sequence, head). The output work runs on every other CU in the same launch (gdn_scan_kernel), each chunk
+// as soon as the state pass has published the packed state at its start.
+//
+// Publication: the state pass stores the packed states with device-coherent (sc1) stores; its period-end wait, which
+// counts in issue order, proves a period's stores complete kStBufs - 2 periods later, and the workgroup then stores
+// its progress counter (epoch << kDuoEpochShift | chunks published) with a device-scope atomic store. An output
+// workgroup waits for the four counters of its (sequence, head) and reads the packed state with sc1 loads. State
+// workgroups come first in the grid, so the dispatcher places every one of them before any output workgroup of its
+// XCD: an output workgroup only ever waits for state workgroups that are resident or done, and every wait is bounded.
+__device__ __forceinline__ unsigned ld_counter(const unsigned* c) {
+  return __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_counter(unsigned* c, unsigned v) {
+  __hip_atomic_store(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kCacheSc1 = 16;  // cache-policy operand of buffer and LDS-DMA instructions: device-coherent (sc1)
 
-// gdn_state_kernel: kSG workgroups per (sequence, head), workgroup g on value columns 32 g .. + 31, its two waves on
+// The state pass: kSG workgroups per (sequence, head), workgroup g on value columns 32 g .. + 31, its two waves on
 // 16 columns each (wave v: columns 32 g + 16 v + c16), so that a head's products spread over kSG CUs; each wave
 // reads the whole of W and K~^T every chunk, which with more waves per CU would make LDS reads the bound. Each chunk's
 // W and K~^T (image blocks 16..47), the workgroup's 32 columns of U (one 1 KiB block per row block) and e^(gc_63),
@@ -493,11 +509,12 @@ struct StateLds {
 };
 
 template <typename T>
-__global__ __launch_bounds__(kSVT) void gdn_state_kernel(GdnArgs a) {
-  extern __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[];
+__device__ __forceinline__ void state_pass(const GdnArgs& a, unsigned char* lds_raw, int g, int bh) {
   StateLds& sm = *reinterpret_cast<StateLds*>(lds_raw);
-  const int g = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int b = bh / a.H, h = bh % a.H;
   const int tid0 = threadIdx.x, v = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  unsigned* const progress = a.sync_flags + (size_t)bh * 64 + 16 * g;
+  const unsigned ep = a.sync_epoch << kDuoEpochShift;
   const int end = a.P + a.L;
   const int nchunks = (a.L + (a.P - a.s0) + kCH - 1) / kCH;
   char* const imgs = (char*)a.img + (size_t)bh * a.img_chunks * kChunkScratch;
@@ -557,9 +574,12 @@ __global__ __launch_bounds__(kSVT) void gdn_state_kernel(GdnArgs a) {
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) Sb[kb] = pack_b(S[2 * kb], S[2 * kb + 1]);
     {
-      __attribute__((address_space(1))) h8* snap = gpw<h8>(imgs + (size_t)p * kChunkScratch + kOffSnap) + lane;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(imgs + (size_t)p * kChunkScratch + kOffSnap, 0, kSnap, 0x00020000);
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++) snap[((g * 4 + kb) * 2 + v) * 64] = Sb[kb];
+      for (int kb = 0; kb < 4; kb++)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, Sb[kb]), rs, (((g * 4 + kb) * 2 + v) * 64 + lane) * 16,
+                                               0, kCacheSc1);
     }
     h8 kt[2][8];
 #pragma unroll
@@ -584,6 +604,8 @@ __global__ __launch_bounds__(kSVT) void gdn_state_kernel(GdnArgs a) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    // the wait also covered both waves' packed-state stores of periods up to p - (kStBufs - 1)
+    if (tid0 == 0 && p >= kStBufs - 1) st_counter(progress, ep + (unsigned)(p - (kStBufs - 2)));
     // every period (a conditional read would make wa a merge that waits at once), issued here: the empty asm keeps
     // the compiler from sinking the reads below the state update
     read_w(min(p + 1, nchunks - 1));
@@ -603,6 +625,12 @@ __global__ __launch_bounds__(kSVT) void gdn_state_kernel(GdnArgs a) {
       for (int ib = 0; ib < 8; ib++) S[ib] = mfma16(kt[1][ib], Vb[1], S[ib]);
     }
   }
+  // every packed state stored: publish them all
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  if (tid0 == 0) st_counter(progress, ep + (unsigned)nchunks);
 #pragma unroll
   for (int ib = 0; ib < 8; ib++)
 #pragma unroll
@@ -610,7 +638,7 @@ __global__ __launch_bounds__(kSVT) void gdn_state_kernel(GdnArgs a) {
       gpw<float>(a.S_out)[sbase + (size_t)(16 * ib + 4 * grp0 + e) * kDV + col0 + c160] = S[ib][e];
 }
 
-// gdn_out_kernel: one 4-wave workgroup per (chunk, sequence, head), wave w on value columns 32 w .. + 31: the chunk's
+// The output pass: one 4-wave workgroup per (chunk, sequence, head), wave w on value columns 32 w .. + 31: the chunk's
 // image in LDS and the packed state at its start from the state pass; X = W S and the first half of o^T = S^T q~^T
 // from the packed state, V_new = U - X, o^T += V_new^T Att^T, the gated norm and the stores. o is computed transposed
 // (the packed state and V_new serve as A operands with the same permuted K order in which they serve as B operands,
@@ -623,10 +651,9 @@ struct OutLds {
 };
 
 template <typename T>
-__global__ __launch_bounds__(kCT) void gdn_out_kernel(GdnArgs a) {
-  extern __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[];
+__device__ __forceinline__ void out_pass(const GdnArgs& a, unsigned char* lds_raw, int p, int bh) {
   OutLds& sm = *reinterpret_cast<OutLds*>(lds_raw);
-  const int p = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int b = bh / a.H, h = bh % a.H;
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, grp = lane >> 4, c16 = lane & 15, lo16 = 16 * lane;
   const int end = a.P + a.L;
@@ -636,14 +663,6 @@ __global__ __launch_bounds__(kCT) void gdn_out_kernel(GdnArgs a) {
   for (int i = w; i < kImg / kBlk; i += kCW)
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + kBlk * (size_t)i + 16 * lane),
                                      (__attribute__((address_space(3))) void*)(sm.img + kBlk * i), 16, 0, 0);
-  h8 Sb[4][2];
-  {
-    const gptr<h8> snap = gp<h8>(src + kOffSnap) + w * 8 * 64 + lane;
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-      for (int jj = 0; jj < 2; jj++) Sb[kb][jj] = snap[(kb * 2 + jj) * 64];
-  }
   f4 zq[4][2];
   if (a.gnorm) {
     const gptr<float> g = gp<float>(src + kImg) + (size_t)(w * 8) * (kBlk / 4) + 4 * lane;
@@ -651,6 +670,24 @@ __global__ __launch_bounds__(kCT) void gdn_out_kernel(GdnArgs a) {
     for (int tb = 0; tb < 4; tb++)
 #pragma unroll
       for (int jj = 0; jj < 2; jj++) zq[tb][jj] = ld4(g + (size_t)(tb * 2 + jj) * (kBlk / 4));
+  }
+  // the packed state at the chunk's start, once the four state workgroups of this (sequence, head) have published it
+  // (at most 2^16 polls of about a microsecond: they are resident or done, so the wait ends)
+  if (tid == 0) {
+    const unsigned want = (a.sync_epoch << kDuoEpochShift) + (unsigned)(p + 1);
+    const unsigned* progress = a.sync_flags + (size_t)bh * 64;
+    for (int g = 0; g < kSG; g++)
+      for (int i = 0; i < (1 << 16) && ld_counter(progress + 16 * g) < want; i++) __builtin_amdgcn_s_sleep(2);
+  }
+  __syncthreads();
+  h8 Sb[4][2];
+  {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(src) + kOffSnap, 0, kSnap, 0x00020000);
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int jj = 0; jj < 2; jj++)
+        Sb[kb][jj] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, (((w * 4 + kb) * 2 + jj) * 64 + lane) * 16, 0, kCacheSc1));
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -737,6 +774,21 @@ __global__ __launch_bounds__(kCT) void gdn_out_kernel(GdnArgs a) {
   }
 }
 
+// Block i < kSG * B * H: the state pass of (sequence, head) i / kSG, value columns 32 (i % kSG) ..; then one block per
+// (chunk, sequence, head), chunk-major, for the outputs.
+constexpr size_t kScanLds = sizeof(StateLds) > sizeof(OutLds) ? sizeof(StateLds) : sizeof(OutLds);
+template <typename T>
+__global__ __launch_bounds__(kCT) void gdn_scan_kernel(GdnArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[];
+  const int bhn = a.B * a.H, nst = kSG * bhn, id = blockIdx.x;
+  if (id < nst) {
+    if (threadIdx.x >= kSVT) return;  // two waves (a barrier waits only for the waves still running)
+    state_pass<T>(a, lds_raw, id % kSG, id / kSG);
+  } else {
+    out_pass<T>(a, lds_raw, (id - nst) / bhn, (id - nst) % bhn);
+  }
+}
+
 template <typename T>
 hipError_t launch(const GdnArgs& a, hipStream_t s) {
   const int nchunks = (a.L + (a.P - a.s0) + kCH - 1) / kCH;
@@ -747,17 +799,10 @@ hipError_t launch(const GdnArgs& a, hipStream_t s) {
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kp, dim3(nchunks, a.B * a.H), dim3(kPT), sizeof(PrepLds), s, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  auto ks = gdn_state_kernel<T>;
-  e = hipFuncSetAttribute(reinterpret_cast<const void*>(ks), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)sizeof(StateLds));
+  auto kc = gdn_scan_kernel<T>;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(kc), hipFuncAttributeMaxDynamicSharedMemorySize, (int)kScanLds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(ks, dim3(kSG, a.B * a.H), dim3(kSVT), sizeof(StateLds), s, a);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  auto ko = gdn_out_kernel<T>;
-  e = hipFuncSetAttribute(reinterpret_cast<const void*>(ko), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)sizeof(OutLds));
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(ko, dim3(nchunks, a.B * a.H), dim3(kCT), sizeof(OutLds), s, a);
+  hipLaunchKernelGGL(kc, dim3((kSG + nchunks) * a.B * a.H), dim3(kCT), kScanLds, s, a);
   return hipGetLastError();
 }
 
@@ -768,6 +813,8 @@ size_t gdn_split_image_bytes() { return (size_t)kChunkScratch; }
 hipError_t launch_gdn_split(const GdnArgs& a, hipStream_t s) {
   if (a.DK != kDK || a.DV != kDV || a.KC != kKC || !a.img) return hipErrorInvalidValue;
   if (a.P - a.s0 >= kCH || a.P < a.s0) return hipErrorInvalidValue;  // at most one open chunk is replayed
+  if (!a.sync_flags || a.sync_epoch == 0 || a.sync_epoch >= (1u << (32 - kDuoEpochShift))) return hipErrorInvalidValue;
+  if ((a.L + (a.P - a.s0) + kCH - 1) / kCH + 1 >= (1 << kDuoEpochShift)) return hipErrorInvalidValue;
   return a.dtype == 0 ? launch<float>(a, s) : launch<_Float16>(a, s);
 }
 

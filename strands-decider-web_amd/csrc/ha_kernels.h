@@ -30,12 +30,13 @@ struct GdnArgs {
   unsigned* seq_cnt;                // sequential form: [B][H] arrival counters (zero between launches)
   void* duo_ring;                   // paired form: [B*H][duo_slots] tile-set slots of kDuoSetBytes, one per chunk
   int duo_slots;                    // paired form: slots per (sequence, head), at least the call's 32-row chunks
-  unsigned* duo_flags;              // paired form: [B*H][64] progress counters (produced at 0, consumed at 32)
-  unsigned duo_epoch;               // paired form: this launch's counter epoch, >= 1 and increasing per flag buffer
+  unsigned* sync_flags;             // [B*H][64] progress counters between workgroups of one launch: paired form (produced
+                                    // at 0, consumed at 32), split form (the state pass's workgroup g at 16 g)
+  unsigned sync_epoch;              // this launch's counter epoch, >= 1 and increasing per flag buffer
 };
 constexpr int kSegRows = 64;        // output rows per launch of the sequential form
 constexpr int kDuoSetBytes = 36 * 1024;   // bytes per tile-set slot of the paired form
-constexpr int kDuoEpochShift = 12;        // paired-form counter value: epoch << kDuoEpochShift | chunks (< 4096)
+constexpr int kDuoEpochShift = 12;        // progress counter value: epoch << kDuoEpochShift | chunks (< 4096)
 
 // Full-attention prep (q/k RMSNorm, partial RoPE, K/V cache write) and attention for rows [P, P + L).
 struct GqaArgs {
