@@ -85,6 +85,7 @@ struct Scratch {
   int device = 0;
   Buf img, seq_raw, seq_cnt, gqa_part, zeros, duo_ring, sync_flags;
   unsigned sync_epoch = 0;  // the progress counters' epoch of the last launch that used them (they start at zero)
+  unsigned gqa_epoch = 0;   // the split-GQA slot marks' epoch of the last launch (the marks start at zero)
   ~Scratch() {
     (void)hipSetDevice(device);
     for (Buf* b : {&img, &seq_raw, &seq_cnt, &gqa_part, &zeros, &duo_ring, &sync_flags})
@@ -568,6 +569,15 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.in = layer_in[i]; a.out = layer_out[i]; a.qw = l.qn; a.kw = l.kn; a.rope = e->rope;
       a.K = l.K; a.V = l.V;
       a.split = e->gqa_split; a.part_slots = e->gqa_part_slots; a.part = static_cast<float*>(sc.gqa_part.p);
+      if (a.split > 0) {
+        // a fresh mark per launch; if the counter wraps, the marks (and partials) are cleared first
+        if (++sc.gqa_epoch == 0) {
+          HA_HIP(hipStreamSynchronize(st));
+          HA_HIP(hipMemset(sc.gqa_part.p, 0, sc.gqa_part.bytes));
+          sc.gqa_epoch = 1;
+        }
+        a.epoch = sc.gqa_epoch;
+      }
       hipError_t he = ha::launch_gqa(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " attention launch: " + hipGetErrorString(he));
     }  // HA_ADAPTER: no token mixer, nothing to run

@@ -203,8 +203,114 @@ inline int host_ntiles(const GqaArgs& a, int qb) { return std::min(a.P + qb * 64
 constexpr int kRows = 64;     // query rows per workgroup
 constexpr int kWaves = 8;
 
+// Split key ranges in one launch: a piece stores its partial results with device-coherent (sc1) stores, waits for
+// them, and marks its slot with the launch's epoch (a device-scope atomic store); the merge workgroups, which come
+// after every piece in the grid, wait for the marks of their block's pieces and read the partials with sc1 loads.
+// Each XCD dispatches its blocks in order, so it starts merge workgroups only once all of its pieces are out:
+// pieces never wait, so every mark is eventually written, and each wait is bounded besides.
+constexpr int kCacheSc1 = 16;  // cache-policy operand of buffer instructions: device-coherent (sc1)
+typedef int i4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ unsigned* part_marks(const GqaArgs& a) {
+  return reinterpret_cast<unsigned*>(a.part + (size_t)a.part_slots * 4 * kRows * (kHD + 2));
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const float* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, 0x7fffffff, 0x00020000);
+}
+
+
+// Merge workgroup mi of a launch with split key ranges: query block qb (descending, as the pieces are ordered) of
+// one (sequence, KV head) pair and query head hh. Once the block's pieces have marked their slots,
+// out = (O / l) * sigmoid(gate) with O = sum_j 2^(m_j - M) O_j, l = sum_j 2^(m_j - M) l_j over the pieces in order,
+// M = max_j m_j: the attention epilogue's arithmetic, and a piece that holds no key of a row adds exact zeros, so a
+// row comes out the same whichever block and pieces it falls in. Thread t: row t / 8, dims 32 (t % 8) .. + 31.
+constexpr int kMaxPieces = 16;
 template <typename T>
-__global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
+__device__ __forceinline__ void merge_block(const GqaArgs& a, int per_pair, int mi) {
+  const int npair = a.B * a.HK, nqb = (a.L + kRows - 1) / kRows;
+  const int hh = mi & 3, pq = mi >> 2, pair = pq % npair, qb = nqb - 1 - pq / npair;
+  const int np = (gqa_ntiles(a, qb) + a.split - 1) / a.split;
+  if (np < 2) return;
+  int cum = 0;
+  for (int q = 0; q < qb; q++) cum += (gqa_ntiles(a, q) + a.split - 1) / a.split;
+  const int slot0 = pair * per_pair + cum;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    const unsigned* marks = part_marks(a);
+    for (int j = 0; j < np; j++)
+      for (int i = 0; i < (1 << 16) && __hip_atomic_load(marks + slot0 + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != a.epoch; i++)
+        __builtin_amdgcn_s_sleep(2);
+  }
+  __syncthreads();
+  const int b = pair / a.HK, h = (pair % a.HK) * 4 + hh;
+  const int row = tid >> 3, d0 = 32 * (tid & 7), t = qb * kRows + row;
+  const __amdgpu_buffer_rsrc_t rs = part_rsrc(a.part);
+  const unsigned ml0 = (unsigned)((size_t)a.part_slots * 4 * kRows * kHD);  // first (max, sum) float
+  auto rowidx = [&](int j) { return (unsigned)(((slot0 + j) * 4 + hh) * kRows + row); };
+  auto ldf = [&](unsigned fidx) { return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, fidx * 4, 0, kCacheSc1)); };
+  f4 g[8];
+  {
+    const int tc = min(t, a.L - 1);  // a row past the end is loaded, never stored
+#pragma unroll
+    for (int i = 0; i < 8; i++) g[i] = ld4(gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD + d0 + 4 * i);
+  }
+  // the reference maxima of every piece in one round of loads, then the pieces four at a time
+  float mj[kMaxPieces];
+#pragma unroll
+  for (int j = 0; j < kMaxPieces; j++)
+    if (j < np) mj[j] = ldf(ml0 + rowidx(j) * 2);
+  float M = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kMaxPieces; j++)
+    if (j < np) M = fmaxf(M, mj[j]);
+  f4 o[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) o[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float l = 0.0f;
+#pragma unroll
+  for (int j0 = 0; j0 < kMaxPieces; j0 += 4) {
+    if (j0 >= np) break;
+    f4 oj[4][8];
+    float lj[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if (j0 + k < np) {
+        const unsigned r = rowidx(j0 + k);
+        lj[k] = ldf(ml0 + r * 2 + 1);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          oj[k][i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, (r * kHD + d0 + 4 * i) * 4, 0, kCacheSc1));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if (j0 + k < np) {
+        const int j = j0 + k;
+        const float w = mj[j] == M ? 1.0f : __builtin_amdgcn_exp2f(mj[j] - M);
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = o[i] + w * oj[k][i];
+        l = l + w * lj[k];
+      }
+    }
+  }
+  const float linv = 1.0f / l;
+  if (t < a.L) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      f4 r;
+#pragma unroll
+      for (int c = 0; c < 4; c++) r[c] = (o[i][c] * linv) * sigmoid(g[i][c]);
+      store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + d0 + 4 * i, r);
+    }
+  }
+}
+
+// Blocks [0, npair * per_pair) run query blocks (or, with split key ranges, pieces of them); the rest merge pieces.
+template <typename T>
+__global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int per_pair) {
+  if ((int)blockIdx.x >= a.B * a.HK * per_pair) {
+    merge_block<T>(a, per_pair, blockIdx.x - a.B * a.HK * per_pair);
+    return;
+  }
   // LDS: tile buffer i (i < 2) at i * 2 kTileBytes: K tile, then V^T tile.
   // K tile: key r at [r][32 chunks of 8 dims], chunk j stored in slot j ^ (r & 31); V^T tile: dim d at [d][8 chunks
   // of 8 positions], chunk c stored in slot c ^ ((d >> 1) & 7). A wave's global_load_lds_dwordx4 covers whole 512 B
@@ -492,15 +598,14 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   const int er = lane >> 5, ec = 4 * (lane & 31);
   if (npieces > 1) {
     // one piece of a split key range: unnormalised O and the row's (reference max, sum) to the partial slot
-    // (slot = pair's first slot + pieces of the blocks below qb + piece); gqa_combine_kernel finishes the rows
-    const int per_pair = gridDim.x / npair;
+    // (slot = pair's first slot + pieces of the blocks below qb + piece), sc1 stores, then the slot's mark
     const int slot = pair * per_pair + (per_pair - (id / npair - piece) - npieces) + piece;
     const size_t rbase = ((size_t)slot * 4 + (wave & 3)) * kRows + 32 * (wave >> 2);
-    float* po = a.part + rbase * kHD;
-    float* pml = a.part + (size_t)a.part_slots * 4 * kRows * kHD + rbase * 2;
+    const __amdgpu_buffer_rsrc_t po = part_rsrc(a.part + rbase * kHD);
+    const __amdgpu_buffer_rsrc_t pml = part_rsrc(a.part + (size_t)a.part_slots * 4 * kRows * kHD + rbase * 2);
     if (half == 0) {
-      pml[2 * c32] = mref;
-      pml[2 * c32 + 1] = lsum;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, mref), pml, 8 * c32, 0, kCacheSc1);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, lsum), pml, 8 * c32 + 4, 0, kCacheSc1);
     }
 #pragma unroll
     for (int p = 0; p < 2; p++) {
@@ -512,10 +617,14 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const f4 o = lds4(ep + (2 * i + er) * kEP + ec);
-        *(__attribute__((address_space(1))) f4*)(po + (size_t)(2 * i + er) * kHD + 128 * p + ec) = o;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, o), po, ((2 * i + er) * kHD + 128 * p + ec) * 4, 0,
+                                               kCacheSc1);
       }
       wave_sync();
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have reached the device-coherent level
+    __syncthreads();                // ... and every wave's
+    if (tid == 0) __hip_atomic_store(part_marks(a) + slot, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   // epilogue: out[t][h][d] = O / l * sigmoid(gate), through LDS (free after the loop's last barrier). Each wave
@@ -560,59 +669,6 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a) {
   }
 }
 
-// Rows of query blocks whose key range was split: out = (O / l) * sigmoid(gate) with O = sum_j 2^(m_j - M) O_j,
-// l = sum_j 2^(m_j - M) l_j over the block's pieces in order, M = max_j m_j. The last two steps are the attention
-// kernel's own epilogue arithmetic, and a piece that holds no key of a row adds exact zeros, so a row comes out
-// the same whichever block and pieces it falls in. Grid (pairs * query blocks * 4 heads, 16): 4 rows per
-// workgroup, one lane per 4 dims of a row, every piece's loads issued together.
-constexpr int kMaxPieces = 16;
-template <typename T>
-__global__ __launch_bounds__(256) void gqa_combine_kernel(GqaArgs a, int per_pair) {
-  const int npair = a.B * a.HK;
-  const int hh = blockIdx.x & 3, pq = blockIdx.x >> 2, pair = pq % npair, qb = pq / npair;
-  const int np = (gqa_ntiles(a, qb) + a.split - 1) / a.split;
-  const int row = 4 * blockIdx.y + ((int)threadIdx.x >> 6), c4 = threadIdx.x & 63;
-  const int t = qb * kRows + row;
-  if (np < 2 || t >= a.L) return;
-  int cum = 0;
-  for (int q = 0; q < qb; q++) cum += (gqa_ntiles(a, q) + a.split - 1) / a.split;
-  const int slot0 = pair * per_pair + cum;
-  const int b = pair / a.HK, h = (pair % a.HK) * 4 + hh;
-  gptr<float> po = gp<float>(a.part);
-  gptr<float> pml = gp<float>(a.part) + (size_t)a.part_slots * 4 * kRows * kHD;
-  const f4 g = ld4(gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)h * 2 * kHD + kHD + 4 * c4);
-  float mj[kMaxPieces], lj[kMaxPieces];
-  f4 oj[kMaxPieces];
-#pragma unroll
-  for (int j = 0; j < kMaxPieces; j++) {
-    if (j < np) {
-      const size_t r = ((size_t)(slot0 + j) * 4 + hh) * kRows + row;
-      mj[j] = pml[r * 2];
-      lj[j] = pml[r * 2 + 1];
-      oj[j] = *(gptr<f4>)(po + r * kHD + 4 * c4);
-    }
-  }
-  float M = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kMaxPieces; j++)
-    if (j < np) M = fmaxf(M, mj[j]);
-  f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-  float l = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kMaxPieces; j++) {
-    if (j < np) {
-      const float w = mj[j] == M ? 1.0f : __builtin_amdgcn_exp2f(mj[j] - M);
-      o = o + w * oj[j];
-      l = l + w * lj[j];
-    }
-  }
-  const float linv = 1.0f / l;
-  f4 r;
-#pragma unroll
-  for (int c = 0; c < 4; c++) r[c] = (o[c] * linv) * sigmoid(g[c]);
-  store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + 4 * c4, r);
-}
-
 template <typename T>
 hipError_t launch_attn(const GqaArgs& a, hipStream_t s) {
   auto k = gqa_attn_kernel<T>;
@@ -632,15 +688,15 @@ hipError_t launch_attn(const GqaArgs& a, hipStream_t s) {
     if (any_split && ((size_t)npair * per_pair > (size_t)a.part_slots || !a.part)) return hipErrorInvalidValue;
     if ((a.LT / kBK + a.split - 1) / a.split > kMaxPieces) return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL(k, dim3(npair * per_pair), dim3(64 * kWaves), kAttnLds, s, a);
-  if ((e = hipGetLastError()) != hipSuccess || !any_split) return e;
-  hipLaunchKernelGGL(gqa_combine_kernel<T>, dim3(npair * nqb * 4, kRows / 4), dim3(256), 0, s, a, per_pair);
+  if (any_split && a.epoch == 0) return hipErrorInvalidValue;
+  const int nmerge = any_split ? npair * nqb * 4 : 0;
+  hipLaunchKernelGGL(k, dim3(npair * per_pair + nmerge), dim3(64 * kWaves), kAttnLds, s, a, per_pair);
   return hipGetLastError();
 }
 
 }  // namespace
 
-size_t gqa_part_slot_bytes() { return (size_t)4 * kRows * (kHD + 2) * sizeof(float); }
+size_t gqa_part_slot_bytes() { return (size_t)4 * kRows * (kHD + 2) * sizeof(float) + sizeof(unsigned); }
 
 // Per pair, a call with P + L <= max_ctx has at most sum_{k=2}^{N+1} ceil(k / split) pieces (N = max_ctx / 64):
 // block qb reads at most P/64 + qb + 2 tiles and there are at most N - P/64 blocks.

@@ -52,10 +52,13 @@ struct GqaArgs {
   _Float16* V;               // [B][HK][HD][LT] cache, transposed (positions contiguous)
   // Split key ranges: with split > 0, the keys of a query block are processed in pieces of `split` 64-key tiles
   // at absolute tile boundaries, by separate workgroups; a block with more than one piece writes per-piece partial
-  // results to `part` (part_slots slots) and gqa_combine_kernel merges them. 0: one workgroup per block.
+  // results to `part` (part_slots slots), marks the slot with `epoch`, and merge workgroups of the same launch
+  // combine them. 0: one workgroup per block.
   int split;
   int part_slots;
-  float* part;               // [slots][4][64][HD] unnormalised O, then [slots][4][64][2] (reference max, sum)
+  float* part;               // [slots][4][64][HD] unnormalised O, then [slots][4][64][2] (reference max, sum), then
+                             // [slots] u32 epoch marks
+  unsigned epoch;            // this launch's mark, >= 1 and different from every earlier launch's on `part`
 };
 
 // Slots of partial results the split GQA path needs for any call on a context of at most max_ctx positions.
