@@ -36,16 +36,12 @@ constexpr int kOffA = 48 * kBlk;      // Att blocks [tb 0..3][kb 0..1] (blocks w
 constexpr int kOffU = 56 * kBlk;      // U in the D layout: blocks [tb 0..3][jt 0..7] of 64 lanes x 4 f16
 constexpr int kOffS = 72 * kBlk;      // e^(gc_63) as f32
 constexpr int kImg = 73 * kBlk;       // whole 1 KiB DMA instructions
-// After the image (not copied to LDS): the gated norm's factors gnorm_w[j] SiLU(z[t][j]) in fp32, in the lane order of
-// the recurrence's transposed output: block (w, tb, jj) of 64 lanes x 4 floats holds, for lane (grp, c16),
-// columns 32 w + 16 jj + 4 grp .. + 3 of chunk row 16 tb + c16.
-constexpr int kGate = 32 * kBlk;
-// After those, the scan schedule's state at the chunk's start, packed as the products with S read it (f16 B operands):
+// After the image, the state at the chunk's start as the state pass leaves it, packed as the products with S read it (f16 B operands):
 // the h8 Sb[kb][jj] of lane l of wave w (state rows {32 kb + 4 grp + e} U {32 kb + 16 + 4 grp + e} of value column
 // 32 w + 16 jj + (l & 15)) at byte ((w * 4 + kb) * 2 + jj) * 1024 + 16 l.
-constexpr int kOffSnap = kImg + kGate;
+constexpr int kOffSnap = kImg;
 constexpr int kSnap = 32 * kBlk;
-constexpr int kChunkScratch = kImg + kGate + kSnap;
+constexpr int kChunkScratch = kImg + kSnap;
 
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i2v __attribute__((ext_vector_type(2)));
@@ -146,19 +142,6 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
     const gptr<T> grow = row_of<T>(a, src, b, min(cs + lane, end - 1));
     ga = (float)grow[aoff];
     gb = (float)grow[boff];
-  }
-  // z for the gate factors: thread (w, lane) takes the recurrence's block (w, tb, jj) lane `lane`: row 16 tb + c16
-  // (rows outside [P, P + L) clamped: their outputs are never stored), columns 32 w + 16 jj + 4 grp .. + 3
-  f4 zr[4][2];
-  if (a.gnorm) {
-    const int lane = tid0 & 63, grp = lane >> 4, c16 = lane & 15;
-    const gptr<T> zb = gp<T>(seq_in) + a.C + h * kDV + 32 * w + 4 * grp;
-#pragma unroll
-    for (int tb = 0; tb < 4; tb++) {
-      const int rr = min(max(cs + 16 * tb + c16 - a.P, 0), a.L - 1);
-#pragma unroll
-      for (int jj = 0; jj < 2; jj++) zr[tb][jj] = ld4(zb + (size_t)rr * a.stride + 16 * jj);
-    }
   }
   // conv taps to LDS, behind the row loads
   for (int i = tid0; i < 3 * 128 * kKC; i += kPT) {
@@ -438,19 +421,6 @@ __global__ __launch_bounds__(kPT) void gdn_prep_kernel(GdnArgs a) {
     }
   }
   if (tid0 == 0) img.st4(kOffS, sm.eg[kCH - 1]);
-  if (a.gnorm) {
-    const f4 gw0 = ld4(gp<float>(a.gnorm) + 32 * w + 4 * grp), gw1 = ld4(gp<float>(a.gnorm) + 32 * w + 16 + 4 * grp);
-#pragma unroll
-    for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-      for (int jj = 0; jj < 2; jj++) {
-        const f4 gw = jj ? gw1 : gw0;
-        f4 g;
-#pragma unroll
-        for (int e = 0; e < 4; e++) g[e] = gw[e] * silu(zr[tb][jj][e]);
-        store4(gpw<float>(slot + kImg + ((w * 4 + tb) * 2 + jj) * kBlk + lo16), g);
-      }
-  }
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -663,13 +633,19 @@ __device__ __forceinline__ void out_pass(const GdnArgs& a, unsigned char* lds_ra
   for (int i = w; i < kImg / kBlk; i += kCW)
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + kBlk * (size_t)i + 16 * lane),
                                      (__attribute__((address_space(3))) void*)(sm.img + kBlk * i), 16, 0, 0);
-  f4 zq[4][2];
+  // z at this lane's (transposed) output positions, row 16 tb + c16 (rows outside [P, P + L) clamped: their outputs
+  // are never stored), columns 32 w + 16 jj + 4 grp .. + 3; the gate factors gnorm_w SiLU(z) are formed at their use
+  f4 zq[4][2], gw[2];
   if (a.gnorm) {
-    const gptr<float> g = gp<float>(src + kImg) + (size_t)(w * 8) * (kBlk / 4) + 4 * lane;
+    gw[0] = ld4(gp<float>(a.gnorm) + 32 * w + 4 * grp);
+    gw[1] = ld4(gp<float>(a.gnorm) + 32 * w + 16 + 4 * grp);
+    const gptr<T> zb = gp<T>((const char*)a.in + (size_t)b * a.L * ((unsigned)a.stride * sizeof(T))) + a.C + h * kDV + 32 * w + 4 * grp;
 #pragma unroll
-    for (int tb = 0; tb < 4; tb++)
+    for (int tb = 0; tb < 4; tb++) {
+      const int rr = min(max(c0 + 16 * tb + c16 - a.P, 0), a.L - 1);
 #pragma unroll
-      for (int jj = 0; jj < 2; jj++) zq[tb][jj] = ld4(g + (size_t)(tb * 2 + jj) * (kBlk / 4));
+      for (int jj = 0; jj < 2; jj++) zq[tb][jj] = ld4(zb + (size_t)rr * a.stride + 16 * jj);
+    }
   }
   // the packed state at the chunk's start, once the four state workgroups of this (sequence, head) have published it
   // (at most 2^16 polls of about a microsecond: they are resident or done, so the wait ends)
@@ -758,7 +734,12 @@ __device__ __forceinline__ void out_pass(const GdnArgs& a, unsigned char* lds_ra
       const f4 r = lds4(&sm.red[(16 * tb + c16) * kCW]);
       const float iv = rsqrtf(((r[0] + r[1]) + (r[2] + r[3])) / kDV + 1e-6f);
 #pragma unroll
-      for (int jj = 0; jj < 2; jj++) O[jj][tb] = O[jj][tb] * iv * zq[tb][jj];
+      for (int jj = 0; jj < 2; jj++) {
+        f4 g;
+#pragma unroll
+        for (int e = 0; e < 4; e++) g[e] = gw[jj][e] * silu(zq[tb][jj][e]);
+        O[jj][tb] = O[jj][tb] * iv * g;
+      }
     }
   }
   const int ostride = a.H * kDV;
