@@ -170,12 +170,11 @@ const ha_engine* snapshot_owner(const ha_snapshot* s) {
 }
 
 // HA_CHUNKED's choice of gated-delta prefill, from the engine's shape alone so that every call rounds alike: the
-// three-kernel form (every chunk's preparation and output work spread over the chip, only the state pass sequential)
-// up to 32 sequence-heads, the paired form above that while its two workgroups per recurrence fit the 256 CUs in one
-// round (B*H a multiple of 8, at most 128), the fused kernel beyond. Measured per layer at T = 2048, 18 forwards back
-// to back (split / paired / fused, us): B=1 68 / 175 / -, B=2 114 / 176 / -, B=3 189 / 183 / -, B=4 252 / 196 / -,
-// B=8 - / 271 / 303,
-// B=16 - / - / 350.
+// split form (every chunk's preparation spread over the chip, then the state pass with the outputs beside it) up to
+// 32 sequence-heads, the paired form above that while its two workgroups per recurrence fit the 256 CUs in one round
+// (B*H a multiple of 8, at most 128), the fused kernel beyond. Measured per layer at T = 2048, 18 forwards back to
+// back (split / paired / fused, us): B=1 68 / 175 / -, B=2 114 / 176 / -, B=3 189 / 183 / -, B=4 252 / 196 / -,
+// B=8 - / 271 / 303, B=16 - / - / 350.
 bool split_by_shape(const ha_config& c) { return c.batch * c.H <= 32; }
 bool paired_by_shape(const ha_config& c) { return !split_by_shape(c) && ha::gdn_duo_fits(c.batch, c.H); }
 
