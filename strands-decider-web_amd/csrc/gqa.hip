@@ -386,6 +386,22 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // The first tile's K/V copy is issued once the lane's Q loads are out, so that those return first.
   float* qw_l = reinterpret_cast<float*>(lds_raw + (size_t)(((kt0 & 1) ^ 1) * 2) * kTileBytes);
   if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = *(gptr<f4>)(gp<float>(a.qw) + 4 * tid);
+  // A wave whose 32 rows all lie past the call's end (the second half of a block with at most 32 rows, as in a
+  // decode step) only copies its share of every tile and meets the other waves' barriers (q's weights staged, first
+  // tile in, then one per tile), then leaves: its rows are never stored (nor read from a piece's partial results),
+  // and no other row depends on it. Barriers after that count only the waves still running.
+  if (q0 >= a.L) {
+    issue(kt0, lane);
+    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kt = kt0; kt < kt1; kt++) {
+      if (kt + 1 < kt1) issue(kt + 1, opaque(tid) & 63);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    return;
+  }
   h8 qreg[16];
   {
     const int tc = min(q0 + c32, a.L - 1);
