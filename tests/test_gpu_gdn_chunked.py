@@ -122,3 +122,21 @@ def test_default_form_by_shape(B, form):
     (forced,), sf = r.forward([x], keep=True, recurrence=form)
     np.testing.assert_array_equal(auto, forced)
     np.testing.assert_array_equal(_state(sa, B), _state(sf, B))
+
+
+@pytest.mark.parametrize("slow", [False, True], ids=["decay", "slow_decay"])
+def test_large_v_headroom(slow, mode):
+    # v columns (after the 2 x 16 x 128 q and k columns) scaled by 30: the chunked forms round v and the packed state
+    # to f16 as MFMA operands, so large values must keep their relative error (no gated norm, which would rescale
+    # the outputs; slow decay lets the state grow to many times |v|)
+    x = gdn_inputs(512, 2, seed=13)
+    x[:, :, 4096:6144] *= 30.0
+    p = synth.gdn_params(seed=13, **(dict(neg_exp_A=-0.02, dt_bias=-2.0) if slow else {}))
+    r = Runner(["linear_attention"], batch=2, gnorm=False)
+    r.set_params(0, p)
+    (out,), snap = r.forward([x], keep=True, recurrence=mode)
+    ref, st = oracle_gdn(x, p, gnorm=False)
+    e, es = rel_err(out, ref), max(rel_err(_state(snap, 2)[b], st[b].S) for b in range(2))
+    print("large v (slow=%s): max |out| %.3g, max |S| %.3g, rel_err out %.2e state %.2e"
+          % (slow, np.abs(ref).max(), max(np.abs(s.S).max() for s in st), e, es))
+    assert np.isfinite(out).all() and e < TOL and es < TOL
