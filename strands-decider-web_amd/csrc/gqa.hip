@@ -305,7 +305,7 @@ __device__ __forceinline__ void merge_block(const GqaArgs& a, int per_pair, int 
 }
 
 // Blocks [0, npair * per_pair) run query blocks (or, with split key ranges, pieces of them); the rest merge pieces.
-template <typename T>
+template <typename T, bool kIdleHalf>
 __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int per_pair) {
   if ((int)blockIdx.x >= a.B * a.HK * per_pair) {
     merge_block<T>(a, per_pair, blockIdx.x - a.B * a.HK * per_pair);
@@ -356,14 +356,17 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // a tile = 32 K instructions (2 keys each) + 32 V^T instructions (8 dims each); each wave issues 4 + 4. The
   // lane's share of the addresses is re-derived from `ln` on every call (cheap VALU) rather than kept live across the
   // loop: spilled addresses would be reloaded through the same counter the tile loads are waited on.
-  auto issue = [&](int kt, int ln) {
+  // kAll: this wave issues twice its share, instructions (wave & 3) + 4 i (the waves of a block's second half,
+  // when they copy the whole tile for the first half's waves)
+  auto issue_share = [&](int kt, int ln, auto all) {
+    constexpr bool kAll = decltype(all)::value;
     _Float16* kb = lds + (size_t)(kt & 1) * 2 * kTileHalves;
     _Float16* vb = kb + kTileHalves;
     const char* kg = (const char*)(Kg + (size_t)kt * kBK * kHD);
     const char* vg = (const char*)(Vg + (size_t)kt * kBK);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int ins = wave + kWaves * i;             // 0..31
+    for (int i = 0; i < (kAll ? 8 : 4); i++) {
+      const int ins = kAll ? (wave & 3) + 4 * i : wave + kWaves * i;  // 0..31
       const int r = 2 * ins + (ln >> 5), js = ln & 31;
       const int j = js ^ (r & 31);                   // global chunk that belongs in slot js
       const unsigned ko = (unsigned)(r * kHD + 8 * j) * 2u;
@@ -376,6 +379,12 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
                                        (__attribute__((address_space(3))) void*)(vb + (size_t)ins * 512), 16, 0, 0);
     }
   };
+  // kIdleHalf (calls of at most 32 rows, as in a decode step, where every block's second half holds no row of the
+  // call): that half's waves copy every tile and the first half's waves none, which takes the copies off the path of
+  // the waves that compute
+  auto issue = [&](int kt, int ln) {
+    if constexpr (!kIdleHalf) issue_share(kt, ln, std::false_type{});
+  };
 
   // Q as the B operand of S^T = K Q^T (32x32x16): qreg[ks] = q[q0 + c32][16 ks + 8 half .. +7], prepared here:
   // RMSNorm (the two halves of a row sit in lanes l and l + 32), RoPE (dim i < 32 in ks 0/1 pairs with i + 32 in
@@ -387,16 +396,16 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   float* qw_l = reinterpret_cast<float*>(lds_raw + (size_t)(((kt0 & 1) ^ 1) * 2) * kTileBytes);
   if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = *(gptr<f4>)(gp<float>(a.qw) + 4 * tid);
   // A wave whose 32 rows all lie past the call's end (the second half of a block with at most 32 rows, as in a
-  // decode step) only copies its share of every tile and meets the other waves' barriers (q's weights staged, first
+  // decode step) copies every tile (the first half's waves copy none) and meets the other waves' barriers (q's weights staged, first
   // tile in, then one per tile), then leaves: its rows are never stored (nor read from a piece's partial results),
   // and no other row depends on it. Barriers after that count only the waves still running.
   if (q0 >= a.L) {
-    issue(kt0, lane);
+    issue_share(kt0, lane, std::integral_constant<bool, kIdleHalf>{});
     __syncthreads();
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int kt = kt0; kt < kt1; kt++) {
-      if (kt + 1 < kt1) issue(kt + 1, opaque(tid) & 63);
+      if (kt + 1 < kt1) issue_share(kt + 1, opaque(tid) & 63, std::integral_constant<bool, kIdleHalf>{});
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
@@ -687,7 +696,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
 
 template <typename T>
 hipError_t launch_attn(const GqaArgs& a, hipStream_t s) {
-  auto k = gqa_attn_kernel<T>;
+  auto k = a.L <= 32 ? gqa_attn_kernel<T, true> : gqa_attn_kernel<T, false>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)kAttnLds);
   if (e != hipSuccess) return e;
