@@ -243,16 +243,14 @@ __device__ __forceinline__ void merge_block(const GqaArgs& a, int per_pair, int 
   __syncthreads();
   const int b = pair / a.HK, h = (pair % a.HK) * 4 + hh;
   const int row = tid >> 3, d0 = 32 * (tid & 7), t = qb * kRows + row;
+  if (t >= a.L) return;  // a row past the call's end is not output
   const __amdgpu_buffer_rsrc_t rs = part_rsrc(a.part);
   const unsigned ml0 = (unsigned)((size_t)a.part_slots * 4 * kRows * kHD);  // first (max, sum) float
   auto rowidx = [&](int j) { return (unsigned)(((slot0 + j) * 4 + hh) * kRows + row); };
   auto ldf = [&](unsigned fidx) { return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, fidx * 4, 0, kCacheSc1)); };
   f4 g[8];
-  {
-    const int tc = min(t, a.L - 1);  // a row past the end is loaded, never stored
 #pragma unroll
-    for (int i = 0; i < 8; i++) g[i] = ld4(gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD + d0 + 4 * i);
-  }
+  for (int i = 0; i < 8; i++) g[i] = ld4(gp<T>(a.in) + ((size_t)b * a.L + t) * a.stride + (size_t)h * 2 * kHD + kHD + d0 + 4 * i);
   // the reference maxima of every piece in one round of loads, then the pieces four at a time
   float mj[kMaxPieces];
 #pragma unroll
@@ -293,14 +291,12 @@ __device__ __forceinline__ void merge_block(const GqaArgs& a, int per_pair, int 
     }
   }
   const float linv = 1.0f / l;
-  if (t < a.L) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      f4 r;
+  for (int i = 0; i < 8; i++) {
+    f4 r;
 #pragma unroll
-      for (int c = 0; c < 4; c++) r[c] = (o[i][c] * linv) * sigmoid(g[i][c]);
-      store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + d0 + 4 * i, r);
-    }
+    for (int c = 0; c < 4; c++) r[c] = (o[i][c] * linv) * sigmoid(g[i][c]);
+    store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + d0 + 4 * i, r);
   }
 }
 
