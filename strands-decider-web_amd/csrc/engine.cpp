@@ -46,6 +46,7 @@ constexpr uint32_t kEngineMagic = 0x4841454eu, kSnapMagic = 0x48415350u, kDeadMa
 constexpr int kKC = 4;                          // conv kernel the kernels are built for
 constexpr int kTailCap = ha::kChunk - 1 + kKC;  // at most 63 open rows + 3 history rows (+1 spare)
 std::atomic<uint64_t> g_engine_ids{1};
+std::atomic<uint64_t> g_snap_uid{0};  // snapshot uids: 1, 2, ...
 // Engines that exist right now. Handle checks look a pointer up here before reading through it, so a snapshot
 // outliving its engine (any order of release is allowed, e.g. under a garbage collector) never touches freed memory.
 std::mutex g_live_mu;
@@ -115,6 +116,10 @@ int grow(Scratch::Buf& b, size_t bytes) {
 struct ha_engine {
   uint32_t magic = kEngineMagic;
   uint64_t id = 0;
+  // the snapshot (by uid) whose K/V rows [0, kv_rows) the working caches are known to hold, 0 for none: set by the
+  // call that resumed from it or kept it, cleared at the start of every call until that call completes
+  uint64_t kv_snap = 0;
+  int kv_rows = 0;
   ha_config cfg{};
   std::vector<unsigned char> kinds;
   int device = 0;
@@ -139,6 +144,7 @@ struct ha_snapshot {
   uint32_t magic = kSnapMagic;
   const ha_engine* owner = nullptr;
   uint64_t owner_id = 0;
+  uint64_t uid = 0;  // unique over the process, never reused
   int P = 0, s0 = 0, tail_rows = 0;
   bool released = false;
   struct Part {
@@ -485,8 +491,12 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   hipStream_t st = e->stream;
   const size_t B = c.batch;
 
-  // resume: K/V rows [0, P) back into the working caches (engine.js:327); state and tail are read in place
-  if (resume && P > 0)
+  // resume: K/V rows [0, P) back into the working caches (engine.js:327), unless they already hold them (the last
+  // completed call resumed from or kept this snapshot, and calls write only rows from their P on); state and tail
+  // are read in place
+  const bool kv_held = resume && e->kv_snap == resume->uid && e->kv_rows >= P;
+  e->kv_snap = 0;  // unknown until this call completes
+  if (resume && P > 0 && !kv_held)
     for (int i = 0; i < c.n_layers; i++)
       if (e->layers[i].kind == HA_FULL_ATTENTION) {
         const size_t w = (size_t)P * c.HD * sizeof(_Float16), dp = (size_t)c.max_ctx * c.HD * sizeof(_Float16);
@@ -591,7 +601,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
 
   if (keep) {
     ha_snapshot* s = new ha_snapshot();
-    s->owner = e; s->owner_id = e->id; s->P = end; s->s0 = e->any_linear ? s1 : end;
+    s->owner = e; s->owner_id = e->id; s->uid = ++g_snap_uid; s->P = end; s->s0 = e->any_linear ? s1 : end;
     s->tail_rows = s->P - (s->s0 - (kKC - 1));
     s->layers.resize(c.n_layers);
     auto bail = [&](int code) { (void)hipStreamSynchronize(st); free_snapshot_buffers(s); s->magic = kDeadMagic; delete s; return code; };
@@ -630,6 +640,9 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   }
   hipError_t le = hipGetLastError();
   if (le != hipSuccess) return fail(HA_ERR_DEVICE, std::string("device error: ") + hipGetErrorString(le));
+  // the working caches now hold the kept snapshot's rows, or still the resumed one's rows [0, P)
+  if (keep) { e->kv_snap = (*keep)->uid; e->kv_rows = end; }
+  else if (resume) { e->kv_snap = resume->uid; e->kv_rows = P; }
   return HA_OK;
 }
 

@@ -78,3 +78,25 @@ def test_snapshot_errors():
     with pytest.raises(ha.HAError) as ei:
         r.eng.set_param(0, "q_norm", np.ones(256))
     assert ei.value.code == ha.HA_ERR_PARAM
+
+
+def test_resumes_without_restore_copy():
+    # Calls resumed from one snapshot back to back: the working K/V caches already hold its rows, so the engine does
+    # not copy them again. Between them a kept snapshot, a resume from that one (again no copy) and a return to the
+    # first (copied again). Every suffix must still equal the same rows of one full forward.
+    r = _runner()
+    prefix = _inputs(1536, part=0)
+    _, snap = r.forward(prefix, keep=True)
+    sufs = [_inputs(L, part=10 + j) for j, L in enumerate([1, 7, 1, 33])]
+    o1, _ = r.forward(sufs[0], cache=snap)
+    o2, _ = r.forward(sufs[1], cache=snap)
+    o3, kept = r.forward(sufs[2], cache=snap, keep=True)
+    o4, _ = r.forward(sufs[3], cache=kept)
+    o5, _ = r.forward(sufs[1], cache=snap)
+    cases = [([sufs[0]], o1), ([sufs[1]], o2), ([sufs[2]], o3), ([sufs[2], sufs[3]], o4), ([sufs[1]], o5)]
+    for n, (parts, outs) in enumerate(cases):
+        full_in = [np.concatenate([p] + [q[i] for q in parts], 1) for i, p in enumerate(prefix)]
+        full, _ = r.forward(full_in)
+        start = full_in[0].shape[1] - outs[0].shape[1]
+        for i in range(len(KINDS)):
+            np.testing.assert_array_equal(outs[i], full[i][:, start:], err_msg="call %d layer %d" % (n + 1, i))
