@@ -120,6 +120,9 @@ struct ha_engine {
   // call that resumed from it or kept it, cleared at the start of every call until that call completes
   uint64_t kv_snap = 0;
   int kv_rows = 0;
+  // one released snapshot's device block, kept for the next snapshot that fits in it (guarded by g_live_mu)
+  void* spare = nullptr;
+  size_t spare_bytes = 0;
   ha_config cfg{};
   std::vector<unsigned char> kinds;
   int device = 0;
@@ -145,6 +148,8 @@ struct ha_snapshot {
   const ha_engine* owner = nullptr;
   uint64_t owner_id = 0;
   uint64_t uid = 0;  // unique over the process, never reused
+  void* block = nullptr;  // one device allocation holding every part below
+  size_t block_bytes = 0;
   int P = 0, s0 = 0, tail_rows = 0;
   bool released = false;
   struct Part {
@@ -244,20 +249,36 @@ void free_engine(ha_engine* e) {
   for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
   for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
   if (e->own) (void)hipStreamDestroy(e->own);
+  void* spare = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_live_mu);
     g_live.erase(e);
+    spare = e->spare;
+    e->spare = nullptr;
   }
+  if (spare) (void)hipFree(spare);
   e->magic = kDeadMagic;
   delete e;
 }
 
+// The snapshot's block goes back to its engine as the spare when that engine is alive and holds none (the caller has
+// synchronised the engine's stream), else to hipFree.
 void free_snapshot_buffers(ha_snapshot* s) {
-  for (auto& p : s->layers) {
-    for (void* q : {(void*)p.S, p.tail, (void*)p.K, (void*)p.V})
-      if (q) (void)hipFree(q);
-    p = ha_snapshot::Part{};
+  for (auto& p : s->layers) p = ha_snapshot::Part{};
+  if (!s->block) return;
+  bool parked = false;
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    ha_engine* e = const_cast<ha_engine*>(s->owner);
+    if (e && g_live.count(e) && e->id == s->owner_id && !e->spare) {
+      e->spare = s->block;
+      e->spare_bytes = s->block_bytes;
+      parked = true;
+    }
   }
+  if (!parked) (void)hipFree(s->block);
+  s->block = nullptr;
+  s->block_bytes = 0;
 }
 
 }  // namespace
@@ -605,14 +626,40 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
     s->tail_rows = s->P - (s->s0 - (kKC - 1));
     s->layers.resize(c.n_layers);
     auto bail = [&](int code) { (void)hipStreamSynchronize(st); free_snapshot_buffers(s); s->magic = kDeadMagic; delete s; return code; };
+    // every part in one device block (256-byte aligned offsets), the engine's spare block when it is large enough;
+    // a new block is rounded up to 2 MiB so that the next snapshots of a growing context fit in it when it returns
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    size_t total = 0;
+    for (int i = 0; i < c.n_layers; i++) {
+      const Layer& l = e->layers[i];
+      if (l.kind == HA_LINEAR_ATTENTION)
+        total += al(sizeof(float) * B * c.H * c.DK * c.DV) + al(dtype_size(c.lin_dtype) * c.lin_stride * B * s->tail_rows);
+      else if (l.kind == HA_FULL_ATTENTION)
+        total += 2 * al((size_t)end * c.HD * sizeof(_Float16) * B * c.HK);
+    }
+    {
+      std::lock_guard<std::mutex> lock(g_live_mu);
+      if (e->spare && e->spare_bytes >= total) {
+        s->block = e->spare; s->block_bytes = e->spare_bytes;
+        e->spare = nullptr; e->spare_bytes = 0;
+      }
+    }
+    if (!s->block) {
+      const size_t bytes = (total + ((size_t)2 << 20) - 1) & ~(((size_t)2 << 20) - 1);
+      int rc = dalloc(reinterpret_cast<char**>(&s->block), bytes);
+      if (rc) return bail(rc);
+      s->block_bytes = bytes;
+    }
+    size_t off = 0;
+    auto take = [&](size_t b) { void* q = static_cast<char*>(s->block) + off; off += al(b); return q; };
     for (int i = 0; i < c.n_layers; i++) {
       Layer& l = e->layers[i];
       ha_snapshot::Part& p = s->layers[i];
-      int rc = HA_OK;
       if (l.kind == HA_LINEAR_ATTENTION) {
         const size_t sb = sizeof(float) * B * c.H * c.DK * c.DV, esz = dtype_size(c.lin_dtype);
         const size_t rowb = esz * c.lin_stride;
-        if ((rc = dalloc(&p.S, sb)) || (rc = dalloc(&p.tail, rowb * B * s->tail_rows))) return bail(rc);
+        p.S = static_cast<float*>(take(sb));
+        p.tail = take(rowb * B * s->tail_rows);
         if (hipMemcpyAsync(p.S, l.S, sb, hipMemcpyDeviceToDevice, st) != hipSuccess ||
             hipMemcpy2DAsync(p.tail, rowb * s->tail_rows, l.tail, rowb * kTailCap, rowb * s->tail_rows, B,
                              hipMemcpyDeviceToDevice, st) != hipSuccess)
@@ -620,7 +667,8 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       } else if (l.kind == HA_FULL_ATTENTION) {
         const size_t w = (size_t)end * c.HD * sizeof(_Float16), sp = (size_t)c.max_ctx * c.HD * sizeof(_Float16);
         const size_t vw = (size_t)end * sizeof(_Float16), vp = (size_t)c.max_ctx * sizeof(_Float16);
-        if ((rc = dalloc(&p.K, w * B * c.HK)) || (rc = dalloc(&p.V, w * B * c.HK))) return bail(rc);
+        p.K = static_cast<_Float16*>(take(w * B * c.HK));
+        p.V = static_cast<_Float16*>(take(w * B * c.HK));
         if (hipMemcpy2DAsync(p.K, w, l.K, sp, w, B * c.HK, hipMemcpyDeviceToDevice, st) != hipSuccess ||
             hipMemcpy2DAsync(p.V, vw, l.V, vp, vw, B * c.HK * c.HD, hipMemcpyDeviceToDevice, st) != hipSuccess)
           return bail(fail(HA_ERR_DEVICE, "snapshot copy failed"));

@@ -100,3 +100,20 @@ def test_resumes_without_restore_copy():
         start = full_in[0].shape[1] - outs[0].shape[1]
         for i in range(len(KINDS)):
             np.testing.assert_array_equal(outs[i], full[i][:, start:], err_msg="call %d layer %d" % (n + 1, i))
+
+
+def test_snapshot_block_reuse():
+    # A released snapshot's device block becomes its engine's spare, and the next snapshot that fits takes it: that
+    # snapshot must hold its own context (a suffix resumed from it equals the same rows of one full forward), and the
+    # released one is refused.
+    r = _runner()
+    long_in, short_in, sfx = _inputs(900, part=20), _inputs(700, part=21), _inputs(16, part=22)
+    _, s1 = r.forward(long_in, keep=True)
+    s1.release()
+    _, s2 = r.forward(short_in, keep=True)
+    outs, _ = r.forward(sfx, cache=s2)
+    full, _ = r.forward([np.concatenate([p, q], 1) for p, q in zip(short_in, sfx)])
+    for i in range(len(KINDS)):
+        np.testing.assert_array_equal(outs[i], full[i][:, 700:], err_msg="layer %d" % i)
+    with pytest.raises(ha.HAError):
+        r.forward(sfx, cache=s1)
