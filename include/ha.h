@@ -131,8 +131,8 @@ int ha_set_param(ha_engine* e, int layer, const char* name, const float* host, s
      layer_in[i]:  [batch][L][lin_stride] (linear) or [batch][L][full_stride] (full) rows in that kind's dtype
      layer_out[i]: [batch][L][H*DV] or [batch][L][HQ*HD] in that kind's dtype
    resume: continue from this snapshot (engine.js:325-327); NULL starts from an empty context. Its GQA K/V rows are
-           copied back into the engine's working caches unless the engine's last completed call resumed from it or
-           kept it (calls write only rows from their own P on, so those rows are still in place)
+           copied back into the engine's working caches unless the engine knows they are still there (a completed
+           call resumed from it or kept it, and no later call wrote below its P or copied another snapshot in)
    keep:   if non-NULL, receives a new snapshot of the context after this call (engine.js:349-362)
    Returns HA_ERR_CONTEXT if P + L > max_ctx. Layers run in order on the engine's stream. No layer_out buffer may
    overlap any layer_in buffer of the same call: the gated-delta layers' raw rows (conv history and replay rows) are

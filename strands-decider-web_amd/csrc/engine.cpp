@@ -116,10 +116,12 @@ int grow(Scratch::Buf& b, size_t bytes) {
 struct ha_engine {
   uint32_t magic = kEngineMagic;
   uint64_t id = 0;
-  // the snapshot (by uid) whose K/V rows [0, kv_rows) the working caches are known to hold, 0 for none: set by the
-  // call that resumed from it or kept it, cleared at the start of every call until that call completes
-  uint64_t kv_snap = 0;
-  int kv_rows = 0;
+  // snapshots (by uid) whose K/V rows [0, rows) the working caches are known to hold (uid 0: empty entry). A call
+  // from position P writes only rows from P on, so it keeps the entries with rows <= P and adds the snapshot it
+  // resumed from (P rows) and the one it kept (P + L rows); the list is cleared while a call runs
+  static constexpr int kKvHeld = 8;
+  struct KvHeld { uint64_t uid; int rows; };
+  KvHeld kv_held[kKvHeld] = {};
   // one released snapshot's device block, kept for the next snapshot that fits in it (guarded by g_live_mu)
   void* spare = nullptr;
   size_t spare_bytes = 0;
@@ -515,8 +517,17 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   // resume: K/V rows [0, P) back into the working caches (engine.js:327), unless they already hold them (the last
   // completed call resumed from or kept this snapshot, and calls write only rows from their P on); state and tail
   // are read in place
-  const bool kv_held = resume && e->kv_snap == resume->uid && e->kv_rows >= P;
-  e->kv_snap = 0;  // unknown until this call completes
+  bool kv_held = false;
+  ha_engine::KvHeld held[ha_engine::kKvHeld];
+  int nheld = 0;
+  for (const auto& h : e->kv_held) {
+    if (!h.uid) continue;
+    if (resume && h.uid == resume->uid && h.rows >= P) kv_held = true;
+    if (h.rows <= P) held[nheld++] = h;  // still in place after this call
+  }
+  // a restore copy rewrites rows [0, P): then no earlier entry holds any more (only the resumed snapshot does)
+  if (resume && P > 0 && !kv_held) nheld = 0;
+  for (auto& h : e->kv_held) h = {0, 0};  // unknown until this call completes
   if (resume && P > 0 && !kv_held)
     for (int i = 0; i < c.n_layers; i++)
       if (e->layers[i].kind == HA_FULL_ATTENTION) {
@@ -688,9 +699,19 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   }
   hipError_t le = hipGetLastError();
   if (le != hipSuccess) return fail(HA_ERR_DEVICE, std::string("device error: ") + hipGetErrorString(le));
-  // the working caches now hold the kept snapshot's rows, or still the resumed one's rows [0, P)
-  if (keep) { e->kv_snap = (*keep)->uid; e->kv_rows = end; }
-  else if (resume) { e->kv_snap = resume->uid; e->kv_rows = P; }
+  // the working caches now hold the kept snapshot's rows, the resumed one's rows [0, P), and those of the earlier
+  // entries that ended at or before P (newest first; the oldest drop out when the list is full)
+  {
+    int n = 0;
+    auto add = [&](uint64_t uid, int rows) {
+      for (int i = 0; i < n; i++)
+        if (e->kv_held[i].uid == uid) return;
+      if (n < ha_engine::kKvHeld) e->kv_held[n++] = {uid, rows};
+    };
+    if (keep) add((*keep)->uid, end);
+    if (resume) add(resume->uid, P);
+    for (int i = 0; i < nheld; i++) add(held[i].uid, held[i].rows);
+  }
   return HA_OK;
 }
 

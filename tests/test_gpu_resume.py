@@ -117,3 +117,23 @@ def test_snapshot_block_reuse():
         np.testing.assert_array_equal(outs[i], full[i][:, 700:], err_msg="layer %d" % i)
     with pytest.raises(ha.HAError):
         r.forward(sfx, cache=s1)
+
+
+def test_restore_copy_invalidates_other_snapshots():
+    # After a resume from an unrelated snapshot u (longer than snap, so its restore copy rewrites all of snap's rows),
+    # a resume from snap must copy snap's rows back; and a fresh forward invalidates both. Each suffix must equal the
+    # same rows of one full forward of its own context.
+    r = _runner()
+    prefix, other = _inputs(1536, part=30), _inputs(1600, part=31)
+    sfx = _inputs(5, part=32)
+    _, snap = r.forward(prefix, keep=True)
+    _, u = r.forward(other, keep=True)  # a fresh forward: the working caches now hold u's rows only
+    runs = []
+    for cache, ctx in [(snap, prefix), (u, other), (snap, prefix), (snap, prefix), (u, other)]:
+        outs, _ = r.forward(sfx, cache=cache)
+        runs.append((outs, ctx))
+    for n, (outs, ctx) in enumerate(runs):
+        full, _ = r.forward([np.concatenate([p, q], 1) for p, q in zip(ctx, sfx)])
+        P = ctx[0].shape[1]
+        for i in range(len(KINDS)):
+            np.testing.assert_array_equal(outs[i], full[i][:, P:], err_msg="call %d layer %d" % (n + 1, i))
