@@ -98,3 +98,21 @@ def test_split_key_ranges_match_oracle_and_unsplit():
     e1, e5, e15 = rel_err(o1, ref), rel_err(o5[:1], ref), rel_err(o1, o5[:1])
     print("split vs oracle %.2e, unsplit vs oracle %.2e, split vs unsplit %.2e" % (e1, e5, e15))
     assert e1 < TOL and e5 < TOL and e15 < TOL
+
+
+@pytest.mark.parametrize("B,P,steps", [(2, 700, [1, 2, 32, 17]), (8, 1536, [1, 1, 8, 32]), (2, 3, [2, 5])])
+def test_short_steps_bit_exact(B, P, steps):
+    # calls of at most 32 rows run their own instantiation (the second half's waves copy the tiles); chained after a
+    # longer prefix, every step must equal the same rows of one forward, which runs the other instantiation
+    T = P + sum(steps)
+    x = synth.gqa_rows(T, B, seed=7)
+    r = Runner(["full_attention"], batch=B, max_ctx=2048)
+    r.set_params(0, synth.gqa_params(seed=7, noise=0.1))
+    (full,), _ = r.forward([x])
+    (pre,), s = r.forward([x[:, :P]], keep=True)
+    np.testing.assert_array_equal(pre, full[:, :P])
+    a = P
+    for L in steps:
+        (o,), s = r.forward([x[:, a:a + L]], cache=s, keep=True)
+        np.testing.assert_array_equal(o, full[:, a:a + L], err_msg="rows %d..%d" % (a, a + L))
+        a += L
