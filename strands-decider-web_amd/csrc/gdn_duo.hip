@@ -46,7 +46,7 @@ constexpr int kP = kC + 8;      // row pitch (halves) of [*][32] f16 tiles
 constexpr int kMP = kC + 4;     // row pitch (floats) of the fp32 A / T tile
 constexpr int kThreads = 512;   // 8 waves per workgroup
 constexpr int kOP = kDV + 4;    // row pitch (floats) of the consumer's output rows
-constexpr int kLead = 6;        // chunks the producer may run ahead of the consumer before it holds back
+constexpr int kLead = 24;       // chunks the producer may run ahead of the consumer before it holds back
 // Vector memory instructions a helper wave issues after its tile-set DMA in every period: the v rows (kKC + 7 loads), the
 // z rows (4) and the counter (1). s_waitcnt with vmcnt = kAfterDma (expcnt and lgkmcnt not waited for) then covers
 // the DMA alone.
