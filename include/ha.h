@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define HA_ABI_VERSION 1
+#define HA_ABI_VERSION 2
 
 typedef struct ha_engine ha_engine;
 typedef struct ha_snapshot ha_snapshot;
@@ -39,7 +39,8 @@ typedef enum ha_status {
   HA_ERR_ARG = -1,      /* bad argument, shape or config */
   HA_ERR_CONTEXT = -2,  /* P + L exceeds max_ctx (engine.js:316 "context ... exceeds") */
   HA_ERR_HANDLE = -3,   /* invalid, foreign or released engine / snapshot handle */
-  HA_ERR_DEVICE = -4,   /* a HIP runtime call failed (engine.js:373 collects device errors) */
+  HA_ERR_DEVICE = -4,   /* a HIP runtime call failed, or a kernel of an earlier call reported a bounded wait
+                           that ran out (engine.js:373 throws the device errors a forward collected) */
   HA_ERR_NOMEM = -5,    /* device or host allocation failed */
   HA_ERR_PARAM = -6     /* unknown tensor name or wrong element count (engine.js:177 "no tensor ...") */
 } ha_status;
@@ -94,11 +95,24 @@ typedef struct ha_forward_opts {
   int timestamps;  /* 1: time the whole forward with HIP events; result in gpu_ms (engine.js:331-348) */
   int sync;        /* 1: wait for the stream before returning */
   float gpu_ms;    /* out: forward time when timestamps = 1 (implies a wait) */
-  float* layer_ms; /* optional out [n_layers]: per-layer GPU ms (the reference's profile(), engine.js:292-307) */
+  float* layer_ms; /* optional out [n_layers]: per-layer GPU ms (the reference's profile(), engine.js:292-307),
+                      each gated-delta layer's raw-row tail copy included */
+  float* mixer_ms; /* optional out [n_layers]: GPU ms of each layer's token-mixer kernels alone (without the tail
+                      copy; 0 for adapter layers). No counterpart in the reference: the kernel time a roofline is
+                      computed on. Implies a wait, like layer_ms */
+  int debug_unpublished_waits; /* test only, 0 otherwise. No counterpart in the reference. 1: every bounded
+                      cross-workgroup wait of this call (the paired form's tile-set wait, the split form's
+                      packed-state wait, the split-key attention merge) waits for a value no workgroup of it
+                      publishes, for a few polls each, then goes on; every kernel still ends, the outputs are
+                      undefined, and the failure is reported as HA_ERR_DEVICE (exercises that path from the host) */
 } ha_forward_opts;
 
 const char* ha_last_error(void);
 int ha_abi_version(void);
+/* The architecture name of HIP device `device` ("gfx950"), into name[bytes]: what the reference's adapter guard
+   engineProblems(adapter) inspects (engine.js:50-52); every kernel here is built for gfx950 only. HA_ERR_DEVICE when
+   no HIP device is visible. */
+int ha_device_arch(int device, char* name, size_t bytes);
 
 /* Engine.create / constructor (engine.js:63-111): validates the config, allocates the working state, history
    and K/V buffers and the RoPE table on HIP device `device`, and creates the engine's stream. */
@@ -106,15 +120,17 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out);
 int ha_destroy(ha_engine* e);
 
 /* Bind the engine to an existing HIP stream (hipStream_t passed as void*), e.g. a framework's current stream.
-   NULL rebinds the engine's own stream. */
+   NULL rebinds the engine's own stream. An engine that shares its call-time buffers with other engines
+   (ha_share_scratch) and moves to a different stream first gets a set of its own again (waiting for the device),
+   so that engines holding one set always run on one stream. */
 int ha_set_stream(ha_engine* e, void* stream);
 /* Let engine e use the call-time device buffers of `holder` (chunk images, the sequential form's raw outputs and
    counters, split-GQA partials, the zero history), growing them to what e's shape needs, and free e's own set once
-   nothing else holds it. For engines whose calls never overlap, e.g. the per-layer engines of one torso on one
-   stream: their calls then run one after another and one set serves all of them. Calls of engines holding one set
-   must not overlap (one stream, or the host waiting between them). The set lives until the last engine holding it
-   is destroyed. No counterpart in the reference, whose engine holds one set of buffers for all its layers
-   (engine.js:89-107). Waits for the device to finish queued work. */
+   nothing else holds it. For the per-layer engines of one torso on one stream: their calls then run one after
+   another and one set serves all of them. Both engines must already run on one stream (HA_ERR_ARG otherwise), and
+   ha_set_stream keeps it so. The set lives until the last engine holding it is destroyed. No counterpart in the
+   reference, whose engine holds one set of buffers for all its layers (engine.js:89-107). Waits for the device to
+   finish queued work. */
 int ha_share_scratch(ha_engine* e, ha_engine* holder);
 /* The stream the engine's calls run on (hipStream_t as void*): for a host that queues its own work, such as the
    projection matmuls (ha_mnb_forward), in order with the token mixers. No counterpart in the reference, whose
@@ -136,7 +152,11 @@ int ha_set_param(ha_engine* e, int layer, const char* name, const float* host, s
    keep:   if non-NULL, receives a new snapshot of the context after this call (engine.js:349-362)
    Returns HA_ERR_CONTEXT if P + L > max_ctx. Layers run in order on the engine's stream. No layer_out buffer may
    overlap any layer_in buffer of the same call: the gated-delta layers' raw rows (conv history and replay rows) are
-   copied from layer_in after all layers have run. */
+   copied from layer_in after all layers have run.
+   Device errors: the kernels' cross-workgroup waits are bounded; a wait that runs out (never in a correct launch)
+   lets its kernel end and marks the engine's error word. The call that synchronises (sync, timestamps, layer_ms,
+   mixer_ms), the next ha_forward, ha_synchronize and ha_copy_to_host then return HA_ERR_DEVICE once, and no
+   snapshot of the failed call is kept. */
 int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* layer_out, const ha_snapshot* resume,
                ha_snapshot** keep, ha_forward_opts* opts);
 
@@ -146,8 +166,16 @@ int ha_snapshot_tokens(const ha_snapshot* s, int* P);
 /* Position of the stored recurrent state (a multiple of 64 after chunked forwards, P after sequential ones) and
    the number of raw rows kept for replay and conv history, [state_pos - (conv_k-1), P). */
 int ha_snapshot_layout(const ha_snapshot* s, int* state_pos, int* tail_rows);
-/* Copy one part of a snapshot to host memory: "state" f32 [batch][H][DK][DV] (linear layer), "tail" rows
-   [batch][tail_rows][lin_stride] in lin_dtype (linear), "K" / "V" f16 [batch][HK][P][HD] (full). */
+/* Copy one part of a snapshot to host memory (linear layers: "state", "state_stored", "tail"; full layers: "K",
+   "V"):
+     "state"        f32 [batch][H][DK][DV]: the recurrent state after all P tokens, as the reference's snapshot holds
+                    it (engine.js:352-356). When the stored state sits at an earlier chunk boundary (state_pos < P),
+                    it is advanced over the replay rows [state_pos, P) with the sequential fp32 rule for this read
+                    (a resume replays those rows in the chunked form instead, so that prefix + suffix stays
+                    bit-identical to one forward; the two agree within the recurrence tolerance)
+     "state_stored" f32 [batch][H][DK][DV]: the stored state at state_pos (what a resume starts from)
+     "tail"         [batch][tail_rows][lin_stride] in lin_dtype: the raw rows [state_pos - (conv_k-1), P)
+     "K" / "V"      f16 [batch][HK][P][HD]. */
 int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* host, size_t bytes);
 /* Free the snapshot's device memory (snapshot.release(), engine.js:361). Idempotent. */
 int ha_snapshot_release(ha_snapshot* s);
@@ -159,6 +187,7 @@ int ha_device_alloc(ha_engine* e, size_t bytes, void** dptr);
 int ha_device_free(ha_engine* e, void* dptr);
 int ha_copy_to_device(ha_engine* e, void* dst, const void* host, size_t bytes);
 int ha_copy_to_host(ha_engine* e, void* host, const void* src, size_t bytes);
+/* Wait for the engine's stream; HA_ERR_DEVICE if a kernel of an earlier call reported a wait that ran out. */
 int ha_synchronize(ha_engine* e);
 
 /* ---- MatMulNBits projections: the matmuls either side of the path ----
@@ -202,18 +231,18 @@ int ha_mnb_forward_noalloc(ha_mnb* w, int M, const void* a, void* y, void* strea
 int ha_mnb_destroy(ha_mnb* w);
 /* In-place orthonormal Walsh-Hadamard transform of every contiguous n-block of the f16 array x (elems values, a
    multiple of n; n a power of two up to 8192): the online input rotation of a tensor exported with `had: n`
-   (FWHT, web/public/engine/wgsl.js:91-108; applied before the matmul at engine.js:240). */
+   (FWHT, web/public/engine/wgsl.js:94-110; applied before the matmul at engine.js:240). */
 int ha_fwht(void* x, long elems, int n, int device, void* stream);
 
 /* ---- The rest of the torso forward (web/public/engine/engine.js:247-284): all device pointers, all on `stream`
    (hipStream_t as void*, NULL: the null stream), on HIP device `device`. */
 
 /* x[t][0..K) = f32 row ids[t] of the quantised embedding table held by `table` (a MatMulNBits handle with N = table
-   rows, K = hidden size; EMBED, web/public/engine/wgsl.js:42-61): (q - 2^(bits-1)) * scale, or q * scale + bias, in
+   rows, K = hidden size; EMBED, web/public/engine/wgsl.js:33-52): (q - 2^(bits-1)) * scale, or q * scale + bias, in
    f32. ids: L u32 on the device; an id >= N gives a row of NaN. */
 int ha_embed(const ha_mnb* table, int L, const void* ids, void* x, void* stream);
 
-/* Residual add + RMSNorm (ADD_NORM, wgsl.js:64-87): for output row r with source row s = rows[r] (rows NULL: s = r),
+/* Residual add + RMSNorm (ADD_NORM, wgsl.js:55-78): for output row r with source row s = rows[r] (rows NULL: s = r),
    if y != NULL first x[s] += y[s] (f32 += f16, written back), then
    h[r] = x[s] * (mean(x[s]^2) + eps)^-1/2 * w   (w: D f32, already 1 + w where the model says so),
    h f16, or f32 when out_f32 (the final norm, engine.js:283-284, 342). x has nx rows of D (D % 8 == 0, D <= 8192);
@@ -221,10 +250,10 @@ int ha_embed(const ha_mnb* table, int L, const void* ids, void* x, void* stream)
 int ha_add_norm(int R, int D, int nx, void* x, const void* y, const float* w, void* h, int out_f32,
                 const void* rows, float eps, int device, void* stream);
 
-/* mid[t][j] = silu(big[t][j]) * big[t][I + j] for t < L, j < I (SILU_MUL, wgsl.js:90-99); f16, I % 8 == 0. */
+/* mid[t][j] = silu(big[t][j]) * big[t][I + j] for t < L, j < I (SILU_MUL, wgsl.js:81-90); f16, I % 8 == 0. */
 int ha_silu_mul(int L, int I, const void* big, void* mid, int device, void* stream);
 
-/* y[t][j] += c[j] for t < L, j < N (ADD_BIAS, wgsl.js:119-121): y f16, c f32 on the device, N % 8 == 0. */
+/* y[t][j] += c[j] for t < L, j < N (ADD_BIAS, wgsl.js:113-121): y f16, c f32 on the device, N % 8 == 0. */
 int ha_add_bias(int L, int N, void* y, const float* c, int device, void* stream);
 
 /* ---- GPU timestamps for diagnostics: the counterpart of the reference's WebGPU timestamp query sets, written at

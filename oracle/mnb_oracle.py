@@ -12,7 +12,7 @@ never loads it. Each function cites the reference lines it restates:
   q * scale + bias).
 - matmul: y[M][N] = a[M][K] . W[N][K]^T in fp64 (the reference's own check, gemmbench/bench.js:48-50, is this sum
   in fp32 on a few columns).
-- fwht: the orthonormal Walsh-Hadamard transform of each n-block, web/public/engine/wgsl.js:91-108 (Sylvester
+- fwht: the orthonormal Walsh-Hadamard transform of each n-block, web/public/engine/wgsl.js:94-110 (Sylvester
   order, scaled by 1/sqrt(n)).
 
 Pins (tests/test_oracle_mnb.py): a scalar restatement of bench.js:48-50's nibble indexing; hand-built blocks with

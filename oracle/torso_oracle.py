@@ -4,14 +4,14 @@ ONLY.
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import this module; the product library
 never loads it. Each function cites the reference lines it restates:
 
-- embed: EMBED, web/public/engine/wgsl.js:42-61. Row `id` of a quantised table in the MatMulNBits formats of
+- embed: EMBED, web/public/engine/wgsl.js:33-52. Row `id` of a quantised table in the MatMulNBits formats of
   gemmbench/kernels.js:1-14 (decode as oracle/mnb_oracle.py), symmetric (q - 2^(bits-1)) * scale or asymmetric
   q * scale + bias, in f32.
-- add_norm: ADD_NORM, wgsl.js:64-87. Output row r reads source row rows[r]; with y the residual add x += y
+- add_norm: ADD_NORM, wgsl.js:55-78. Output row r reads source row rows[r]; with y the residual add x += y
   (written back) comes first; then h = x * (mean(x^2) + eps)^-1/2 * w. The weight is used as given (the exporter
   stores 1 + w for the zero-centred norms, export_engine.py).
-- silu_mul: SILU_MUL, wgsl.js:90-99. mid = silu(g) * u, with big[t] = [g (I) | u (I)].
-- add_bias: ADD_BIAS, wgsl.js:119-121. y += c per column.
+- silu_mul: SILU_MUL, wgsl.js:81-90. mid = silu(g) * u, with big[t] = [g (I) | u (I)].
+- add_bias: ADD_BIAS, wgsl.js:113-121. y += c per column.
 
 Pins (tests/test_oracle_torso.py):
 - torch's own rms_norm and silu (library routines);

@@ -17,6 +17,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -87,6 +88,8 @@ struct Scratch {
   Buf img, seq_raw, seq_cnt, gqa_part, zeros, duo_ring, sync_flags;
   unsigned sync_epoch = 0;  // the progress counters' epoch of the last launch that used them (they start at zero)
   unsigned gqa_epoch = 0;   // the split-GQA slot marks' epoch of the last launch (the marks start at zero)
+  // the engines holding this set (guarded by g_live_mu); all of them run on one stream, so their calls never overlap
+  std::vector<const ha_engine*> holders;
   ~Scratch() {
     (void)hipSetDevice(device);
     for (Buf* b : {&img, &seq_raw, &seq_cnt, &gqa_part, &zeros, &duo_ring, &sync_flags})
@@ -140,7 +143,11 @@ struct ha_engine {
   int img_chunks = 0, duo_slots = 0;
   int gqa_split = 0, gqa_part_slots = 0;
   hipEvent_t ev[2] = {nullptr, nullptr};
-  std::vector<hipEvent_t> lev;
+  std::vector<hipEvent_t> lev, mev;  // per-layer events: layer starts (and the end), ends of each layer's mixer kernels
+  // error word of this engine's launches (ha::WaitCheck): pinned, host-coherent memory that a kernel whose bounded
+  // wait ran out writes its bit into; read on the host without a copy, at the next call and after synchronisation
+  volatile unsigned* err_host = nullptr;
+  unsigned* err_dev = nullptr;
   int C = 0;
   bool any_linear = false, any_full = false;
 };
@@ -247,10 +254,17 @@ void free_engine(ha_engine* e) {
       if (p) (void)hipFree(p);
   }
   if (e->rope) (void)hipFree(e->rope);
+  if (e->scratch) {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    auto& hs = e->scratch->holders;
+    hs.erase(std::remove(hs.begin(), hs.end(), e), hs.end());
+  }
   e->scratch.reset();
   for (auto ev : e->ev) if (ev) (void)hipEventDestroy(ev);
   for (auto ev : e->lev) if (ev) (void)hipEventDestroy(ev);
+  for (auto ev : e->mev) if (ev) (void)hipEventDestroy(ev);
   if (e->own) (void)hipStreamDestroy(e->own);
+  if (e->err_host) (void)hipHostFree(const_cast<unsigned*>(e->err_host));
   void* spare = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_live_mu);
@@ -283,6 +297,22 @@ void free_snapshot_buffers(ha_snapshot* s) {
   s->block_bytes = 0;
 }
 
+// A bounded cross-workgroup wait of one of e's launches ran out (see ha::WaitCheck): report it once, as
+// HA_ERR_DEVICE, and clear the word. The engine.js counterpart throws the device errors a forward collected
+// (engine.js:373).
+int take_device_error(ha_engine* e) {
+  const unsigned v = *e->err_host;
+  if (!v) return HA_OK;
+  *e->err_host = 0u;
+  std::string what;
+  if (v & ha::kErrDuoWait) what += " a paired-form consumer gave up waiting for a tile set;";
+  if (v & ha::kErrSplitWait) what += " a split-form output workgroup gave up waiting for a packed state;";
+  if (v & ha::kErrGqaMerge) what += " a split-key attention merge gave up waiting for its pieces;";
+  if (what.empty()) what = " unknown code " + std::to_string(v) + ";";
+  return fail(HA_ERR_DEVICE, "device error in an earlier kernel of this engine (its outputs are undefined):" +
+                                 what.substr(0, what.size() - 1));
+}
+
 }  // namespace
 
 static_assert(ha::kMnbScratchBytes == HA_MNB_SCRATCH_BYTES, "ha.h states the no-allocation scratch size");
@@ -306,6 +336,20 @@ extern "C" {
 
 const char* ha_last_error(void) { return g_err.c_str(); }
 int ha_abi_version(void) { return HA_ABI_VERSION; }
+
+int ha_device_arch(int device, char* name, size_t bytes) {
+  if (!name || bytes == 0) return fail(HA_ERR_ARG, "name must be non-NULL with bytes > 0");
+  name[0] = 0;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(HA_ERR_DEVICE, "no HIP device is visible");
+  if (device < 0 || device >= ndev) return fail(HA_ERR_ARG, "no HIP device " + std::to_string(device));
+  hipDeviceProp_t p;
+  HA_HIP(hipGetDeviceProperties(&p, device));
+  std::string a(p.gcnArchName);
+  a = a.substr(0, a.find(':'));  // "gfx950:sramecc+:xnack-" -> "gfx950"
+  std::snprintf(name, bytes, "%s", a.c_str());
+  return HA_OK;
+}
 
 int ha_create(const ha_config* cfg, int device, ha_engine** out) {
   if (!out) return fail(HA_ERR_ARG, "out is NULL");
@@ -336,8 +380,20 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
   if (hipEventCreate(&e->ev[0]) != hipSuccess || hipEventCreate(&e->ev[1]) != hipSuccess)
     return bail(fail(HA_ERR_DEVICE, "hipEventCreate failed"));
   e->lev.assign(c.n_layers + 1, nullptr);
-  for (auto& ev : e->lev)
-    if (hipEventCreate(&ev) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipEventCreate failed"));
+  e->mev.assign(c.n_layers, nullptr);
+  for (auto* evs : {&e->lev, &e->mev})
+    for (auto& ev : *evs)
+      if (hipEventCreate(&ev) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipEventCreate failed"));
+  {
+    void* w = nullptr;
+    if (hipHostMalloc(&w, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+      return bail(fail(HA_ERR_NOMEM, "hipHostMalloc of the error word failed"));
+    e->err_host = static_cast<volatile unsigned*>(w);
+    *e->err_host = 0u;
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, w, 0) != hipSuccess) return bail(fail(HA_ERR_DEVICE, "hipHostGetDevicePointer failed"));
+    e->err_dev = static_cast<unsigned*>(d);
+  }
 
   e->layers.resize(c.n_layers);
   for (int i = 0; i < c.n_layers; i++) {
@@ -369,6 +425,10 @@ int ha_create(const ha_config* cfg, int device, ha_engine** out) {
   }
   e->scratch = std::make_shared<Scratch>();
   e->scratch->device = device;
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    e->scratch->holders.push_back(e);
+  }
   if (e->any_linear) {
     e->need_zeros = dtype_size(c.lin_dtype) * B * (kKC - 1) * c.lin_stride;
     // chunk images: every chunk a call can touch (max_ctx / 64, plus the replayed open chunk); allocated here only
@@ -426,13 +486,43 @@ int ha_destroy(ha_engine* e) {
 
 int ha_set_stream(ha_engine* e, void* stream) {
   if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
-  e->stream = stream ? static_cast<hipStream_t>(stream) : e->own;
+  hipStream_t to = stream ? static_cast<hipStream_t>(stream) : e->own;
+  if (to == e->stream) return HA_OK;
+  // Engines holding one set of call-time buffers must stay on one stream (their launches use the same progress
+  // counters and tile-set slots, and a newer epoch's counters would satisfy an older launch's waits at once). An
+  // engine that moves to another stream while the set is held by others gets a set of its own first.
+  bool shared = false;
+  {
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    for (const ha_engine* h : e->scratch->holders) shared |= h != e;
+  }
+  if (shared) {
+    HA_HIP(hipSetDevice(e->device));
+    HA_HIP(hipDeviceSynchronize());  // no queued call may still use the set being left
+    auto s = std::make_shared<Scratch>();
+    s->device = e->device;
+    const ha_config& c = e->cfg;
+    int rc;
+    if ((rc = grow(s->zeros, e->need_zeros)) || (rc = grow(s->seq_raw, e->need_seq_raw)) ||
+        (rc = grow(s->seq_cnt, e->need_seq_cnt)) || (rc = grow(s->sync_flags, e->need_sync_flags)) ||
+        (rc = grow(s->gqa_part, e->need_gqa)) || (rc = grow(s->img, split_by_shape(c) ? e->need_img : 0)) ||
+        (rc = grow(s->duo_ring, paired_by_shape(c) ? e->need_duo_ring : 0)))
+      return rc;
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    auto& hs = e->scratch->holders;
+    hs.erase(std::remove(hs.begin(), hs.end(), e), hs.end());
+    s->holders.push_back(e);
+    e->scratch = s;
+  }
+  e->stream = to;
   return HA_OK;
 }
 
 int ha_share_scratch(ha_engine* e, ha_engine* holder) {
   if (!engine_ok(e) || !engine_ok(holder)) return fail(HA_ERR_HANDLE, "invalid engine handle");
   if (e->device != holder->device) return fail(HA_ERR_ARG, "engines are on different devices");
+  if (e->stream != holder->stream)
+    return fail(HA_ERR_ARG, "engines sharing call-time buffers must run on one stream (ha_set_stream first)");
   if (e->scratch == holder->scratch) return HA_OK;
   HA_HIP(hipSetDevice(e->device));
   HA_HIP(hipDeviceSynchronize());  // no queued call of either engine may still use a buffer that is replaced
@@ -446,6 +536,10 @@ int ha_share_scratch(ha_engine* e, ha_engine* holder) {
       (rc = grow(to.duo_ring, from.duo_ring.bytes ? e->need_duo_ring : 0)) ||
       (rc = grow(to.sync_flags, e->need_sync_flags)))
     return rc;
+  std::lock_guard<std::mutex> lock(g_live_mu);
+  auto& hs = e->scratch->holders;
+  hs.erase(std::remove(hs.begin(), hs.end(), e), hs.end());
+  holder->scratch->holders.push_back(e);
   e->scratch = holder->scratch;
   return HA_OK;
 }
@@ -509,7 +603,14 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   if (mode == HA_CHUNKED_PAIRED && !ha::gdn_duo_fits(c.batch, c.H))
     return fail(HA_ERR_ARG, "the paired form needs batch * H a multiple of 8 and at most 128");
   const bool chunked = mode != HA_SEQUENTIAL;
-  const bool timing = opts && (opts->timestamps || opts->layer_ms);
+  const bool per_layer = opts && (opts->layer_ms || opts->mixer_ms);
+  const bool timing = opts && (opts->timestamps || per_layer);
+  // a bounded wait of an earlier call that ran out (its outputs are undefined) fails this call before it runs
+  if (int rc = take_device_error(e)) return rc;
+  ha::WaitCheck wait;
+  wait.err = e->err_dev;
+  const bool unpublished = opts && opts->debug_unpublished_waits;
+  if (unpublished) wait.polls = 4;
   HA_HIP(hipSetDevice(e->device));
   hipStream_t st = e->stream;
   const size_t B = c.batch;
@@ -569,7 +670,7 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   if (timing) HA_HIP(hipEventRecord(e->ev[0], st));
   for (int i = 0; i < c.n_layers; i++) {
     Layer& l = e->layers[i];
-    if (opts && opts->layer_ms) HA_HIP(hipEventRecord(e->lev[i], st));
+    if (per_layer) HA_HIP(hipEventRecord(e->lev[i], st));
     if (l.kind == HA_LINEAR_ATTENTION) {
       ha::GdnArgs a{};
       a.B = c.batch; a.H = c.H; a.DK = c.DK; a.DV = c.DV; a.KC = kKC; a.stride = c.lin_stride; a.C = e->C;
@@ -582,6 +683,9 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
       a.conv_w = l.conv; a.negA = l.negA; a.dtb = l.dtb; a.gnorm = c.lin_gnorm ? l.gnorm : nullptr;
       a.img = sc.img.p; a.img_chunks = e->img_chunks;
       a.seq_raw = static_cast<float*>(sc.seq_raw.p); a.seq_cnt = static_cast<unsigned*>(sc.seq_cnt.p);
+      // progress counter values are epoch << kDuoEpochShift | chunks: a skew of one epoch is never published
+      a.wait = wait;
+      if (unpublished) a.wait.skew = 1u << ha::kDuoEpochShift;
       hipError_t he;
       if (!chunked) {
         he = ha::launch_gdn_sequential(a, st);
@@ -599,8 +703,9 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
         he = ha::launch_gdn_chunked(a, st);
       }
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " gated-delta launch: " + hipGetErrorString(he));
+      if (per_layer) HA_HIP(hipEventRecord(e->mev[i], st));
       t.in[t.n] = a.in; t.tail[t.n] = a.tail; t.tail_out[t.n] = l.tail; t.n++;
-      if ((opts && opts->layer_ms) || t.n == ha::kTailLayers) {
+      if (per_layer || t.n == ha::kTailLayers) {
         he = flush_tails();
         if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " tail update: " + hipGetErrorString(he));
       }
@@ -620,15 +725,21 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
         }
         a.epoch = sc.gqa_epoch;
       }
+      // the merge waits for marks equal to this launch's epoch: epoch + 1 is never written by it
+      a.wait = wait;
+      if (unpublished) a.wait.skew = 1u;
       hipError_t he = ha::launch_gqa(a, st);
       if (he != hipSuccess) return fail(HA_ERR_DEVICE, "layer " + std::to_string(i) + " attention launch: " + hipGetErrorString(he));
-    }  // HA_ADAPTER: no token mixer, nothing to run
+      if (per_layer) HA_HIP(hipEventRecord(e->mev[i], st));
+    } else if (per_layer) {  // HA_ADAPTER: no token mixer, nothing to run
+      HA_HIP(hipEventRecord(e->mev[i], st));
+    }
   }
   if (t.n > 0) {
     const hipError_t he = flush_tails();
     if (he != hipSuccess) return fail(HA_ERR_DEVICE, std::string("tail update: ") + hipGetErrorString(he));
   }
-  if (opts && opts->layer_ms) HA_HIP(hipEventRecord(e->lev[c.n_layers], st));
+  if (per_layer) HA_HIP(hipEventRecord(e->lev[c.n_layers], st));
   if (timing) HA_HIP(hipEventRecord(e->ev[1], st));
 
   if (keep) {
@@ -693,9 +804,19 @@ int ha_forward(ha_engine* e, int L, const void* const* layer_in, void* const* la
   }
   if (timing || (opts && opts->sync)) {
     HA_HIP(hipStreamSynchronize(st));
+    if (int rc = take_device_error(e)) {
+      // this call's outputs are undefined: no snapshot of them is handed out
+      if (keep && *keep) {
+        (void)ha_snapshot_destroy(*keep);
+        *keep = nullptr;
+      }
+      return rc;
+    }
     if (opts && opts->timestamps) HA_HIP(hipEventElapsedTime(&opts->gpu_ms, e->ev[0], e->ev[1]));
     if (opts && opts->layer_ms)
       for (int i = 0; i < c.n_layers; i++) HA_HIP(hipEventElapsedTime(&opts->layer_ms[i], e->lev[i], e->lev[i + 1]));
+    if (opts && opts->mixer_ms)
+      for (int i = 0; i < c.n_layers; i++) HA_HIP(hipEventElapsedTime(&opts->mixer_ms[i], e->lev[i], e->mev[i]));
   }
   hipError_t le = hipGetLastError();
   if (le != hipSuccess) return fail(HA_ERR_DEVICE, std::string("device error: ") + hipGetErrorString(le));
@@ -742,7 +863,32 @@ int ha_snapshot_read(const ha_snapshot* s, int layer, const char* what, void* ho
   const void* src = nullptr;
   size_t want = 0;
   const bool lin = e->layers[layer].kind == HA_LINEAR_ATTENTION, full = e->layers[layer].kind == HA_FULL_ATTENTION;
-  if (lin && w == "state") { src = s->layers[layer].S; want = sizeof(float) * B * c.H * c.DK * c.DV; }
+  if (lin && w == "state" && s->s0 < s->P) {
+    // the state at P, as the reference's snapshot holds it (engine.js:352-356): the stored state advanced over the
+    // snapshot's replay rows [state_pos, P) by the sequential fp32 rule, into a temporary buffer
+    want = sizeof(float) * B * c.H * c.DK * c.DV;
+    if (bytes != want) return fail(HA_ERR_ARG, "expected " + std::to_string(want) + " bytes, got " + std::to_string(bytes));
+    HA_HIP(hipSetDevice(e->device));
+    float* tmp = nullptr;
+    int rc = dalloc(&tmp, want);
+    if (rc) return rc;
+    const Layer& l = e->layers[layer];
+    ha::GdnArgs a{};
+    a.B = c.batch; a.H = c.H; a.DK = c.DK; a.DV = c.DV; a.KC = kKC; a.stride = c.lin_stride; a.C = e->C;
+    a.P = s->P; a.L = 0; a.s0 = s->s0;
+    a.tail = s->layers[layer].tail; a.tail_cap = s->tail_rows;
+    a.dtype = c.lin_dtype == HA_F16 ? 1 : 0;
+    a.S_in = s->layers[layer].S; a.S_out = tmp;
+    a.conv_w = l.conv; a.negA = l.negA; a.dtb = l.dtb; a.gnorm = nullptr;  // no output rows: replay only
+    hipError_t he = ha::launch_gdn_sequential(a, e->stream);
+    if (he == hipSuccess) he = hipMemcpyAsync(host, tmp, want, hipMemcpyDeviceToHost, e->stream);
+    const hipError_t se = hipStreamSynchronize(e->stream);  // also before the free when a step above failed
+    if (he == hipSuccess) he = se;
+    (void)hipFree(tmp);
+    if (he != hipSuccess) return fail(HA_ERR_DEVICE, std::string("snapshot state at P: ") + hipGetErrorString(he));
+    return HA_OK;
+  }
+  if (lin && (w == "state" || w == "state_stored")) { src = s->layers[layer].S; want = sizeof(float) * B * c.H * c.DK * c.DV; }
   else if (lin && w == "tail") { src = s->layers[layer].tail; want = dtype_size(c.lin_dtype) * B * s->tail_rows * c.lin_stride; }
   else if (full && (w == "K" || w == "V")) {
     src = w == "K" ? (const void*)s->layers[layer].K : (const void*)s->layers[layer].V;
@@ -820,14 +966,14 @@ int ha_copy_to_host(ha_engine* e, void* host, const void* src, size_t bytes) {
   HA_HIP(hipSetDevice(e->device));
   HA_HIP(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, e->stream));
   HA_HIP(hipStreamSynchronize(e->stream));
-  return HA_OK;
+  return take_device_error(e);  // the copied outputs of a call whose wait ran out are undefined
 }
 
 int ha_synchronize(ha_engine* e) {
   if (!engine_ok(e)) return fail(HA_ERR_HANDLE, "invalid engine handle");
   HA_HIP(hipSetDevice(e->device));
   HA_HIP(hipStreamSynchronize(e->stream));
-  return HA_OK;
+  return take_device_error(e);
 }
 
 // ---- MatMulNBits projections ----

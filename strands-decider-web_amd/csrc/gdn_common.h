@@ -148,6 +148,12 @@ __device__ __forceinline__ f4 mfma16(const h8& a, const h8& b, const f4& c) {
 
 __device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
+// A bounded wait that ran out: its bit into the engine's host-visible error word (one system-scope vector store;
+// several such stores may race, and any non-zero value reports the failure).
+__device__ __forceinline__ void report_wait(const WaitCheck& w, unsigned bit) {
+  if (w.err) __hip_atomic_store(w.err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <int N>
 struct Width {
   static constexpr int value = N;

@@ -435,7 +435,7 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
 // ---------------------------------------------------------------------------------------------------------------
 // Consumer
 
-template <typename T>
+template <typename T, bool kDebugWaits>
 __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, ConsumerLds& sm, const char* ring,
                                         const unsigned* produced, unsigned* consumed, unsigned ep) {
   const int tid0 = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid0 >> 6);
@@ -501,10 +501,18 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     for (int q = 0; q < 4; q++) zn[q] = ld4(zr + 32 * q);
   };
   // chunk c's tile set from its slot into LDS: whole 1 KiB DMA instructions, helper wave wq issues every fourth. The
-  // producer is resident or done (it is dispatched first and waits for nothing), so the wait ends; its bound (2^16
-  // polls) only keeps the kernel finite.
+  // producer is resident or done (it is dispatched first and waits for nothing), so the wait ends; its bound only
+  // keeps the kernel finite. A wait that runs out sets `seen` to ~0u, a value no counter takes (the chunk field stays
+  // below 4095): the launch's outputs are undefined from there on, later waits pass at once, and the kernel's end
+  // reports it through the engine's error word (the test instantiation kDebugWaits waits with a.wait's skew and poll
+  // bound instead of none and kWaitPolls).
+  const unsigned epw = kDebugWaits ? ep + a.wait.skew : ep;
   auto dma_set = [&](int c, int wq) {
-    if (seen < ep + (unsigned)(c + 1)) seen = max(seen, wait_counter(produced, ep + (unsigned)(c + 1), 1 << 16));
+    const unsigned want = epw + (unsigned)(c + 1);
+    if (seen < want) {
+      const unsigned x = wait_counter(produced, want, kDebugWaits ? a.wait.polls : kWaitPolls);
+      seen = x >= want ? max(seen, x) : ~0u;
+    }
     const char* from = ring + (size_t)c * kDuoSetBytes;
     unsigned char* to = sm.s[c & 1].raw;
     const int ln = opaque(tid0) & 63;
@@ -710,12 +718,14 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
           gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16] = S[ct][it][e];
   }
   for (; p <= n; p++) period(p);
+  if (seen == ~0u && (tid0 & 63) == 0) report_wait(a.wait, kErrDuoWait);
 }
 
 // Blocks 16 i + r (r < 8, the producer) and 16 i + 8 + r (the consumer) form pair 8 i + r. The dispatcher hands
 // consecutive blocks to the XCDs in turn and each XCD takes its blocks in order, so both members of a pair share an
-// XCD (and its L2), and the producer comes first.
-template <typename T>
+// XCD (and its L2), and the producer comes first. kDebugWaits: the instantiation a test of the wait-failure report
+// launches (a.wait.skew != 0), whose consumer waits use a.wait's skew and poll bound.
+template <typename T, bool kDebugWaits>
 __global__ __launch_bounds__(kThreads) void gdn_duo_kernel(GdnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   const int blk = blockIdx.x;
@@ -726,14 +736,14 @@ __global__ __launch_bounds__(kThreads) void gdn_duo_kernel(GdnArgs a) {
   char* const ring = (char*)a.duo_ring + (size_t)pair * a.duo_slots * kDuoSetBytes;
   const unsigned ep = a.sync_epoch << kDuoEpochShift;
   if ((blk >> 3) & 1)
-    consume<T>(a, b, h, *reinterpret_cast<ConsumerLds*>(lds_raw), ring, produced, consumed, ep);
+    consume<T, kDebugWaits>(a, b, h, *reinterpret_cast<ConsumerLds*>(lds_raw), ring, produced, consumed, ep);
   else
     produce<T>(a, b, h, *reinterpret_cast<ProducerLds*>(lds_raw), ring, produced, consumed, ep);
 }
 
 template <typename T>
 hipError_t launch(const GdnArgs& a, hipStream_t s) {
-  auto k = gdn_duo_kernel<T>;
+  auto k = a.wait.skew ? gdn_duo_kernel<T, true> : gdn_duo_kernel<T, false>;
   const int lds = (int)(sizeof(ConsumerLds) > sizeof(ProducerLds) ? sizeof(ConsumerLds) : sizeof(ProducerLds));
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess) return e;

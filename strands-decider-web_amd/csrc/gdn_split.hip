@@ -648,12 +648,18 @@ __device__ __forceinline__ void out_pass(const GdnArgs& a, unsigned char* lds_ra
     }
   }
   // the packed state at the chunk's start, once the four state workgroups of this (sequence, head) have published it
-  // (at most 2^16 polls of about a microsecond: they are resident or done, so the wait ends)
+  // (a bounded number of polls of about a microsecond: they are resident or done, so the wait ends; one that runs out
+  // is reported through the engine's error word)
   if (tid == 0) {
-    const unsigned want = (a.sync_epoch << kDuoEpochShift) + (unsigned)(p + 1);
+    const unsigned want = (a.sync_epoch << kDuoEpochShift) + a.wait.skew + (unsigned)(p + 1);
     const unsigned* progress = a.sync_flags + (size_t)bh * 64;
-    for (int g = 0; g < kSG; g++)
-      for (int i = 0; i < (1 << 16) && ld_counter(progress + 16 * g) < want; i++) __builtin_amdgcn_s_sleep(2);
+    bool late = false;
+    for (int g = 0; g < kSG; g++) {
+      int i = 0;
+      for (; i < a.wait.polls && ld_counter(progress + 16 * g) < want; i++) __builtin_amdgcn_s_sleep(2);
+      late |= i == a.wait.polls;
+    }
+    if (late) report_wait(a.wait, kErrSplitWait);
   }
   __syncthreads();
   h8 Sb[4][2];

@@ -235,10 +235,18 @@ __device__ __forceinline__ void merge_block(const GqaArgs& a, int per_pair, int 
   const int slot0 = pair * per_pair + cum;
   const int tid = threadIdx.x;
   if (tid == 0) {
+    // bounded; a wait that runs out is reported through the engine's error word (a test's skew makes every mark
+    // this wait looks for one that no piece writes)
     const unsigned* marks = part_marks(a);
-    for (int j = 0; j < np; j++)
-      for (int i = 0; i < (1 << 16) && __hip_atomic_load(marks + slot0 + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != a.epoch; i++)
+    const unsigned want = a.epoch + a.wait.skew;
+    bool late = false;
+    for (int j = 0; j < np; j++) {
+      int i = 0;
+      for (; i < a.wait.polls && __hip_atomic_load(marks + slot0 + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want; i++)
         __builtin_amdgcn_s_sleep(2);
+      late |= i == a.wait.polls;
+    }
+    if (late && a.wait.err) __hip_atomic_store(a.wait.err, kErrGqaMerge, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   __syncthreads();
   const int b = pair / a.HK, h = (pair % a.HK) * 4 + hh;

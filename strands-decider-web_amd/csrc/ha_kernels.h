@@ -6,6 +6,24 @@
 
 namespace ha {
 
+// Cross-workgroup waits of one launch (the paired form's tile-set wait, the split form's packed-state wait, the split
+// GQA merge's wait for its pieces) are bounded: a workgroup polls at most `polls` times (about a microsecond each).
+// Every waited-for value is published by a workgroup that is resident or done, so in a correct launch a wait always
+// ends early. If one runs out anyway, the workgroup goes on (so the launch still ends), and stores its bit into
+// `*err`, a word in host-visible memory the engine checks after its next stream synchronisation and at its next
+// call, which then fail with HA_ERR_DEVICE.
+// `skew` is 0 except in tests of this path: a launch given a non-zero skew waits for values no workgroup of it ever
+// publishes (its waits give up after `polls` polls each, its outputs are undefined, every kernel still ends).
+constexpr unsigned kErrDuoWait = 1u;    // paired form: a consumer gave up waiting for a tile set
+constexpr unsigned kErrSplitWait = 2u;  // split form: an output workgroup gave up waiting for a packed state
+constexpr unsigned kErrGqaMerge = 4u;   // split-key GQA: a merge workgroup gave up waiting for its pieces
+constexpr int kWaitPolls = 1 << 16;
+struct WaitCheck {
+  unsigned* err = nullptr;  // host-visible error word (system-scope stores), or nullptr
+  unsigned skew = 0;
+  int polls = kWaitPolls;
+};
+
 // One gated-delta layer over absolute rows [s0, P + L) of `B` sequences.
 // Rows r < P come from `tail` (raw rows kept by the previous call: [s0 - (KC-1), P)), rows >= P from `in`.
 // The conv of row r reads rows r-3..r, so rows s0-3..s0-1 must be present in `tail` (zeros at the start of a
@@ -33,6 +51,7 @@ struct GdnArgs {
   unsigned* sync_flags;             // [B*H][64] progress counters between workgroups of one launch: paired form (produced
                                     // at 0, consumed at 32), split form (the state pass's workgroup g at 16 g)
   unsigned sync_epoch;              // this launch's counter epoch, >= 1 and increasing per flag buffer
+  WaitCheck wait;                   // bounded cross-workgroup waits: poll limit, test skew, error word
 };
 constexpr int kSegRows = 64;        // output rows per launch of the sequential form
 constexpr int kDuoSetBytes = 36 * 1024;   // bytes per tile-set slot of the paired form
@@ -59,6 +78,7 @@ struct GqaArgs {
   float* part;               // [slots][4][64][HD] unnormalised O, then [slots][4][64][2] (reference max, sum), then
                              // [slots] u32 epoch marks
   unsigned epoch;            // this launch's mark, >= 1 and different from every earlier launch's on `part`
+  WaitCheck wait;            // the merge workgroups' bounded wait for their pieces
 };
 
 // Slots of partial results the split GQA path needs for any call on a context of at most max_ctx positions.

@@ -2,7 +2,7 @@
 //
 // Reference: web/public/gemmbench/kernels.js:1-14 (weight formats) and 15-36 (block decode),
 // convert/export_engine.py:17-26 (int4 RTN export), web/public/engine/engine.js:236-246 (matmul dispatch) and
-// engine.js:17-33 (kernel choice by M), web/public/engine/wgsl.js:91-108 (FWHT input rotation).
+// engine.js:17-33 (kernel choice by M), web/public/engine/wgsl.js:94-110 (FWHT input rotation).
 //
 //   y[M][N] (f16) = a[M][K] (f16) x W^T, fp32 accumulation, W[n][k] dequantised from blocks of 32 consecutive k
 //   of one row n: 4 bits: 4 words per block, element e at bits 4(e%8) of word e/8 (MatMulNBits: element 2i in the
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(256) void mnb_split_sum_kernel(const float* ws, _Fl
 
 
 // In-place orthonormal Walsh-Hadamard transform (Sylvester order) of each contiguous n-block of an f16 row, one
-// workgroup per block (wgsl.js:91-108): the online input rotation of a tensor exported with `had: n`.
+// workgroup per block (wgsl.js:94-110): the online input rotation of a tensor exported with `had: n`.
 __global__ __launch_bounds__(256) void fwht_kernel(_Float16* x, int n, float scale) {
   extern __shared__ float sh[];
   _Float16* o = x + (size_t)blockIdx.x * n;

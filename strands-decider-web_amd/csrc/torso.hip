@@ -1,7 +1,7 @@
 // The rest of the torso's per-layer work around the token mixers and the projections, gfx950: the embedding
 // gather, the residual add + RMSNorm before each projection, the MLP's SiLU gate and an adapter layer's bias.
 //
-// Reference: web/public/engine/wgsl.js:42-61 (EMBED), 64-87 (ADD_NORM), 90-99 (SILU_MUL), 119-121 (ADD_BIAS), and
+// Reference: web/public/engine/wgsl.js:33-52 (EMBED), 55-78 (ADD_NORM), 81-90 (SILU_MUL), 113-121 (ADD_BIAS), and
 // their dispatch in Engine.plan(), web/public/engine/engine.js:247-281 (final-norm row gather: engine.js:283-284,
 // 342). All are HBM-bound: each element is read and written once, in 16-byte accesses.
 #include <hip/hip_runtime.h>

@@ -44,7 +44,8 @@ class HaMnbFormat(ctypes.Structure):
 
 class HaForwardOpts(ctypes.Structure):
     _fields_ = [("recurrence", ctypes.c_int), ("timestamps", ctypes.c_int), ("sync", ctypes.c_int),
-                ("gpu_ms", ctypes.c_float), ("layer_ms", ctypes.POINTER(ctypes.c_float))]
+                ("gpu_ms", ctypes.c_float), ("layer_ms", ctypes.POINTER(ctypes.c_float)),
+                ("mixer_ms", ctypes.POINTER(ctypes.c_float)), ("debug_unpublished_waits", ctypes.c_int)]
 
 
 _lib = None
@@ -182,7 +183,8 @@ class Engine:
         _check(_lib.ha_set_stream(self._h, ctypes.c_void_p(stream) if stream else None))
 
     def share_scratch(self, holder):
-        """Use `holder`'s call-time device buffers (ha_share_scratch); the two engines' calls must not overlap."""
+        """Use `holder`'s call-time device buffers (ha_share_scratch); both engines must already run on one stream
+        (set_stream), so that their calls never overlap."""
         _check(_lib.ha_share_scratch(self._h, holder._h))
 
     def set_param(self, layer, name, values):
@@ -192,13 +194,17 @@ class Engine:
                                  a.size))
 
     def forward(self, L, layer_in, layer_out, cache=None, keep_cache=False, recurrence=CHUNKED, timestamps=False,
-                layer_ms=False, sync=False):
+                layer_ms=False, sync=False, mixer_ms=False, debug_unpublished_waits=False):
+        """ha_forward. layer_ms / mixer_ms add per-layer GPU times (with / without the raw-row tail copy) to the
+        result; debug_unpublished_waits is the test-only option of ha_forward_opts (the call then fails with
+        HA_ERR_DEVICE once it is waited for)."""
         n = self.n_layers
         ins = (ctypes.c_void_p * n)(*[_ptr(x) for x in layer_in])
         outs = (ctypes.c_void_p * n)(*[_ptr(x) for x in layer_out])
         lm = (ctypes.c_float * n)() if layer_ms else None
+        mm = (ctypes.c_float * n)() if mixer_ms else None
         opts = HaForwardOpts(recurrence=recurrence, timestamps=int(timestamps), sync=int(sync), gpu_ms=0.0,
-                             layer_ms=lm)
+                             layer_ms=lm, mixer_ms=mm, debug_unpublished_waits=int(bool(debug_unpublished_waits)))
         keep = ctypes.c_void_p() if keep_cache else None
         rc = _lib.ha_forward(self._h, L, ins, outs, cache.handle if cache is not None else None,
                              ctypes.byref(keep) if keep_cache else None, ctypes.byref(opts))
@@ -208,6 +214,8 @@ class Engine:
             res["gpu_ms"] = opts.gpu_ms
         if layer_ms:
             res["layer_ms"] = list(lm)
+        if mixer_ms:
+            res["mixer_ms"] = list(mm)
         return res
 
     def synchronize(self):
@@ -264,7 +272,7 @@ class MnbWeight:
 
 
 def fwht(x, elems, n, device=0, stream=None):
-    """In-place orthonormal Walsh-Hadamard transform of each n-block of the f16 device array x (wgsl.js:91-108)."""
+    """In-place orthonormal Walsh-Hadamard transform of each n-block of the f16 device array x (wgsl.js:94-110)."""
     load_library()
     _check(_lib.ha_fwht(_ptr(x), elems, n, device, _ptr(stream) if stream is not None else None))
 
@@ -275,27 +283,27 @@ def _st(stream):
 
 def embed(table, L, ids, x, stream=None):
     """x[t] = f32 row ids[t] of the quantised embedding table `table` (an MnbWeight with N = table rows, K = hidden
-    size; wgsl.js:42-61). ids: L u32 on the device; an id outside the table gives a NaN row."""
+    size; wgsl.js:33-52). ids: L u32 on the device; an id outside the table gives a NaN row."""
     load_library()
     _check(_lib.ha_embed(table._h, L, _ptr(ids), _ptr(x), _st(stream)))
 
 
 def add_norm(R, D, nx, x, y, w, h, out_f32=False, rows=None, eps=1e-6, device=0, stream=None):
     """Residual add (x[s] += y[s] when y is given) then RMSNorm h[r] = x[s] rsqrt(mean(x[s]^2) + eps) w, with
-    s = rows[r] (identity when rows is None); h f16, or f32 with out_f32 (wgsl.js:64-87)."""
+    s = rows[r] (identity when rows is None); h f16, or f32 with out_f32 (wgsl.js:55-78)."""
     load_library()
     _check(_lib.ha_add_norm(R, D, nx, _ptr(x), _ptr(y), _ptr(w), _ptr(h), int(bool(out_f32)), _ptr(rows), eps,
                             device, _st(stream)))
 
 
 def silu_mul(L, I, big, mid, device=0, stream=None):
-    """mid[t][j] = silu(big[t][j]) * big[t][I + j] (f16; wgsl.js:90-99)."""
+    """mid[t][j] = silu(big[t][j]) * big[t][I + j] (f16; wgsl.js:81-90)."""
     load_library()
     _check(_lib.ha_silu_mul(L, I, _ptr(big), _ptr(mid), device, _st(stream)))
 
 
 def add_bias(L, N, y, c, device=0, stream=None):
-    """y[t][j] += c[j] (y f16, c f32; wgsl.js:119-121)."""
+    """y[t][j] += c[j] (y f16, c f32; wgsl.js:113-121)."""
     load_library()
     _check(_lib.ha_add_bias(L, N, _ptr(y), _ptr(c), device, _st(stream)))
 

@@ -158,6 +158,32 @@ function ptrOf(x) {
   throw new TypeError('layer buffers must be DeviceBuffer or BigInt device pointers');
 }
 
+/*
+ * Why HIP device `device` (default 0) cannot run the engine: an empty array if it can. The counterpart of the
+ * reference's adapter guard engineProblems(adapter) (engine.js:50-52, which asks for shader-f16): every kernel here
+ * is built for gfx950 only. The reference's subgroups32(adapter) chooses between two WGSL variants of one kernel; a
+ * gfx950 wavefront is 64 wide and there is one implementation, so it has no counterpart.
+ */
+function engineProblems(device) {
+  const d = device === undefined || device === null ? 0 : device;
+  let arch;
+  try {
+    arch = native.deviceArch(d);
+  } catch (e) {
+    return [e.message];
+  }
+  return arch === 'gfx950' ? [] : ['HIP device ' + d + ' is ' + arch + '; the kernels are built for gfx950 only'];
+}
+
+/*
+ * The projection kernel a forward over L rows runs: the name Torso.forward returns as `kernel`, like the reference's
+ * plan.kernel (its matmul kernel key chosen by L, engine.js:17-33,285,367). ha_mnb_forward reads the packed weights
+ * with a GEMV kernel up to 64 rows and runs the tiled MFMA GEMM beyond (include/ha.h).
+ */
+function projectionKernel(L) {
+  return L <= 64 ? 'mnb_gemv' : 'mnb_gemm';
+}
+
 class Engine {
   // The reference's Engine.create is async (engine.js:63); so is this one. opts: {device}
   static create(config, opts) {
@@ -246,7 +272,7 @@ class MatMulNBits {
 }
 
 // In-place orthonormal Walsh-Hadamard transform of every n-block of an f16 device buffer of `elems` values: the
-// input rotation of a weight exported with `had: n` (web/public/engine/wgsl.js:91-108), on the engine's stream.
+// input rotation of a weight exported with `had: n` (web/public/engine/wgsl.js:94-110), on the engine's stream.
 function fwht(engine, x, elems, n) {
   native.fwht(ptrOf(x), elems, n, engine ? engine.device : 0, engine ? engine._h : null);
 }
@@ -363,8 +389,8 @@ class Torso {
    *   timestamps: gpu_ms, the GPU time from the embedding to the final norm;
    *   debugLayers: layers[i - 1] = the residual stream x entering layer i >= 1 (f32 [L][D], after the residual add
    *     that opens the layer: the output of layer i - 1), read back between the layers.
-   * Returns {hidden: Float32Array(rows.length * D), d: D, cache, fetch_ms (host time of embedRows)[, gpu_ms][,
-   * layers]}.
+   * Returns {hidden: Float32Array(rows.length * D), d: D, kernel (the projection kernel, projectionKernel(L)), cache,
+   * fetch_ms (host time of embedRows)[, gpu_ms][, layers]}.
    */
   forward(ids, rows, options) {
     const o = options || {};
@@ -427,7 +453,7 @@ class Torso {
         snap = { P: (cache ? cache.P : 0) + L, ids: (cache ? cache.ids : []).concat(Array.from(ids)), layers: snaps,
           release: function () { snaps.forEach((s) => { if (s) s.release(); }); } };
       }
-      const res = { hidden: out, d: D, cache: snap, fetch_ms: fetchMs };
+      const res = { hidden: out, d: D, kernel: projectionKernel(L), cache: snap, fetch_ms: fetchMs };
       if (timer) res.gpu_ms = native.timerElapsed(timer, 0, 1);
       if (debug) res.layers = layers;
       return res;
@@ -507,4 +533,6 @@ module.exports = {
   CHUNKED_SPLIT: CHUNKED_SPLIT,
   CHUNKED_PAIRED: CHUNKED_PAIRED,
   abiVersion: native.abiVersion,
+  engineProblems: engineProblems,
+  projectionKernel: projectionKernel,
 };

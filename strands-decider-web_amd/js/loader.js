@@ -213,4 +213,33 @@ function initLazyEmbed(torso, dir, manifest, o) {
   return E;
 }
 
-module.exports = { loadTorso: loadTorso, decodeScales: decodeScales, unpackShard: unpackShard };
+/*
+ * Engine.create(base, {onProgress, fetchShard, subgroups, maxCtx, device}) -> Promise<Torso>: the reference's async
+ * constructor (engine.js:63-87) over an export at `base`. It throws, as the reference does, when the device cannot run
+ * the engine (engineProblems). fetchShard(url, path, wire) may return a shard's bytes or a promise of them (a
+ * download, as the reference's option); by default shards are read from `base` on the file system. Every shard and the
+ * lazy embedding's bundle are fetched before the torso is built from them (loadTorso), and onProgress(path) is called
+ * once per shard after it is on the device. subgroups is accepted and has no effect (one implementation).
+ */
+const Engine = {
+  create: async function (base, opts) {
+    const o = opts || {};
+    const problems = ha.engineProblems(o.device || 0);
+    if (problems.length) throw new Error("this GPU can't run the engine: " + problems.join(', '));
+    const manifest = JSON.parse(fs.readFileSync(path.join(base, 'manifest.json'), 'utf8'));
+    const fetched = new Map();
+    const want = manifest.shards.map((s) => [s.path, s.wire]);
+    if (manifest.embed) want.push([manifest.embed.bundle, undefined]);
+    for (const [p, wire] of want) {
+      const data = o.fetchShard ? await o.fetchShard(base + '/' + p, p, wire) : readFile(base, p);
+      fetched.set(p, data instanceof Uint8Array ? data : new Uint8Array(data));
+    }
+    return loadTorso(base, { maxCtx: o.maxCtx, device: o.device, onProgress: o.onProgress,
+      readShard: (p) => {
+        if (!fetched.has(p)) throw new Error('shard ' + p + ' was not fetched');
+        return fetched.get(p);
+      } });
+  },
+};
+
+module.exports = { Engine: Engine, loadTorso: loadTorso, decodeScales: decodeScales, unpackShard: unpackShard };

@@ -22,10 +22,13 @@ typedef struct engine_box {
   int kind;
   ha_engine* e;
   /* shareStream: the engine whose stream this one runs on, held by a strong reference so that it cannot be
-     collected (and its stream destroyed) while this engine lives; and how many engines run on this one's stream */
+     collected (and its stream destroyed) while this engine lives; and the engines that run on this one's stream.
+     Links are dropped from both ends: at environment teardown Node finalizes in no set order, so an owner finalized
+     before its borrowers first moves each of them back to its own stream and clears their link to it. */
   napi_ref stream_owner;
   struct engine_box* owner_box;
-  int borrowers;
+  struct engine_box** borrower;
+  int borrowers, borrower_cap;
 } engine_box;
 
 typedef struct {
@@ -160,21 +163,49 @@ static int get_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
 
 /* ---- finalizers ---- */
 
-/* drop an engine's link to the engine whose stream it borrowed */
+/* drop an engine's link to the engine whose stream it borrowed (the owner is alive while the link exists) */
 static void unshare_stream(napi_env env, engine_box* b) {
-  if (b->stream_owner) {
-    if (b->owner_box) b->owner_box->borrowers--;
-    napi_delete_reference(env, b->stream_owner);
-    b->stream_owner = NULL;
-    b->owner_box = NULL;
+  engine_box* o = b->owner_box;
+  if (o) {
+    for (int i = 0; i < o->borrowers; i++)
+      if (o->borrower[i] == b) {
+        o->borrower[i] = o->borrower[--o->borrowers];
+        break;
+      }
   }
+  if (b->stream_owner) napi_delete_reference(env, b->stream_owner);
+  b->stream_owner = NULL;
+  b->owner_box = NULL;
+}
+
+static int add_borrower(engine_box* o, engine_box* b) {
+  if (o->borrowers == o->borrower_cap) {
+    const int cap = o->borrower_cap ? 2 * o->borrower_cap : 4;
+    engine_box** p = (engine_box**)realloc(o->borrower, (size_t)cap * sizeof(engine_box*));
+    if (!p) return 0;
+    o->borrower = p;
+    o->borrower_cap = cap;
+  }
+  o->borrower[o->borrowers++] = b;
+  return 1;
 }
 
 static void engine_finalize(napi_env env, void* data, void* hint) {
   (void)hint;
   engine_box* b = (engine_box*)data;
-  if (b->e) ha_destroy(b->e);
+  /* engines still running on this one's stream (only at environment teardown, where finalizers run in no set
+     order; destroy() refuses otherwise): back to their own streams before that stream goes away */
+  for (int i = 0; i < b->borrowers; i++) {
+    engine_box* x = b->borrower[i];
+    if (x->e) ha_set_stream(x->e, NULL);
+    if (x->stream_owner) napi_delete_reference(env, x->stream_owner);
+    x->stream_owner = NULL;
+    x->owner_box = NULL;
+  }
+  b->borrowers = 0;
   unshare_stream(env, b);
+  if (b->e) ha_destroy(b->e);
+  free(b->borrower);
   free(b);
 }
 
@@ -274,7 +305,9 @@ static napi_value js_create(napi_env env, napi_callback_info info) {
   b->e = e;
   b->stream_owner = NULL;
   b->owner_box = NULL;
+  b->borrower = NULL;
   b->borrowers = 0;
+  b->borrower_cap = 0;
   napi_value r;
   if (napi_create_external(env, b, engine_finalize, NULL, &r) != napi_ok) {
     ha_destroy(e);
@@ -724,20 +757,26 @@ static napi_value js_share_stream(napi_env env, napi_callback_info info) {
   engine_box* b = get_engine(env, argv[1]);
   if (!a || !a->e || !b || !b->e) return type_error(env, "both arguments must be live engine handles");
   if (a == b) return type_error(env, "an engine cannot borrow its own stream");
-  void* st = NULL;
+  if (b->owner_box == a) return type_error(env, "the other engine runs on this engine's stream");
+  void *st = NULL, *was = NULL;
   CHECK_HA(ha_get_stream(b->e, &st));
-  CHECK_HA(ha_share_scratch(a->e, b->e));
+  CHECK_HA(ha_get_stream(a->e, &was));
   napi_ref ref;
   CHECK_NAPI(napi_create_reference(env, argv[1], 1, &ref));
+  /* the stream first: engines holding one set of call-time buffers must already share a stream */
   int rc = ha_set_stream(a->e, st);
+  if (!rc && (rc = ha_share_scratch(a->e, b->e)) != 0) (void)ha_set_stream(a->e, was);
   if (rc) {
     napi_delete_reference(env, ref);
     return throw_status(env, rc);
   }
   unshare_stream(env, a);
+  if (!add_borrower(b, a)) {
+    napi_delete_reference(env, ref);
+    return type_error(env, "out of host memory");
+  }
   a->stream_owner = ref;
   a->owner_box = b;
-  b->borrowers++;
   return NULL;
 }
 
@@ -805,12 +844,26 @@ static napi_value js_add_bias(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* deviceArch(device) -> "gfx950" (the name ha_device_arch reports) */
+static napi_value js_device_arch(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  int32_t dev;
+  if (napi_get_value_int32(env, argv[0], &dev) != napi_ok) return type_error(env, "device must be an integer");
+  char name[64];
+  CHECK_HA(ha_device_arch(dev, name, sizeof(name)));
+  napi_value r;
+  CHECK_NAPI(napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &r));
+  return r;
+}
+
 static napi_value init(napi_env env, napi_value exports) {
   const struct {
     const char* name;
     napi_callback fn;
   } fns[] = {
       {"abiVersion", js_abi_version},       {"lastError", js_last_error},
+      {"deviceArch", js_device_arch},
       {"create", js_create},                {"destroy", js_destroy},
       {"setParam", js_set_param},           {"forward", js_forward},
       {"snapshotTokens", js_snapshot_tokens}, {"snapshotLayout", js_snapshot_layout},

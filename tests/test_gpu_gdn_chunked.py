@@ -37,6 +37,28 @@ def test_config0_chunked(gnorm, mode):
     assert snap.state_pos == 64 and snap.tail_rows == 3
 
 
+@pytest.mark.parametrize("T", [100, 64 + 1, 130])
+def test_snapshot_state_at_P(T, mode):
+    # the snapshot's "state" is the state after all P = T rows, as the reference's snapshot holds it (engine.js:352),
+    # although the stored state sits at the last 64-row boundary ("state_stored", what a resume starts from)
+    x = gdn_inputs(T, 2, seed=13)
+    p = synth.gdn_params(seed=13)
+    r = Runner(["linear_attention"], batch=2)
+    r.set_params(0, p)
+    _, snap = r.forward([x], keep=True, recurrence=mode)
+    assert snap.state_pos == 64 * (T // 64) < T
+    _, st_P = oracle_gdn(x, p)
+    _, st_s = oracle_gdn(x[:, :snap.state_pos], p)
+    at_P = _state(snap, 2)
+    stored = np.zeros_like(at_P)
+    snap.read(0, "state_stored", stored)
+    e_P = rel_err(at_P, np.stack([s.S for s in st_P]))
+    e_s = rel_err(stored, np.stack([s.S for s in st_s]))
+    print("T=%d state at P vs fp64 %.2e, stored state at %d vs fp64 %.2e" % (T, e_P, snap.state_pos, e_s))
+    assert e_P < TOL and e_s < TOL
+    snap.release()
+
+
 def test_config2_T2048_against_oracle_and_sequential(mode):
     # one gated-delta layer at T=2048 with the T=64 case's input distributions; chunked result vs the sequential fp32 recurrence
     x = gdn_inputs(2048, seed=7)

@@ -24,8 +24,11 @@ CONFIG = {"hidden_size": D, "intermediate_size": I, "num_hidden_layers": len(TYP
 ROWS = [[0, 20, 39], [0, 29]]
 
 
-@pytest.mark.parametrize("form", ["plain", "wire", "lazy"])
+@pytest.mark.parametrize("form", ["plain", "wire", "lazy", "lazy-create"])
 def test_loaded_export_matches_the_arrays(tmp_path, form):
+    # "lazy-create": the lazy export through the async Engine.create(base, {onProgress, fetchShard}) (engine.js:63-87)
+    create = form.endswith("-create")
+    form = form.replace("-create", "")
     W, V, M = _model(seed=21)
     Vall = dict(V)
     for i, k, x in M:
@@ -42,11 +45,14 @@ def test_loaded_export_matches_the_arrays(tmp_path, form):
         json.dump(ROWS, f)
     print("loader: %s export, %d shard files" % (form, len([p for p in os.listdir(exp) if p.startswith(("weights", "wire"))])),
           flush=True)
-    r = subprocess.run([shutil.which("node"), os.path.join(ROOT, "tests", "js", "napi_loader.js"), exp, work],
-                       capture_output=True, text=True, timeout=300)
+    r = subprocess.run([shutil.which("node"), os.path.join(ROOT, "tests", "js", "napi_loader.js"), exp, work] +
+                       (["create"] if create else []), capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     info = json.loads(r.stdout.strip().splitlines()[-1])
     assert info["ok"] and info["shards"] > 1
+    # the projection kernel of each forward (40 and 30 rows: the packed-weight GEMV), as the reference's plan.kernel;
+    # and the device guard finds nothing to object to on this GPU
+    assert info["kernels"] == ["mnb_gemv", "mnb_gemv"] and info["problems"] == []
     if form == "lazy":
         assert info["evictions"] == 1  # the second forward found the 40 slots full and refilled them
     js = [np.fromfile(os.path.join(work, "hidden%d.bin" % k), np.float32).reshape(len(ROWS[k]), D) for k in (0, 1)]

@@ -31,12 +31,13 @@ def _params():
     return [synth.gdn_params(seed=5, layer=0), synth.gqa_params(seed=5, layer=1, noise=0.1)]
 
 
-def test_node_forward_resume_release(tmp_path):
+@pytest.mark.parametrize("rec", [ha.CHUNKED, ha.CHUNKED_PAIRED], ids=["default-split", "paired"])
+def test_node_forward_resume_release(tmp_path, rec):
     d = str(tmp_path)
     params = _params()
-    # the engine's default form for B * H = 32 (the paired form) in both hosts, while this process is alive and has
-    # run that form itself
-    rec = ha.CHUNKED
+    # the same recurrence in both hosts, while this process is alive and has run that form itself: the engine's
+    # default for B * H = 32 (the split form) and the paired form (the default from B * H = 48 on, the form of the
+    # B = 8 stack)
     spec = {"kinds": KINDS, "batch": B, "maxCtx": 4096, "T0": T0, "T1": T1, "params": [], "recurrence": rec}
     for i, p in enumerate(params):
         names = {}

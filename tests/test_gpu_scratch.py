@@ -64,3 +64,29 @@ def test_shared_scratch_is_bit_identical_and_lazy_images_match_the_oracle():
     e = rel_err(own[3], ref)
     print("forced split form at B=4 vs fp64: %.2e" % e)
     assert e < 2e-3
+
+
+def test_engines_sharing_a_set_stay_on_one_stream():
+    # engines holding one set of call-time buffers use the same progress counters and tile-set slots, so they must
+    # never run on two streams at once: sharing needs one stream, and an engine that moves to another stream gets a
+    # set of its own first; its calls then compute what they computed before
+    import torch
+    lin1, lin4, _ = _engines(torch, share=False)
+    s1 = torch.cuda.Stream(device="cuda:0").cuda_stream
+    s2 = torch.cuda.Stream(device="cuda:0").cuda_stream
+    lin1.eng.set_stream(s1)
+    lin4.eng.set_stream(s2)
+    with pytest.raises(ha.HAError) as ei:
+        lin4.eng.share_scratch(lin1.eng)
+    assert ei.value.code == ha.HA_ERR_ARG
+    x4 = gdn_inputs(130, 4, seed=4)
+    want = lin4.forward([x4])[0][0]
+    lin4.eng.set_stream(s1)
+    lin4.eng.share_scratch(lin1.eng)
+    assert np.array_equal(lin4.forward([x4])[0][0], want)
+    lin4.eng.set_stream(s2)  # leaves lin1's set for one of its own
+    assert np.array_equal(lin4.forward([x4])[0][0], want)
+    x1 = gdn_inputs(300, seed=3)
+    a = lin1.forward([x1])[0][0]
+    lin1.eng.set_stream(None)  # lin1 holds its set alone now: it keeps it
+    assert np.array_equal(lin1.forward([x1])[0][0], a)

@@ -24,6 +24,7 @@ out.cfg = m.configFromManifest({layer_types: ['linear_attention', 'linear_attent
 try { m.configFromManifest({layer_types: ['mamba']}); } catch (e) { out.bad_kind = e.message; }
 out.adapter = m.configFromManifest({layer_types: ['linear_attention', 'adapter', 'full_attention']}).layerKinds;
 try { m.Engine.createSync(out.cfg, {device: 0}); out.created = true; } catch (e) { out.err = [e.code, e.message]; }
+out.problems = m.engineProblems(0);
 const nat = require(require('path').join(require('path').dirname(%r), 'ha_napi.node'));
 try { nat.mnbForward({}, 1, BigInt(0), BigInt(0), null); } catch (e) { out.bad_handle = e.name + ': ' + e.message; }
 try { new m.MatMulNBits(null, 16, 2048, BigInt(16), BigInt(16), null, {bits: 5}); } catch (e) { out.bad_shape = e.code; }
@@ -43,9 +44,10 @@ def _run():
 
 def test_addon_loads_and_maps_manifest_config():
     out = _run()
-    assert out["abi"] == 1
+    with open(os.path.join(ROOT, "include", "ha.h")) as f:
+        assert "#define HA_ABI_VERSION %d\n" % out["abi"] in f.read()
     assert {"Engine", "Snapshot", "DeviceBuffer", "configFromManifest", "CHUNKED", "SEQUENTIAL", "MatMulNBits",
-            "fwht"} <= set(out["exports"])
+            "fwht", "engineProblems", "projectionKernel"} <= set(out["exports"])
     # a handle of the wrong kind is a TypeError from the addon, not a crash
     assert out["bad_handle"] == "TypeError: not a MatMulNBits handle"
     # format checks come before any device access (bits 5): HA_ERR_ARG
@@ -67,3 +69,5 @@ def test_create_without_device_throws_with_status_code():
     assert out["err"][0] == "HA_4" and "no HIP device" in out["err"][1]
     assert out["no_dev"] == "HA_4"  # ha_mnb_create: the device query fails without a GPU, as for the engine
     assert out["async"] == "HA_4"
+    # the adapter guard's counterpart (engine.js:50-52) names the reason instead of throwing
+    assert out["problems"] == ["no HIP device is visible"]

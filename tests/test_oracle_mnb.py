@@ -1,6 +1,6 @@
 """Pins of the MatMulNBits oracle (oracle/mnb_oracle.py) on the CPU: the weight formats of
 web/public/gemmbench/kernels.js:1-14, the exporter's int4 quantiser (convert/export_engine.py:17-26) and the FWHT
-input rotation (web/public/engine/wgsl.js:91-108)."""
+input rotation (web/public/engine/wgsl.js:94-110)."""
 import os
 import sys
 
