@@ -135,17 +135,6 @@ def time_forwards(torch, eng, T, ins, outs, steps, warmup, stream):
     return wall, e0.elapsed_time(e1) / steps
 
 
-def mixer_launch_ms(eng, T, ins, outs, n=30, warmup=3, **kw):
-    """Median over n forwards of a one-layer engine of its token-mixer kernels' GPU time alone: HIP events that
-    ha_forward records on the launch stream right before the layer's first kernel and right after its last
-    (ha_forward_opts.mixer_ms; the raw-row tail copy is outside them). The kernel durations a rocprofv3 kernel trace of
-    `bench.py --profile-kernel gdn|gqa` reports for the same launches add up to this."""
-    for _ in range(warmup):
-        eng.forward(T, ins, outs, **kw)
-    ts = sorted(eng.forward(T, ins, outs, mixer_ms=True, **kw)["mixer_ms"][0] for _ in range(n))
-    return ts[n // 2]
-
-
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -467,9 +456,21 @@ def main():
         print(json.dumps({"profile_kernel": "mnb", "steps": args.steps, "result": res,
                           "wall_s": round(time.perf_counter() - t0, 2)}), flush=True)
         return
-    if args.profile_kernel:
+    if args.profile_kernel in ("gdn", "gqa"):
+        # exactly the bench line's roofline leg (same engine and seeds): --warmup forwards, then --steps forwards
+        # back to back timed by HIP events on the launch stream; a kernel trace of this command covers those launches
         kind = "full_attention" if args.profile_kernel == "gqa" else "linear_attention"
-        rec = ha.SEQUENTIAL if args.profile_kernel == "gdn-seq" else ha.CHUNKED
+        B = args.profile_batch
+        with torch.cuda.stream(stream):
+            e = make_engine(ha, [kind], B, 4096, stream.cuda_stream)
+            i, o = make_buffers(torch, [kind], B, T, seed=1 if kind == "linear_attention" else 2)
+            _, ms = time_forwards(torch, e, T, i, o, args.steps, args.warmup, stream)
+        print(json.dumps({"profile_kernel": args.profile_kernel, "B": B, "T": T, "warmup": args.warmup,
+                          "steps": args.steps, "ms_per_launch": round(ms, 5)}), flush=True)
+        return
+    if args.profile_kernel:
+        kind = "linear_attention"
+        rec = ha.SEQUENTIAL
         B = args.profile_batch
         with torch.cuda.stream(stream):
             e = make_engine(ha, [kind], B, 4096, stream.cuda_stream)
@@ -501,15 +502,14 @@ def main():
         # stream
         e1 = make_engine(ha, ["linear_attention"], B, 4096, stream.cuda_stream)
         i1, o1 = make_buffers(torch, ["linear_attention"], B, T, seed=1)
-        gdn_launch_ms = mixer_launch_ms(e1, T, i1, o1)
-        _, gdn_layer_ms = time_forwards(torch, e1, T, i1, o1, 30, 3, stream)
+        _, gdn_launch_ms = time_forwards(torch, e1, T, i1, o1, 30, 3, stream)
         gdn_bytes = B * T * gdn_bytes_per_token() + B * H * DK * DV * 4  # + final state write
         achieved = gdn_bytes / (gdn_launch_ms * 1e-3) / 1e9
         del e1, i1, o1
         # GQA layer (K/V prep + attention kernels) against the dense f16 MFMA peak
         e2 = make_engine(ha, ["full_attention"], B, 4096, stream.cuda_stream)
         i2, o2 = make_buffers(torch, ["full_attention"], B, T, seed=2)
-        gqa_launch_ms = mixer_launch_ms(e2, T, i2, o2)
+        _, gqa_launch_ms = time_forwards(torch, e2, T, i2, o2, 30, 3, stream)
         gqa_tf = B * gqa_flops(T) / (gqa_launch_ms * 1e-3) / 1e12
         del e2, i2, o2
         torch.cuda.empty_cache()
@@ -549,11 +549,15 @@ def main():
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": gdn_bytes, "bytes_per_token": gdn_bytes_per_token(),
-                     "launch_ms": round(gdn_launch_ms, 5), "layer_ms_with_tail_copy": round(gdn_layer_ms, 5)},
+                     "launch_ms": round(gdn_launch_ms, 5),
+                     "timing": "30 back-to-back one-layer forwards after 3 warm-up, HIP events on the launch stream; "
+                               "includes the layer's 3-row tail copy kernel (about 2% of it)"},
         "roofline_gqa": {"bound": "mfma", "kernel": "gqa_kv_kernel + gqa_attn_kernel",
                          "achieved": round(gqa_tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": round(gqa_tf / 2500.0, 4), "flops_per_launch": B * gqa_flops(T),
-                         "launch_ms": round(gqa_launch_ms, 5)},
+                         "launch_ms": round(gqa_launch_ms, 5),
+                         "timing": "30 back-to-back one-layer forwards after 3 warm-up, HIP events on the launch "
+                                   "stream"},
         "sweep": sweep,
     }
     if not args.no_decode:

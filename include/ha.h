@@ -78,7 +78,8 @@ typedef struct ha_config {
   /* gated-delta layers: linear_num_key_heads (= value heads), linear_key_head_dim, linear_value_head_dim,
      linear_conv_kernel_dim */
   int H, DK, DV, conv_k;
-  int lin_stride;   /* row stride (elements) of the fused in_proj rows qkv | z | a | b (8256 in the engine) */
+  int lin_stride;   /* row stride (elements) of the fused in_proj rows qkv | z | a | b (8256 in the engine); a
+                       multiple of 8, so every head's 128-channel row segment is 16-byte aligned */
   int lin_dtype;    /* ha_dtype of linear-layer input rows and outputs */
   int lin_gnorm;    /* 1: output the gated RMSNorm (GNORM, the engine's layer output); 0: the raw core output */
   /* full-attention layers: num_attention_heads, num_key_value_heads, head_dim, rotary_dim */

@@ -216,6 +216,7 @@ int check_config(const ha_config* c) {
     const int C = 2 * c->H * c->DK + c->H * c->DV;
     if (c->lin_stride < C + c->H * c->DV + 2 * c->H)
       return fail(HA_ERR_ARG, "lin_stride smaller than the fused row qkv | z | a | b");
+    if (c->lin_stride % 8) return fail(HA_ERR_ARG, "lin_stride must be a multiple of 8 (16-byte row segments)");
     if (c->lin_dtype != HA_F32 && c->lin_dtype != HA_F16) return fail(HA_ERR_ARG, "lin_dtype must be HA_F32 or HA_F16");
   }
   if (full) {

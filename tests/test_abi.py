@@ -43,6 +43,7 @@ def _cfg(**over):
     (dict(DK=64), "d_k = d_v = 128"),
     (dict(conv_k=3), "conv kernel 4"),
     (dict(lin_stride=8000), "lin_stride"),
+    (dict(lin_stride=8260), "multiple of 8"),
     (dict(HQ=6), "4 query heads per KV head"),
     (dict(HD=128), "head_dim 256"),
     (dict(rot_dim=48), "rotary_dim"),
