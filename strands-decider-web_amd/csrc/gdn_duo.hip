@@ -15,10 +15,12 @@
 //   producer: everything that does not depend on the state, chunk by chunk: q/k conv + SiLU + l2 norm, the gates, the
 //     A and score tiles, T = (I + A)^-1, T diag(beta) and T diag(beta e^gc). In one period wave 0 runs chunk q's T
 //     chain, waves 1..2 its score tiles, wave 3 chunk q + 1's gates, waves 4..7 chunk q + 1's q/k conv, and waves
-//     1..3 copy chunk q - 1's finished tile set (36 KiB) into that chunk's slot in device memory.
+//     1..3 copy chunk q - 1's finished tile set (22.25 KiB: q^, k^, the three [32][32] tiles and two gate vectors,
+//     no padding) into that chunk's slot in device memory.
 //   consumer: waves 0..3 own 32 value columns each of the fp32 state in MFMA accumulators and do the state work of
-//     chunk p; meanwhile waves 4..7 (helpers) DMA chunk p + 1's tile set from its slot into LDS, apply the gated
-//     RMSNorm to chunk p - 1's output and store it, and run chunk p + 1's v conv.
+//     chunk p, each first transposing a quarter of k^ into a shared k^T (an LDS counter orders those writes before
+//     the state update reads them); meanwhile waves 4..7 (helpers) DMA chunk p + 1's tile set from its slot into
+//     LDS, apply the gated RMSNorm to chunk p - 1's output and store it, and run chunk p + 1's v conv.
 // Each role passes one workgroup barrier per period.
 // The two exchange progress through counters: `produced` (tile sets in their slots) and `consumed` (sets copied into
 // the consumer's LDS). Counter values carry a per-launch epoch (epoch << kDuoEpochShift | chunks), so values left by
@@ -51,48 +53,72 @@ constexpr int kLead = 24;       // chunks the producer may run ahead of the cons
 // z rows (4) and the counter (1). s_waitcnt with vmcnt = kAfterDma (expcnt and lgkmcnt not waited for) then covers
 // the DMA alone.
 constexpr int kAfterDma = kKC + 7 + 4 + 1;
-constexpr int kWaitDma = (kAfterDma & 15) | ((kAfterDma >> 4) << 14) | (7 << 4) | (15 << 8);
+// s_waitcnt operand that waits until at most n vector memory instructions are outstanding (expcnt, lgkmcnt: no wait)
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitDma = wait_vm(kAfterDma);
 
 typedef int i4v __attribute__((ext_vector_type(4)));
 
 // One chunk's tiles, as the producer builds them in LDS and the consumer reads them; copied between the two as bytes.
+// No padding: the row layouts are swizzled in 8-half (16-byte) units instead (qk_at, sq_at), so the whole set is data.
 struct Set {
-  _Float16 Qs[kC * kQP];   // q^ / sqrt(DK), [t][i]
-  _Float16 Ks[kC * kQP];   // k^, [t][i]
-  _Float16 KT[kDK * kP];   // k^ transposed, [i][t], 8-column groups swizzled by kt32
-  _Float16 Tb[kC * kP];    // T diag(beta), [t][t'] (the block above the diagonal stays zero)
-  _Float16 Tw[kC * kP];    // T diag(beta e^gc)
-  _Float16 Att[kC * kP];   // decay-masked causal q^ k^T
-  float gc[kC];            // cumulative log decay inside the chunk
+  _Float16 Qs[kC * kDK];   // q^ / sqrt(DK), [t][i], by qk_at
+  _Float16 Ks[kC * kDK];   // k^, [t][i], by qk_at
+  _Float16 Tb[kC * kC];    // T diag(beta), [t][t'], by sq_at (the block above the diagonal stays zero)
+  _Float16 Tw[kC * kC];    // T diag(beta e^gc), by sq_at
+  _Float16 Att[kC * kC];   // decay-masked causal q^ k^T, by sq_at
   float eg[kC];            // e^gc
-  float bt[kC];            // beta
   float ed[kC];            // e^(gc_31 - gc)
-  float rowf[kC];          // e^(gc_t - gc_16(t/16)), in (0, 1]
-  float brow[kC];          // beta_t rowf_t
-  float colf[kC];          // e^(gc_16 - gc_t') for t' < 16, in (0, 1]
 };
 static_assert(sizeof(Set) <= kDuoSetBytes, "a tile set fits one ring slot");
+static_assert(sizeof(Set) % 16 == 0 && sizeof(Set) / 16 > 22 * 64 && sizeof(Set) / 16 <= 23 * 64,
+              "the producer's copy (7 + 8 + 8 instructions of 64 units) and the consumer's DMA (23 of 1 KiB) cover the set");
 static_assert(kDuoSetBytes % 1024 == 0, "ring slots are whole 1 KiB DMA instructions");
 union SetBuf {
   Set s;
   unsigned char raw[kDuoSetBytes];
 };
+// The gate vectors only the producer reads
+struct Gates {
+  float gc[kC];            // cumulative log decay inside the chunk
+  float bt[kC];            // beta
+  float rowf[kC];          // e^(gc_t - gc_16(t/16)), in (0, 1]
+  float brow[kC];          // beta_t rowf_t
+  float colf[kC];          // e^(gc_16 - gc_t') for t' < 16, in (0, 1]
+};
 
 struct ProducerLds {
   SetBuf s[3];                 // chunk q (T chain), q + 1 (written by the conv waves), q - 1 (copied out), by c % 3
+  Gates g[3];                  // the same chunks' producer-side gate vectors
   float Tm[kC * kMP];          // A, then T, fp32
   float cwq[4][64][kKC];       // q/k conv taps: channel 4 g + c (g < 64: q then k) at cwq[c][g]
 };
 struct ConsumerLds {
   SetBuf s[2];                 // chunk p (state waves) and chunk p + 1 (DMA target)
+  _Float16 KT[kDK * kP];       // k^ of chunk p transposed, [i][t] (8-column groups swizzled by kt32), built by the state waves
   _Float16 VT[2][kDV * kP];    // v^ transposed, [j][t] (8-row groups swizzled by vt32), by chunk parity
   float osg[2][kC * kOP];      // output rows before the gated norm, by chunk parity
   float red[2][kC * 4];        // gated-norm partial sums, [t][state wave], by chunk parity
   float cwv[4][32][kKC];       // v conv taps: channel 4 g + c at cwv[c][g]
+  unsigned kt_ready;           // state waves that have written their quarter of KT so far in the launch (4 per full chunk)
 };
 
-// k^T element (i, t) lives at i * kP + 8 * ((t / 8) ^ ((i / 16) % 4)) + t % 8: a producer lane writes 8 rows of one
-// channel (16 bytes) and the 32 lanes writing channels 4 l + c land on different banks
+// q^ / k^ element (t, i): 8-half unit i / 8 of row t sits at unit (i / 8) ^ (t % 16), so the 16 rows an MFMA operand
+// read covers at one column land on 16 different units
+__device__ __forceinline__ int qk_at(int t, int i) { return t * kDK + 8 * ((i >> 3) ^ (t & 15)) + (i & 7); }
+// element (t, t') of a [32][32] f16 tile: unit t' / 8 of row t sits at unit (t' / 8) ^ ((t / 4) % 4)
+__device__ __forceinline__ int sq_at(int t, int j) { return t * kC + 8 * ((j >> 3) ^ ((t >> 2) & 3)) + (j & 7); }
+// perm_a (gdn_common.h) for the swizzled tiles: A row r, K block kb, lane group grp, the two 4-half pieces at
+// K = 32 kb + 4 grp and 32 kb + 16 + 4 grp
+template <int (*AT)(int, int)>
+__device__ __forceinline__ h8 perm_a_sw(const _Float16* base, int r, int kb, int grp) {
+  const h4 lo = *reinterpret_cast<const h4*>(base + AT(r, 32 * kb + 4 * grp));
+  const h4 hi = *reinterpret_cast<const h4*>(base + AT(r, 32 * kb + 16 + 4 * grp));
+  return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// k^T element (i, t) lives at i * kP + 8 * ((t / 8) ^ ((i / 16) % 4)) + t % 8: a helper lane writes 8 rows of one
+// channel (16 bytes) and the lanes writing channels 2 l + c land on different banks
 __device__ __forceinline__ int kt32(int i, int g8) { return i * kP + 8 * (g8 ^ ((i >> 4) & 3)); }
 
 // v^T element (j, t) lives at j * kP + 8 * ((t / 8) ^ ((j / 16) % 4)) + t % 8: the state waves read 8 rows of one
@@ -175,37 +201,38 @@ __device__ __forceinline__ void fetch_rows(const GdnArgs& a, const RowSrc& src, 
 
 // One 16x16 tile of K K^T (-> A, fp32, in Tm) or Q K^T (-> decay-masked scores, f16) of the chunk in st; block row
 // ti, block column tj <= ti
-__device__ __forceinline__ void tile(Set& st, float* Tm, bool isq, int ti, int tj, int grp, int c16) {
-  const _Float16* ab = (isq ? st.Qs : st.Ks) + (16 * ti + c16) * kQP + 8 * grp;
-  const _Float16* bb = st.Ks + (16 * tj + c16) * kQP + 8 * grp;
+__device__ __forceinline__ void tile(Set& st, const Gates& gt, float* Tm, bool isq, int ti, int tj, int grp, int c16) {
+  const _Float16* ab = isq ? st.Qs : st.Ks;
+  const int ra = 16 * ti + c16, rb = 16 * tj + c16;
   f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ks = 0; ks < 4; ks++)
-    acc = mfma16(*reinterpret_cast<const h8*>(ab + 32 * ks), *reinterpret_cast<const h8*>(bb + 32 * ks), acc);
+    acc = mfma16(*reinterpret_cast<const h8*>(ab + qk_at(ra, 8 * grp + 32 * ks)),
+                 *reinterpret_cast<const h8*>(st.Ks + qk_at(rb, 8 * grp + 32 * ks)), acc);
   const int tp = 16 * tj + c16, t0 = 16 * ti + 4 * grp;
   if (ti != tj) {
     // below the diagonal blocks gc_t <= gc_16 <= gc_t', so e^(gc_t - gc_t') factors into two terms <= 1
-    const float cf = st.colf[tp];
+    const float cf = gt.colf[tp];
     if (!isq) {
-      const f4 bf = lds4(&st.brow[t0]);
+      const f4 bf = lds4(&gt.brow[t0]);
 #pragma unroll
       for (int e = 0; e < 4; e++) Tm[(t0 + e) * kMP + tp] = acc[e] * bf[e] * cf;
     } else {
-      const f4 rf = lds4(&st.rowf[t0]);
+      const f4 rf = lds4(&gt.rowf[t0]);
 #pragma unroll
-      for (int e = 0; e < 4; e++) st.Att[(t0 + e) * kP + tp] = (_Float16)(acc[e] * rf[e] * cf);
+      for (int e = 0; e < 4; e++) st.Att[sq_at(t0 + e, tp)] = (_Float16)(acc[e] * rf[e] * cf);
     }
   } else {
-    const float gq = st.gc[tp];
-    const f4 gt = lds4(&st.gc[t0]), bt = lds4(&st.bt[t0]);
+    const float gq = gt.gc[tp];
+    const f4 gv = lds4(&gt.gc[t0]), bv = lds4(&gt.bt[t0]);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const int t = t0 + e;
-      const float dec = __expf(fminf(gt[e] - gq, 0.0f));
+      const float dec = __expf(fminf(gv[e] - gq, 0.0f));
       if (!isq)
-        Tm[t * kMP + tp] = tp < t ? bt[e] * acc[e] * dec : 0.0f;
+        Tm[t * kMP + tp] = tp < t ? bv[e] * acc[e] * dec : 0.0f;
       else
-        st.Att[t * kP + tp] = (_Float16)(tp <= t ? acc[e] * dec : 0.0f);
+        st.Att[sq_at(t, tp)] = (_Float16)(tp <= t ? acc[e] * dec : 0.0f);
     }
   }
 }
@@ -214,7 +241,7 @@ __device__ __forceinline__ void tile(Set& st, float* Tm, bool isq, int ti, int t
 // owning column c16. Right-looking: once entry r of the column is final, it is eliminated from the rows below, so each
 // step's updates are independent (column r of A read as broadcasts within the group). Groups 0 and 1 store their
 // block: T_bb in Tm, T diag(beta) and T diag(beta e^gc) in the f16 tiles.
-__device__ __forceinline__ void solve_diag(Set& st, float* Tm, int grp, int c16) {
+__device__ __forceinline__ void solve_diag(Set& st, const Gates& gt, float* Tm, int grp, int c16) {
   const int base = 16 * (grp & 1);
   float pc[16];
 #pragma unroll
@@ -226,19 +253,19 @@ __device__ __forceinline__ void solve_diag(Set& st, float* Tm, int grp, int c16)
   }
   wave_sync();  // every lane has read A's block before it is overwritten
   if (grp < 2) {
-    const float cb = st.bt[base + c16], cbw = cb * st.eg[base + c16];
+    const float cb = gt.bt[base + c16], cbw = cb * st.eg[base + c16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       Tm[(base + r) * kMP + base + c16] = pc[r];
-      st.Tb[(base + r) * kP + base + c16] = (_Float16)(pc[r] * cb);
-      st.Tw[(base + r) * kP + base + c16] = (_Float16)(pc[r] * cbw);
+      st.Tb[sq_at(base + r, base + c16)] = (_Float16)(pc[r] * cb);
+      st.Tw[sq_at(base + r, base + c16)] = (_Float16)(pc[r] * cbw);
     }
   }
 }
 
 // The block below the diagonal: T_10 = -T_11 (A_10 T_00) on v_mfma_f32_16x16x4f32, D layout (rows 4 grp + e of the
 // block, column c16) used directly as the next product's B operand, the A operand read in the same K order
-__device__ __forceinline__ void solve_offdiag(Set& st, const float* Tm, int grp, int c16) {
+__device__ __forceinline__ void solve_offdiag(Set& st, const Gates& gt, const float* Tm, int grp, int c16) {
   f4 X = {0.0f, 0.0f, 0.0f, 0.0f}, Y = X;
   const f4 av = lds4(&Tm[(16 + c16) * kMP + 4 * grp]);
   f4 t0;
@@ -249,12 +276,12 @@ __device__ __forceinline__ void solve_offdiag(Set& st, const float* Tm, int grp,
   const f4 tv = lds4(&Tm[(16 + c16) * kMP + 16 + 4 * grp]);
 #pragma unroll
   for (int e = 0; e < 4; e++) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(tv[e], X[e], Y, 0, 0, 0);
-  const float fb = st.bt[c16], fw = fb * st.eg[c16];
+  const float fb = gt.bt[c16], fw = fb * st.eg[c16];
 #pragma unroll
   for (int e = 0; e < 4; e++) {
     const int t = 16 + 4 * grp + e;
-    st.Tb[t * kP + c16] = (_Float16)(-Y[e] * fb);
-    st.Tw[t * kP + c16] = (_Float16)(-Y[e] * fw);
+    st.Tb[sq_at(t, c16)] = (_Float16)(-Y[e] * fb);
+    st.Tw[sq_at(t, c16)] = (_Float16)(-Y[e] * fw);
   }
 }
 
@@ -276,9 +303,9 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
   // the block above the diagonal of every set's f16 T and score tiles is read by full K blocks and never written
   for (int idx = tid0; idx < 3 * 16 * 16; idx += kThreads) {
     const int st = idx >> 8, t = (idx >> 4) & 15, tp = 16 + (idx & 15);
-    sm.s[st].s.Tb[t * kP + tp] = (_Float16)0.0f;
-    sm.s[st].s.Tw[t * kP + tp] = (_Float16)0.0f;
-    sm.s[st].s.Att[t * kP + tp] = (_Float16)0.0f;
+    sm.s[st].s.Tb[sq_at(t, tp)] = (_Float16)0.0f;
+    sm.s[st].s.Tw[sq_at(t, tp)] = (_Float16)0.0f;
+    sm.s[st].s.Att[sq_at(t, tp)] = (_Float16)0.0f;
   }
   const float na = gp<float>(a.negA)[h], db = gp<float>(a.dtb)[h];
   const int aoff = a.C + a.H * kDV + h, boff = aoff + a.H;
@@ -310,11 +337,36 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
   unsigned seen = 0;  // the consumer's progress as last read (copy waves)
   __syncthreads();  // conv taps and zero blocks visible
 
+  // Chunk q - 1's set into its slot: copy wave w (1..3) takes NU 16-byte units from unit u0 on (one store instruction
+  // per 64 units; the set's last instruction is partial), then waits until at most those NU stores are outstanding,
+  // which leaves the previous period's stores complete at the barrier. While the consumer has not yet taken chunk
+  // q - 1 - kLead, the wave holds back for up to 64 polls first (the slot is this chunk's alone, so going on is
+  // always safe).
+  constexpr int kSetUnits = (int)sizeof(Set) / 16;
+  auto copy_out = [&](int c, int u0, auto nu) {
+    constexpr int NU = decltype(nu)::value;
+    if (c >= kLead && seen < ep + (unsigned)(c - kLead + 1))
+      seen = wait_counter(consumed, ep + (unsigned)(c - kLead + 1), 64);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)c * kDuoSetBytes, 0, kDuoSetBytes, 0x00020000);
+    const unsigned char* from = sm.s[c % 3].raw;
+    const int lane = opaque(tid0) & 63;
+#pragma unroll
+    for (int it = 0; it < NU; it++) {
+      const int u = u0 + 64 * it + lane;
+      if (u < kSetUnits) {
+        const f4 v = lds4(reinterpret_cast<const float*>(from + 16 * u));
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), rs, 16 * u, 0, 16);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(wait_vm(NU));
+  };
+
   // Period q: wave 0 runs chunk q's T chain (set q % 3); waves 1..3 copy chunk q - 1's finished set (q - 1) % 3 into
-  // its ring slot, waves 1 and 2 also make chunk q's score tiles, wave 3 the gates of chunk q + 1; the conv waves
-  // write chunk q + 1 into set (q + 1) % 3. One barrier per period. The copy's stores are left to complete during
-  // the next period (the copy waves wait for them before issuing the next copy), so chunk q - 2 is published after
-  // period q's barrier.
+  // its ring slot, waves 1 and 2 after making chunk q's score tiles, wave 3 after the gates of chunk q + 1; the conv
+  // waves write chunk q + 1 into set (q + 1) % 3. One barrier per period. The copy's stores complete during the next
+  // period (the copy waves wait for them after issuing the next copy), so chunk q - 2 is published after period q's
+  // barrier.
   for (int q = -1; q <= n + 1; q++) {
     const int c1 = a.s0 + kC * (q + 1);  // chunk q + 1
     const int tid = opaque(tid0), lane = tid & 63, grp = lane >> 4, c16 = lane & 15;
@@ -345,43 +397,36 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
 #pragma unroll
           for (int c = 0; c < 4; c++) uq[r][c] *= rs;
           const h4 hv = {(_Float16)uq[r][0], (_Float16)uq[r][1], (_Float16)uq[r][2], (_Float16)uq[r][3]};
-          *reinterpret_cast<h4*>((isk ? st.Ks : st.Qs) + (8 * cw + r) * kQP + 4 * l32) = hv;
-        }
-        if (isk) {
-#pragma unroll
-          for (int c = 0; c < 4; c++) {
-            h8 kt;
-#pragma unroll
-            for (int r = 0; r < 8; r++) kt[r] = (_Float16)uq[r][c];
-            *reinterpret_cast<h8*>(st.KT + kt32(4 * l32 + c, cw)) = kt;
-          }
+          *reinterpret_cast<h4*>((isk ? st.Ks : st.Qs) + qk_at(8 * cw + r, 4 * l32)) = hv;
         }
       } else {
         fetch_qk(c1 + kC);
       }
+    } else if (w == 0) {
+      if (q >= 0 && q < n) {
+        Set& st = sm.s[q % 3].s;
+        const Gates& gt = sm.g[q % 3];
+        tile(st, gt, sm.Tm, false, 0, 0, grp, c16);
+        tile(st, gt, sm.Tm, false, 1, 1, grp, c16);
+        tile(st, gt, sm.Tm, false, 1, 0, grp, c16);
+        wave_sync();
+        solve_diag(st, gt, sm.Tm, grp, c16);
+        wave_sync();
+        solve_offdiag(st, gt, sm.Tm, grp, c16);
+      }
     } else {
-      if (w == 0) {
-        if (q >= 0 && q < n) {
-          Set& st = sm.s[q % 3].s;
-          tile(st, sm.Tm, false, 0, 0, grp, c16);
-          tile(st, sm.Tm, false, 1, 1, grp, c16);
-          tile(st, sm.Tm, false, 1, 0, grp, c16);
-          wave_sync();
-          solve_diag(st, sm.Tm, grp, c16);
-          wave_sync();
-          solve_offdiag(st, sm.Tm, grp, c16);
+      if (q >= 0 && q < n) {
+        Set& st = sm.s[q % 3].s;
+        const Gates& gt = sm.g[q % 3];
+        if (w == 1) {
+          tile(st, gt, sm.Tm, true, 0, 0, grp, c16);
+          tile(st, gt, sm.Tm, true, 1, 0, grp, c16);
+        } else if (w == 2) {
+          tile(st, gt, sm.Tm, true, 1, 1, grp, c16);
         }
-      } else {
-        if (q >= 0 && q < n) {
-          Set& st = sm.s[q % 3].s;
-          if (w == 1) {
-            tile(st, sm.Tm, true, 0, 0, grp, c16);
-            tile(st, sm.Tm, true, 1, 0, grp, c16);
-          } else if (w == 2) {
-            tile(st, sm.Tm, true, 1, 1, grp, c16);
-          }
-        }
-        if (w == 3 && q + 1 < n) {
+      }
+      if (w == 3) {
+        if (q + 1 < n) {
           // beta and the cumulative log decay of row `lane` (lanes 0..31) of chunk q + 1
           const int gl = lane & 31, m = min(kC, end - c1);
           float gcr = 0.0f, btr = 0.0f;
@@ -398,33 +443,29 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
           const float glast = __shfl(gcr, 31), g16 = __shfl(gcr, 16);
           const float rf = __expf(gcr - __shfl(gcr, lane & 16));
           Set& st = sm.s[(q + 1) % 3].s;
+          Gates& gt = sm.g[(q + 1) % 3];
           if (lane < 32) {
-            st.gc[lane] = gcr;
+            gt.gc[lane] = gcr;
             st.eg[lane] = __expf(gcr);
-            st.bt[lane] = btr;
+            gt.bt[lane] = btr;
             st.ed[lane] = __expf(glast - gcr);
-            st.rowf[lane] = rf;
-            st.brow[lane] = btr * rf;
-            st.colf[lane] = lane < 16 ? __expf(g16 - gcr) : 0.0f;
+            gt.rowf[lane] = rf;
+            gt.brow[lane] = btr * rf;
+            gt.colf[lane] = lane < 16 ? __expf(g16 - gcr) : 0.0f;
           }
         }
-        // the previous period's ring stores have reached the device-coherent level (they had a period to get there)
-        __builtin_amdgcn_s_waitcnt(0);
-        // chunk q - 1's set into its slot; while the consumer has not yet taken chunk q - 1 - kLead, hold back for up
-        // to 64 polls (the slot is this chunk's alone, so going on is always safe)
-        if (q >= 1 && q <= n) {
-          const int c = q - 1;
-          if (c >= kLead && seen < ep + (unsigned)(c - kLead + 1))
-            seen = wait_counter(consumed, ep + (unsigned)(c - kLead + 1), 64);
-          const __amdgpu_buffer_rsrc_t rs =
-              __builtin_amdgcn_make_buffer_rsrc(ring + (size_t)c * kDuoSetBytes, 0, kDuoSetBytes, 0x00020000);
-          const unsigned char* from = sm.s[c % 3].raw;
-          for (int i = tid - 64; i < kDuoSetBytes / 16; i += 192) {
-            const f4 v = lds4(reinterpret_cast<const float*>(from + 16 * i));
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), rs, 16 * i, 0, 16);
-          }
-        }
-        if (w == 3) fetch_ab(c1 + kC);  // after the drain above, which would otherwise wait for these loads too
+        // issued before the copy's stores, so that the next period's wait for them does not wait for the stores too
+        fetch_ab(c1 + kC);
+      }
+      if (q >= 1 && q <= n) {
+        if (w == 1)
+          copy_out(q - 1, 15 * 64, Width<8>{});
+        else if (w == 2)
+          copy_out(q - 1, 7 * 64, Width<8>{});
+        else
+          copy_out(q - 1, 0, Width<7>{});
+      } else {
+        __builtin_amdgcn_s_waitcnt(wait_vm(0));
       }
     }
     __syncthreads();
@@ -453,6 +494,9 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     const int lc = i / kKC, j = i % kKC;
     sm.cwv[lc & 3][lc >> 2][j] = gp<float>(a.conv_w)[(size_t)(2 * a.H * kDK + h * kDV + lc) * kKC + j];
   }
+  if (tid0 == 0) sm.kt_ready = 0;  // visible to every wave after the prologue's barriers
+  bool kt_late = false;            // a state wave's wait for k^T ran out (never expected: every state wave writes its
+                                   // quarter before its own chunk work)
 
   // Helper lanes: v conv of rows 8 vrg .. + 7 (vrg = the helper wave), channels 2 cvg, 2 cvg + 1 (a row's 128 channels
   // are one 512-byte load across the wave, and the 11 rows a lane loads for its 8 outputs overlap the next wave's by
@@ -560,6 +604,22 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
       if (p < n) {
         const int m = min(kC, end - c0);
         Set& st = sm.s[p & 1].s;
+        if (m == kC) {
+          // k^T of the chunk for the state update: this wave's rows 8 w .. + 7, lane's channels 2 lane and 2 lane + 1;
+          // then one count on kt_ready (the fence orders only LDS)
+          h8 kt[2];
+#pragma unroll
+          for (int r = 0; r < 8; r++) {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            const h2 v = *reinterpret_cast<const h2*>(st.Ks + qk_at(8 * w + r, 2 * lane));
+            kt[0][r] = v[0];
+            kt[1][r] = v[1];
+          }
+#pragma unroll
+          for (int c = 0; c < 2; c++) *reinterpret_cast<h8*>(sm.KT + kt32(2 * lane + c, w)) = kt[c];
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+          if (lane == 0) __hip_atomic_fetch_add(&sm.kt_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
         const _Float16* VT = sm.VT[p & 1];
         float* osg = sm.osg[p & 1];
         // k^ S and q^ S together, K block outermost (one f16 copy of that block of S at a time)
@@ -571,8 +631,8 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
           for (int ct = 0; ct < 2; ct++) S16[ct] = pack_b(S[ct][2 * kb], S[ct][2 * kb + 1]);
 #pragma unroll
           for (int ti = 0; ti < 2; ti++) {
-            const h8 ka = perm_a(st.Ks, kQP, 16 * ti + c16, kb, grp);
-            const h8 qa = perm_a(st.Qs, kQP, 16 * ti + c16, kb, grp);
+            const h8 ka = perm_a_sw<qk_at>(st.Ks, 16 * ti + c16, kb, grp);
+            const h8 qa = perm_a_sw<qk_at>(st.Qs, 16 * ti + c16, kb, grp);
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) {
               const f4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -588,8 +648,8 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
           for (int ct = 0; ct < 2; ct++) KSb[ct] = pack_b(KS[ct][0], KS[ct][1]);
 #pragma unroll
           for (int ti = 0; ti < 2; ti++) {
-            const h8 tb = *reinterpret_cast<const h8*>(st.Tb + (16 * ti + c16) * kP + 8 * grp);
-            const h8 tw = perm_a(st.Tw, kP, 16 * ti + c16, 0, grp);
+            const h8 tb = *reinterpret_cast<const h8*>(st.Tb + sq_at(16 * ti + c16, 8 * grp));
+            const h8 tw = perm_a_sw<sq_at>(st.Tw, 16 * ti + c16, 0, grp);
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) {
               const int col = 32 * w + 16 * ct + c16;
@@ -608,7 +668,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
 #pragma unroll
           for (int ti = 0; ti < 2; ti++) {
             const f4 eg = lds4(&st.eg[16 * ti + 4 * grp]);
-            const h8 at = perm_a(st.Att, kP, 16 * ti + c16, 0, grp);
+            const h8 at = perm_a_sw<sq_at>(st.Att, 16 * ti + c16, 0, grp);
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) O[ct][ti] = mfma16(at, Vb[ct], O[ct][ti] * eg);
           }
@@ -625,9 +685,20 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
 #pragma unroll
           for (int ct = 0; ct < 2; ct++) Vd[ct] = pack_b(Vn[ct][0], Vn[ct][1]);
           const float el = st.eg[kC - 1];
+          // k^T of chunk p: each state wave writes a quarter of it at the start of the period (the counter counts
+          // full chunks only, and chunks before the last are full)
+          const unsigned want = 4u * (unsigned)(p + 1);
+          for (int i = 0; __hip_atomic_load(&sm.kt_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < want; i++) {
+            if (i == kWaitPolls) {
+              kt_late = true;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
           for (int it = 0; it < 8; it++) {
-            const h8 k = perm_a_kt32(st.KT, 16 * it + c16, grp);
+            const h8 k = perm_a_kt32(sm.KT, 16 * it + c16, grp);
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) S[ct][it] = mfma16(k, Vd[ct], S[ct][it] * el);
           }
@@ -718,7 +789,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
           gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16] = S[ct][it][e];
   }
   for (; p <= n; p++) period(p);
-  if (seen == ~0u && (tid0 & 63) == 0) report_wait(a.wait, kErrDuoWait);
+  if ((seen == ~0u || kt_late) && (tid0 & 63) == 0) report_wait(a.wait, kErrDuoWait);
 }
 
 // Blocks 16 i + r (r < 8, the producer) and 16 i + 8 + r (the consumer) form pair 8 i + r. The dispatcher hands

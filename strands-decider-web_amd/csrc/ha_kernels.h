@@ -54,7 +54,7 @@ struct GdnArgs {
   WaitCheck wait;                   // bounded cross-workgroup waits: poll limit, test skew, error word
 };
 constexpr int kSegRows = 64;        // output rows per launch of the sequential form
-constexpr int kDuoSetBytes = 36 * 1024;   // bytes per tile-set slot of the paired form
+constexpr int kDuoSetBytes = 23 * 1024;   // bytes per tile-set slot of the paired form
 constexpr int kDuoEpochShift = 12;        // progress counter value: epoch << kDuoEpochShift | chunks (< 4096)
 
 // Full-attention prep (q/k RMSNorm, partial RoPE, K/V cache write) and attention for rows [P, P + L).
