@@ -18,9 +18,9 @@
 //     1..3 copy chunk q - 1's finished tile set (22.25 KiB: q^, k^, the three [32][32] tiles and two gate vectors,
 //     no padding) into that chunk's slot in device memory.
 //   consumer: waves 0..3 own 32 value columns each of the fp32 state in MFMA accumulators and do the state work of
-//     chunk p, each first transposing a quarter of k^ into a shared k^T (an LDS counter orders those writes before
-//     the state update reads them); meanwhile waves 4..7 (helpers) DMA chunk p + 1's tile set from its slot into
-//     LDS, apply the gated RMSNorm to chunk p - 1's output and store it, and run chunk p + 1's v conv.
+//     chunk p (the state update reads its k^T operand from k^ itself with transposing LDS reads); meanwhile waves
+//     4..7 (helpers) DMA chunk p + 1's tile set from its slot into LDS, apply the gated RMSNorm to chunk p - 1's output
+//     and store it, and run chunk p + 1's v conv.
 // Each role passes one workgroup barrier per period.
 // The two exchange progress through counters: `produced` (tile sets in their slots) and `consumed` (sets copied into
 // the consumer's LDS). Counter values carry a per-launch epoch (epoch << kDuoEpochShift | chunks), so values left by
@@ -95,17 +95,29 @@ struct ProducerLds {
 };
 struct ConsumerLds {
   SetBuf s[2];                 // chunk p (state waves) and chunk p + 1 (DMA target)
-  _Float16 KT[kDK * kP];       // k^ of chunk p transposed, [i][t] (8-column groups swizzled by kt32), built by the state waves
   _Float16 VT[2][kDV * kP];    // v^ transposed, [j][t] (8-row groups swizzled by vt32), by chunk parity
   float osg[2][kC * kOP];      // output rows before the gated norm, by chunk parity
   float red[2][kC * 4];        // gated-norm partial sums, [t][state wave], by chunk parity
   float cwv[4][32][kKC];       // v conv taps: channel 4 g + c at cwv[c][g]
-  unsigned kt_ready;           // state waves that have written their quarter of KT so far in the launch (4 per full chunk)
 };
 
-// q^ / k^ element (t, i): 8-half unit i / 8 of row t sits at unit (i / 8) ^ (t % 16), so the 16 rows an MFMA operand
-// read covers at one column land on 16 different units
-__device__ __forceinline__ int qk_at(int t, int i) { return t * kDK + 8 * ((i >> 3) ^ (t & 15)) + (i & 7); }
+// q^ / k^ element (t, i): 8-half unit i / 8 of row t sits at unit (i / 8) ^ rot(t % 16), rot a one-bit rotation of the
+// row's 4 low bits. A bijection of t % 16: the 16 rows an MFMA operand read covers at one column land on 16 different
+// units. The rotation puts rows 4 g .. 4 g + 3 on units that differ in bits 1..2, so the transposing reads of the
+// state update (two units of each of 4 rows per 16 lanes) touch 8 different units.
+__device__ __forceinline__ int qk_at(int t, int i) {
+  return t * kDK + 8 * ((i >> 3) ^ (((t << 1) | ((t >> 3) & 1)) & 15)) + (i & 7);
+}
+// k^T operand of the state update, read from k^ itself with ds_read_b64_tr_b16. In each 16-lane group of that
+// instruction, lane m receives element (4 e + m / 4, m % 4) of the 16 x 4 matrix whose row j is the 4 halves at lane
+// j's address. Lane (grp, m) supplying the address of k^[r0 + 4 grp + m / 4][i0 + 4 (m % 4)] therefore receives
+// k^[r0 + 4 grp + e][i0 + m], e = 0..3: row i0 + m of k^T at the K indices 4 grp + e of the permuted order.
+__device__ __forceinline__ h4 kT_piece(const _Float16* Ks, int r0, int i0, int grp, int m) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const _Float16* p = Ks + qk_at(r0 + 4 * grp + (m >> 2), i0 + 4 * (m & 3));
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p));
+  return __builtin_bit_cast(h4, v);
+}
 // element (t, t') of a [32][32] f16 tile: unit t' / 8 of row t sits at unit (t' / 8) ^ ((t / 4) % 4)
 __device__ __forceinline__ int sq_at(int t, int j) { return t * kC + 8 * ((j >> 3) ^ ((t >> 2) & 3)) + (j & 7); }
 // perm_a (gdn_common.h) for the swizzled tiles: A row r, K block kb, lane group grp, the two 4-half pieces at
@@ -117,22 +129,10 @@ __device__ __forceinline__ h8 perm_a_sw(const _Float16* base, int r, int kb, int
   return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// k^T element (i, t) lives at i * kP + 8 * ((t / 8) ^ ((i / 16) % 4)) + t % 8: a helper lane writes 8 rows of one
-// channel (16 bytes) and the lanes writing channels 2 l + c land on different banks
-__device__ __forceinline__ int kt32(int i, int g8) { return i * kP + 8 * (g8 ^ ((i >> 4) & 3)); }
-
 // v^T element (j, t) lives at j * kP + 8 * ((t / 8) ^ ((j / 16) % 4)) + t % 8: the state waves read 8 rows of one
 // channel (16 bytes, a B operand) and the helpers write 4 rows of channels 4 cvg + c, which without the swizzle
 // would put every fourth lane on the same banks
 __device__ __forceinline__ int vt32(int j, int g8) { return j * kP + 8 * (g8 ^ ((j >> 4) & 3)); }
-
-// perm_a for the swizzled k^T tile (one K block of 32 chunk rows)
-__device__ __forceinline__ h8 perm_a_kt32(const _Float16* kt, int r, int grp) {
-  const int sub = 4 * (grp & 1);
-  const h4 lo = *reinterpret_cast<const h4*>(kt + kt32(r, grp >> 1) + sub);
-  const h4 hi = *reinterpret_cast<const h4*>(kt + kt32(r, 2 + (grp >> 1)) + sub);
-  return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
 
 // sum over 32 lanes (0..31 or 32..63): the 16 lanes of a DPP row, then the paired row
 __device__ __forceinline__ float sum32(float v) {
@@ -494,9 +494,6 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     const int lc = i / kKC, j = i % kKC;
     sm.cwv[lc & 3][lc >> 2][j] = gp<float>(a.conv_w)[(size_t)(2 * a.H * kDK + h * kDV + lc) * kKC + j];
   }
-  if (tid0 == 0) sm.kt_ready = 0;  // visible to every wave after the prologue's barriers
-  bool kt_late = false;            // a state wave's wait for k^T ran out (never expected: every state wave writes its
-                                   // quarter before its own chunk work)
 
   // Helper lanes: v conv of rows 8 vrg .. + 7 (vrg = the helper wave), channels 2 cvg, 2 cvg + 1 (a row's 128 channels
   // are one 512-byte load across the wave, and the 11 rows a lane loads for its 8 outputs overlap the next wave's by
@@ -604,22 +601,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
       if (p < n) {
         const int m = min(kC, end - c0);
         Set& st = sm.s[p & 1].s;
-        if (m == kC) {
-          // k^T of the chunk for the state update: this wave's rows 8 w .. + 7, lane's channels 2 lane and 2 lane + 1;
-          // then one count on kt_ready (the fence orders only LDS)
-          h8 kt[2];
-#pragma unroll
-          for (int r = 0; r < 8; r++) {
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            const h2 v = *reinterpret_cast<const h2*>(st.Ks + qk_at(8 * w + r, 2 * lane));
-            kt[0][r] = v[0];
-            kt[1][r] = v[1];
-          }
-#pragma unroll
-          for (int c = 0; c < 2; c++) *reinterpret_cast<h8*>(sm.KT + kt32(2 * lane + c, w)) = kt[c];
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-          if (lane == 0) __hip_atomic_fetch_add(&sm.kt_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
+
         const _Float16* VT = sm.VT[p & 1];
         float* osg = sm.osg[p & 1];
         // k^ S and q^ S together, K block outermost (one f16 copy of that block of S at a time)
@@ -685,20 +667,10 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
 #pragma unroll
           for (int ct = 0; ct < 2; ct++) Vd[ct] = pack_b(Vn[ct][0], Vn[ct][1]);
           const float el = st.eg[kC - 1];
-          // k^T of chunk p: each state wave writes a quarter of it at the start of the period (the counter counts
-          // full chunks only, and chunks before the last are full)
-          const unsigned want = 4u * (unsigned)(p + 1);
-          for (int i = 0; __hip_atomic_load(&sm.kt_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < want; i++) {
-            if (i == kWaitPolls) {
-              kt_late = true;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
           for (int it = 0; it < 8; it++) {
-            const h8 k = perm_a_kt32(sm.KT, 16 * it + c16, grp);
+            const h4 lo = kT_piece(st.Ks, 0, 16 * it, grp, c16), hi = kT_piece(st.Ks, 16, 16 * it, grp, c16);
+            const h8 k = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) S[ct][it] = mfma16(k, Vd[ct], S[ct][it] * el);
           }
@@ -789,7 +761,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
           gpw<float>(a.S_out)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16] = S[ct][it][e];
   }
   for (; p <= n; p++) period(p);
-  if ((seen == ~0u || kt_late) && (tid0 & 63) == 0) report_wait(a.wait, kErrDuoWait);
+  if (seen == ~0u && (tid0 & 63) == 0) report_wait(a.wait, kErrDuoWait);
 }
 
 // Blocks 16 i + r (r < 8, the producer) and 16 i + 8 + r (the consumer) form pair 8 i + r. The dispatcher hands
