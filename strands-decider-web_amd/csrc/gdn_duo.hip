@@ -58,6 +58,7 @@ constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 constexpr int kWaitDma = wait_vm(kAfterDma);
 
 typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i2v __attribute__((ext_vector_type(2)));
 
 // One chunk's tiles, as the producer builds them in LDS and the consumer reads them; copied between the two as bytes.
 // No padding: the row layouts are swizzled in 8-half (16-byte) units instead (qk_at, sq_at), so the whole set is data.
@@ -484,6 +485,9 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
   const int n = (end - a.s0 + kC - 1) / kC;
   const int s1 = a.s0 + 64 * ((end - a.s0) / 64);  // the stored state position
   const unsigned orowb = (unsigned)(a.H * kDV) * sizeof(T);
+  // this sequence's output rows as a buffer: stores at offsets past its L rows are dropped by the hardware
+  const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (char*)a.out + (size_t)b * a.L * orowb, 0, (int)((unsigned)a.L * orowb), 0x00020000);
   const char* const seq_in = (const char*)a.in + (size_t)b * a.L * ((unsigned)a.stride * sizeof(T));
   const size_t sbase = ((size_t)b * a.H + h) * kDK * kDV;
   const bool state = w < 4;
@@ -713,8 +717,11 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
       ahead = ld_counter(produced);  // for the next period's check
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
-      if (p >= 1) {
-        // chunk p - 1's gated norm and store
+      {
+        // chunk p - 1's gated norm and store, and chunk p + 1's v conv, without branches so that the compiler can
+        // interleave the two chains: in period 0 the norm works on unused LDS and every row is masked, past the last
+        // chunk the conv writes a v^T buffer no state wave reads. Rows outside the call get a buffer offset past the
+        // sequence's output rows, and the hardware drops those stores.
         const int cp = c0 - kC, mp = min(kC, end - cp), fr = ht0 >> 3, fc = 4 * (ht0 & 7);
         const float* osg = sm.osg[(p - 1) & 1];
         f4 y[4];
@@ -728,14 +735,20 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
 #pragma unroll
             for (int c = 0; c < 4; c++) y[q][c] = y[q][c] * iv * (gw[q][c] * silu(zq[q][c]));
         }
-        if (fr < mp && cp + fr >= a.P) {
-          __attribute__((address_space(1))) T* orow =
-              gpw<T>((char*)a.out + ((size_t)b * a.L + (cp + fr - a.P)) * (size_t)orowb) + (size_t)h * kDV + fc;
+        const bool live = fr < mp && cp + fr >= a.P;
+        const unsigned off = live ? (unsigned)(cp + fr - a.P) * orowb + (unsigned)(h * kDV + fc) * (unsigned)sizeof(T)
+                                  : 0x80000000u;
 #pragma unroll
-          for (int q = 0; q < 4; q++) store4(orow + 32 * q, y[q]);
+        for (int q = 0; q < 4; q++) {
+          if constexpr (sizeof(T) == 4) {
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, y[q]), orsrc, off + 128u * q, 0, 0);
+          } else {
+            const h4 hv = {(_Float16)y[q][0], (_Float16)y[q][1], (_Float16)y[q][2], (_Float16)y[q][3]};
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2v, hv), orsrc, off + 64u * q, 0, 0);
+          }
         }
+        vconv(c0 + kC);
       }
-      if (p + 1 < n) vconv(c0 + kC);
       // chunk p + 1's tile set has landed in LDS: at most the kAfterDma loads issued after the DMA (and the stores
       // after them) may still be in flight (vmcnt counts in issue order)
       __builtin_amdgcn_s_waitcnt(kWaitDma);
