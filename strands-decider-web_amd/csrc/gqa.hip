@@ -132,15 +132,25 @@ __device__ __forceinline__ float wave_sum64(float v) {
 // K rows and V^T columns for rows [t0, t0 + 64) of one (sequence, KV head). Wave w takes rows kKvRows w ..
 // kKvRows w + kKvRows - 1, lane l dims 4 l .. 4 l + 3: every row's k and v loads are issued before any is used. k:
 // RMSNorm (wave-wide sum of squares), gain, rotate-half RoPE on dims [0, 64) (dim i < 32 pairs with i + 32, held by
-// lane l ^ 8), f16. v: f16 into LDS, then each thread writes 32 positions of one dim of V^T, 16 bytes at a time when
-// aligned.
+// lane l ^ 8), f16. v: a lane holds its 4 dims of the wave's 8 rows, so it writes V^T straight from registers: per
+// dim the 8 positions as one 16-byte store when all 8 rows are live and aligned, else position by position.
 constexpr int kKvWaves = 8, kKvRows = 64 / kKvWaves;
 template <typename T>
 __global__ __launch_bounds__(64 * kKvWaves) void gqa_kv_kernel(GqaArgs a) {
-  __shared__ _Float16 vs[64][kHD + 8];
+  static_assert(kKvRows == 8, "a lane's 8 rows of one dim form one 16-byte V^T store");
+  __shared__ f4 rope_l[64][16];  // the RoPE table rows (64 cos/sin floats) of the workgroup's 64 positions
   const int t0 = blockIdx.x * 64, kh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const size_t kvb = ((size_t)b * a.HK + kh) * a.LT * kHD;
+  // the table rows go out first, so that staging them waits for them alone; the row loads below stay in flight
+  // across the barrier that publishes them
+  {
+    const int pr = tid >> 3, c = 2 * (tid & 7);
+    gptr<float> rp = gp<float>(a.rope) + (size_t)(a.P + min(t0 + pr, a.L - 1)) * a.RD + 4 * c;
+    const f4 r0 = *(gptr<f4>)(rp), r1 = *(gptr<f4>)(rp + 4);
+    rope_l[pr][c] = r0;
+    rope_l[pr][c + 1] = r1;
+  }
   const f4 kw = *(gptr<f4>)(gp<float>(a.kw) + 4 * lane);
   f4 x[kKvRows], vv[kKvRows];
 #pragma unroll
@@ -152,6 +162,7 @@ __global__ __launch_bounds__(64 * kKvWaves) void gqa_kv_kernel(GqaArgs a) {
   }
   const bool rot = lane < 16;  // dims 0 .. 63 (RD = 64)
   const int ri = 4 * (lane & 7);
+  __syncthreads();  // RoPE rows staged
 #pragma unroll
   for (int r = 0; r < kKvRows; r++) {
     const int t = t0 + kKvRows * wave + r, pos = a.P + min(t, a.L - 1);
@@ -160,10 +171,9 @@ __global__ __launch_bounds__(64 * kKvWaves) void gqa_kv_kernel(GqaArgs a) {
     f4 k = x[r] * inv * kw;
     f4 pk;
 #pragma unroll
-    for (int c = 0; c < 4; c++) pk[c] = __shfl_xor(k[c], 8);
+    for (int c = 0; c < 4; c++) pk[c] = dpp<0x128>(k[c]);  // lane l ^ 8: row_ror:8 within each 16-lane row
     if (rot) {
-      const f4 cs0 = *(gptr<f4>)(gp<float>(a.rope) + (size_t)pos * a.RD + 2 * ri);
-      const f4 cs1 = *(gptr<f4>)(gp<float>(a.rope) + (size_t)pos * a.RD + 2 * ri + 4);
+      const f4 cs0 = rope_l[kKvRows * wave + r][ri >> 1], cs1 = rope_l[kKvRows * wave + r][(ri >> 1) + 1];
       const float cs[4] = {cs0[0], cs0[2], cs1[0], cs1[2]}, sn[4] = {cs0[1], cs0[3], cs1[1], cs1[3]};
 #pragma unroll
       for (int c = 0; c < 4; c++) k[c] = lane < 8 ? k[c] * cs[c] - pk[c] * sn[c] : k[c] * cs[c] + pk[c] * sn[c];
@@ -171,23 +181,23 @@ __global__ __launch_bounds__(64 * kKvWaves) void gqa_kv_kernel(GqaArgs a) {
     if (t < a.L)
       *(__attribute__((address_space(1))) h4*)(gpw<_Float16>(a.K) + kvb + (size_t)pos * kHD + 4 * lane) =
           h4{(_Float16)k[0], (_Float16)k[1], (_Float16)k[2], (_Float16)k[3]};
-    *reinterpret_cast<h4*>(&vs[kKvRows * wave + r][4 * lane]) =
-        h4{(_Float16)vv[r][0], (_Float16)vv[r][1], (_Float16)vv[r][2], (_Float16)vv[r][3]};
   }
-  __syncthreads();
-  const int d = tid & (kHD - 1), p0 = 32 * (tid >> 8);  // dim, first of this thread's 32 positions
-  const int n = min(64, a.L - t0);
-  __attribute__((address_space(1))) _Float16* vt = gpw<_Float16>(a.V) + kvb + (size_t)d * a.LT + a.P + t0;
-  if (n == 64 && ((a.P + t0) & 7) == 0) {
+  const int tw = t0 + kKvRows * wave;  // the wave's first row
+  __attribute__((address_space(1))) _Float16* vt = gpw<_Float16>(a.V) + kvb + (size_t)(4 * lane) * a.LT + a.P + tw;
+  if (tw + kKvRows <= a.L && ((a.P + tw) & 7) == 0) {
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
+    for (int c = 0; c < 4; c++) {
       h8 v8;
 #pragma unroll
-      for (int e = 0; e < 8; e++) v8[e] = vs[p0 + 8 * g + e][d];
-      *(__attribute__((address_space(1))) h8*)(vt + p0 + 8 * g) = v8;
+      for (int r = 0; r < kKvRows; r++) v8[r] = (_Float16)vv[r][c];
+      *(__attribute__((address_space(1))) h8*)(vt + (size_t)c * a.LT) = v8;
     }
   } else {
-    for (int r = p0; r < min(n, p0 + 32); r++) vt[r] = vs[r][d];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+      for (int r = 0; r < kKvRows; r++)
+        if (tw + r < a.L) vt[(size_t)c * a.LT + r] = (_Float16)vv[r][c];
   }
 }
 
