@@ -220,6 +220,7 @@ constexpr int kWaves = 8;
 // pieces never wait, so every mark is eventually written, and each wait is bounded besides.
 constexpr int kCacheSc1 = 16;  // cache-policy operand of buffer instructions: device-coherent (sc1)
 typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ unsigned* part_marks(const GqaArgs& a) {
   return reinterpret_cast<unsigned*>(a.part + (size_t)a.part_slots * 4 * kRows * (kHD + 2));
 }
@@ -671,20 +672,37 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // so gate loads and output stores are 8- or 16-byte accesses, all issued before they are needed.
   // The gate loads of f16 rows (both passes, 64 VGPRs once Q is dead) are all issued first; f32 rows load each pass's
   // at its start.
+  // The sequence's input and output rows are buffer ranges: a row at or past the call's end lies past the range, so
+  // its gate loads read zeros and its stores are dropped by the hardware (the range check covers the per-lane
+  // offset, which carries the row). No row index is clamped or tested, and each row costs one offset add.
   typedef typename std::conditional<sizeof(T) == 2, h4, f4>::type G4;
+  const __amdgpu_buffer_rsrc_t gin = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(reinterpret_cast<const char*>(a.in)) + (size_t)b * a.L * a.stride * sizeof(T), 0,
+      (int)((size_t)a.L * a.stride * sizeof(T)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t gout = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<char*>(a.out) + (size_t)b * a.L * a.HQ * kHD * sizeof(T), 0,
+      (int)((size_t)a.L * a.HQ * kHD * sizeof(T)), 0x00020000);
+  const unsigned gv0 = ((unsigned)(q0 + er) * (unsigned)a.stride + (unsigned)(h * 2 * kHD + kHD + ec)) * sizeof(T);
+  const unsigned ov0 = ((unsigned)(q0 + er) * (unsigned)(a.HQ * kHD) + (unsigned)(h * kHD + ec)) * sizeof(T);
+  const unsigned gstep = 2u * (unsigned)a.stride * sizeof(T), ostep = 2u * (unsigned)(a.HQ * kHD) * sizeof(T);
   G4 graw[2][16];
   auto load_gates = [&](int p) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      const int tc = min(q0 + 2 * i + er, a.L - 1);
-      graw[p][i] = *(gptr<G4>)(gp<T>(a.in) + ((size_t)b * a.L + tc) * a.stride + (size_t)h * 2 * kHD + kHD + 128 * p + ec);
+      const unsigned off = gv0 + (unsigned)i * gstep + 128u * p * sizeof(T);
+      if constexpr (sizeof(T) == 2)
+        graw[p][i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(gin, off, 0, 0));
+      else
+        graw[p][i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(gin, off, 0, 0));
     }
   };
   load_gates(0);
   if constexpr (sizeof(T) == 2) load_gates(1);
+  // 1 / l: one division per lane for its own row (lane c32 holds row c32's sum), handed to the lanes that need it
+  const float rinv = 1.0f / lsum;
   float linv[16];
 #pragma unroll
-  for (int v = 0; v < 16; v++) linv[v] = 1.0f / __shfl(lsum, 8 * (v >> 2) + 4 * half + (v & 3));
+  for (int v = 0; v < 16; v++) linv[v] = __shfl(rinv, 8 * (v >> 2) + 4 * half + (v & 3));
 #pragma unroll
   for (int p = 0; p < 2; p++) {
     if constexpr (sizeof(T) == 4) {
@@ -697,12 +715,16 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
     wave_sync();
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      const int t = q0 + 2 * i + er;
       const f4 o = lds4(ep + (2 * i + er) * kEP + ec);
       f4 r;
 #pragma unroll
       for (int c = 0; c < 4; c++) r[c] = o[c] * sigmoid((float)graw[p][i][c]);
-      if (t < a.L) store4(gpw<T>(a.out) + ((size_t)b * a.L + t) * (size_t)(a.HQ * kHD) + (size_t)h * kHD + 128 * p + ec, r);
+      const unsigned off = ov0 + (unsigned)i * ostep + 128u * p * sizeof(T);
+      if constexpr (sizeof(T) == 2)
+        __builtin_amdgcn_raw_buffer_store_b64(
+            __builtin_bit_cast(i2v, h4{(_Float16)r[0], (_Float16)r[1], (_Float16)r[2], (_Float16)r[3]}), gout, off, 0, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, r), gout, off, 0, 0);
     }
     wave_sync();
   }
