@@ -437,25 +437,33 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
       for (int j = 0; j < 4; j++) rz[ks][j] = *(gptr<f4>)(rp + 32 * ks + 4 * j);
-    const float scale = rsqrtf((float)kHD);
+    // x 1/sqrt(HD) = 2^-4 on the f16 value: an exact power-of-two scale, so the f16 product (packed, two dims per
+    // instruction) is the f16 rounding of the exact one
+    static_assert(kHD == 256, "the q scale 1/sqrt(HD) is 2^-4");
+    const h8 scale = h8{} + (_Float16)0.0625f;
     float ss = 0.0f;
     // n(ks, e) = q * inv * w for dim 16 ks + 8 half + e, from the raw value x
     auto finish = [&](int ks, const float* x, float inv) {
       const f4 w0 = lds4(qw_l + 16 * ks + 8 * half), w1 = lds4(qw_l + 16 * ks + 8 * half + 4);
+      h8 n;
 #pragma unroll
-      for (int e = 0; e < 8; e++) qreg[ks][e] = (_Float16)((float)(_Float16)(x[e] * inv * (e < 4 ? w0[e] : w1[e - 4])) * scale);
+      for (int e = 0; e < 8; e++) n[e] = (_Float16)(x[e] * inv * (e < 4 ? w0[e] : w1[e - 4]));
+      qreg[ks] = n * scale;
     };
     auto rotate = [&](int ks, const float* x1, const float* x2, float inv) {
       const f4 w10 = lds4(qw_l + 16 * ks + 8 * half), w11 = lds4(qw_l + 16 * ks + 8 * half + 4);
       const f4 w20 = lds4(qw_l + 16 * ks + 8 * half + 32), w21 = lds4(qw_l + 16 * ks + 8 * half + 36);
+      h8 r1, r2;
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const float n1 = x1[e] * inv * (e < 4 ? w10[e] : w11[e - 4]), n2 = x2[e] * inv * (e < 4 ? w20[e] : w21[e - 4]);
         const f4 c = rz[ks][e >> 1];
         const float cs = c[2 * (e & 1)], sn = c[2 * (e & 1) + 1];
-        qreg[ks][e] = (_Float16)((float)(_Float16)(n1 * cs - n2 * sn) * scale);
-        qreg[ks + 2][e] = (_Float16)((float)(_Float16)(n2 * cs + n1 * sn) * scale);
+        r1[e] = (_Float16)(n1 * cs - n2 * sn);
+        r2[e] = (_Float16)(n2 * cs + n1 * sn);
       }
+      qreg[ks] = r1 * scale;
+      qreg[ks + 2] = r2 * scale;
     };
     if constexpr (sizeof(T) == 2) {
       // f16 rows: the whole row slice (16 x 16 B) is loaded at once and converted in place
