@@ -397,8 +397,12 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // kIdleHalf (calls of at most 32 rows, as in a decode step, where every block's second half holds no row of the
   // call): that half's waves copy every tile and the first half's waves none, which takes the copies off the path of
   // the waves that compute
+  // Longer calls: waves 0..3 (which always hold rows) copy every tile and waves 4..7 none, which staggers the two
+  // waves of each SIMD a little (one starts a tile's MFMAs while the other still issues copies).
   auto issue = [&](int kt, int ln) {
-    if constexpr (!kIdleHalf) issue_share(kt, ln, std::false_type{});
+    if constexpr (!kIdleHalf) {
+      if (wave < 4) issue_share(kt, ln, std::true_type{});
+    }
   };
 
   // Q as the B operand of S^T = K Q^T (32x32x16): qreg[ks] = q[q0 + c32][16 ks + 8 half .. +7], prepared here:
@@ -410,17 +414,20 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // The first tile's K/V copy is issued once the lane's Q loads are out, so that those return first.
   float* qw_l = reinterpret_cast<float*>(lds_raw + (size_t)(((kt0 & 1) ^ 1) * 2) * kTileBytes);
   if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = *(gptr<f4>)(gp<float>(a.qw) + 4 * tid);
-  // A wave whose 32 rows all lie past the call's end (the second half of a block with at most 32 rows, as in a
-  // decode step) copies every tile (the first half's waves copy none) and meets the other waves' barriers (q's weights staged, first
-  // tile in, then one per tile), then leaves: its rows are never stored (nor read from a piece's partial results),
-  // and no other row depends on it. Barriers after that count only the waves still running.
+  // A wave whose 32 rows all lie past the call's end (the second half of a block with at most 32 rows) meets the
+  // other waves' barriers (q's weights staged, first tile in, then one per tile), copying every tile in calls of at
+  // most 32 rows (kIdleHalf: the first half's waves copy none) and nothing in longer ones (the first half's waves
+  // copy every tile), then leaves: its rows are never stored (nor read from a piece's partial results), and no other
+  // row depends on it. Barriers after that count only the waves still running.
   if (q0 >= a.L) {
-    issue_share(kt0, lane, std::integral_constant<bool, kIdleHalf>{});
+    if constexpr (kIdleHalf) issue_share(kt0, lane, std::true_type{});
     __syncthreads();
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int kt = kt0; kt < kt1; kt++) {
-      if (kt + 1 < kt1) issue_share(kt + 1, opaque(tid) & 63, std::integral_constant<bool, kIdleHalf>{});
+      if constexpr (kIdleHalf) {
+        if (kt + 1 < kt1) issue_share(kt + 1, opaque(tid) & 63, std::true_type{});
+      }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
