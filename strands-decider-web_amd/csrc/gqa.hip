@@ -788,6 +788,10 @@ hipError_t launch_gqa(const GqaArgs& a, hipStream_t s) {
   // RD = 64 puts both halves of every rotated q pair in one lane of the fused q preparation
   if (a.HD != kHD || a.RD != 64 || a.HQ % a.HK || a.HQ / a.HK != 4) return hipErrorInvalidValue;
   if (a.LT % kBK) return hipErrorInvalidValue;  // V^T tiles are read 64 positions at a time, inside [0, LT)
+  // the attention epilogue addresses a sequence's input and output rows by 32-bit byte offsets, rows past the call's
+  // end (up to 64 on) included: they must not wrap
+  const size_t esz = a.dtype == 0 ? 4 : 2, rows = (size_t)a.L + 64;
+  if (rows * a.stride * esz > 0xFFFFFFFFull || rows * a.HQ * kHD * esz > 0xFFFFFFFFull) return hipErrorInvalidValue;
   dim3 kgrid((a.L + 63) / 64, a.HK, a.B), kblock(64 * kKvWaves);
   if (a.dtype == 0)
     hipLaunchKernelGGL(gqa_kv_kernel<float>, kgrid, kblock, 0, s, a);
