@@ -339,10 +339,9 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
   __syncthreads();  // conv taps and zero blocks visible
 
   // Chunk q - 1's set into its slot: copy wave w (1..3) takes NU 16-byte units from unit u0 on (one store instruction
-  // per 64 units; the set's last instruction is partial), then waits until at most those NU stores are outstanding,
-  // which leaves the previous period's stores complete at the barrier. While the consumer has not yet taken chunk
-  // q - 1 - kLead, the wave holds back for up to 64 polls first (the slot is this chunk's alone, so going on is
-  // always safe).
+  // per 64 units; the set's last instruction is partial); the period's end waits for those stores. While the consumer
+  // has not yet taken chunk q - 1 - kLead, the wave holds back for up to 64 polls first (the slot is this chunk's
+  // alone, so going on is always safe).
   constexpr int kSetUnits = (int)sizeof(Set) / 16;
   auto copy_out = [&](int c, int u0, auto nu) {
     constexpr int NU = decltype(nu)::value;
@@ -360,13 +359,12 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, v), rs, 16 * u, 0, 16);
       }
     }
-    __builtin_amdgcn_s_waitcnt(wait_vm(NU));
   };
 
   // Period q: wave 0 runs chunk q's T chain (set q % 3); waves 1..3 copy chunk q - 1's finished set (q - 1) % 3 into
   // its ring slot, waves 1 and 2 after making chunk q's score tiles, wave 3 after the gates of chunk q + 1; the conv
-  // waves write chunk q + 1 into set (q + 1) % 3. One barrier per period. The copy's stores complete during the next
-  // period (the copy waves wait for them after issuing the next copy), so chunk q - 2 is published after period q's
+  // waves write chunk q + 1 into set (q + 1) % 3. One barrier per period. The copy waves wait for their stores at the
+  // period's end (they were issued a good part of a period earlier), so chunk q - 1 is published after period q's
   // barrier.
   for (int q = -1; q <= n + 1; q++) {
     const int c1 = a.s0 + kC * (q + 1);  // chunk q + 1
@@ -465,12 +463,11 @@ __device__ __forceinline__ void produce(const GdnArgs& a, int b, int h, Producer
           copy_out(q - 1, 7 * 64, Width<8>{});
         else
           copy_out(q - 1, 0, Width<7>{});
-      } else {
-        __builtin_amdgcn_s_waitcnt(wait_vm(0));
       }
+      __builtin_amdgcn_s_waitcnt(wait_vm(0));  // this period's set stores (and wave 3's gate loads) are complete
     }
     __syncthreads();
-    if (tid0 == 64 && q >= 2) st_counter(produced, ep + (unsigned)(q - 1));  // chunks 0 .. q - 2 are in their slots
+    if (tid0 == 64 && q >= 1) st_counter(produced, ep + (unsigned)min(q, n));  // chunks 0 .. q - 1 are in their slots
   }
 }
 
