@@ -574,8 +574,9 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
           S[ct][it][e] = a.S_in ? gp<float>(a.S_in)[sbase + (size_t)(16 * it + 4 * g0 + e) * kDV + 32 * w + 16 * ct + l16]
                                 : 0.0f;
   } else {
+    // the first chunk's v conv and the next rows' loads before the wait for the producer's first tile set, which
+    // they do not need
     fetch_v(a.s0);
-    dma_set(0, hw);
     __syncthreads();  // v conv taps visible (the state waves pass this barrier below)
 #pragma unroll
     for (int r = 0; r < kKC + 7; r++)
@@ -584,6 +585,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     vconv(a.s0);
     fetch_v(a.s0 + kC);
     fetch_z(a.s0);
+    dma_set(0, hw);
   }
   // Drain the prologue's loads: the compiler's wait counting merges the loop's entry state into every period, so a load
   // still outstanding at the loop head would make each period's first use of its registers wait for every global access
