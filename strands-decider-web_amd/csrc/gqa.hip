@@ -368,20 +368,19 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   gptr<_Float16> Kg = gp<_Float16>(a.K) + kvb;
   gptr<_Float16> Vg = gp<_Float16>(a.V) + kvb;
 
-  // a tile = 32 K instructions (2 keys each) + 32 V^T instructions (8 dims each); each wave issues 4 + 4. The
-  // lane's share of the addresses is re-derived from `ln` on every call (cheap VALU) rather than kept live across the
-  // loop: spilled addresses would be reloaded through the same counter the tile loads are waited on.
-  // kAll: this wave issues twice its share, instructions (wave & 3) + 4 i (the waves of a block's second half,
-  // when they copy the whole tile for the first half's waves)
-  auto issue_share = [&](int kt, int ln, auto all) {
-    constexpr bool kAll = decltype(all)::value;
+  // A tile = 32 K instructions (2 keys each) + 32 V^T instructions (8 dims each), all issued by the four waves of
+  // one half of the block (waves 0..3 in longer calls, waves 4..7 in calls of at most 32 rows): instructions
+  // (wave & 3) + 4 i, 8 + 8 per wave. The lane's share of the addresses is re-derived from `ln` on every call (cheap
+  // VALU) rather than kept live across the loop: spilled addresses would be reloaded through the same counter the
+  // tile loads are waited on.
+  auto issue_tile = [&](int kt, int ln) {
     _Float16* kb = lds + (size_t)(kt & 1) * 2 * kTileHalves;
     _Float16* vb = kb + kTileHalves;
     const char* kg = (const char*)(Kg + (size_t)kt * kBK * kHD);
     const char* vg = (const char*)(Vg + (size_t)kt * kBK);
 #pragma unroll
-    for (int i = 0; i < (kAll ? 8 : 4); i++) {
-      const int ins = kAll ? (wave & 3) + 4 * i : wave + kWaves * i;  // 0..31
+    for (int i = 0; i < 8; i++) {
+      const int ins = (wave & 3) + 4 * i;  // 0..31
       const int r = 2 * ins + (ln >> 5), js = ln & 31;
       const int j = js ^ (r & 31);                   // global chunk that belongs in slot js
       const unsigned ko = (unsigned)(r * kHD + 8 * j) * 2u;
@@ -401,7 +400,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // waves of each SIMD a little (one starts a tile's MFMAs while the other still issues copies).
   auto issue = [&](int kt, int ln) {
     if constexpr (!kIdleHalf) {
-      if (wave < 4) issue_share(kt, ln, std::true_type{});
+      if (wave < 4) issue_tile(kt, ln);
     }
   };
 
@@ -420,13 +419,13 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // copy every tile), then leaves: its rows are never stored (nor read from a piece's partial results), and no other
   // row depends on it. Barriers after that count only the waves still running.
   if (q0 >= a.L) {
-    if constexpr (kIdleHalf) issue_share(kt0, lane, std::true_type{});
+    if constexpr (kIdleHalf) issue_tile(kt0, lane);
     __syncthreads();
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int kt = kt0; kt < kt1; kt++) {
       if constexpr (kIdleHalf) {
-        if (kt + 1 < kt1) issue_share(kt + 1, opaque(tid) & 63, std::true_type{});
+        if (kt + 1 < kt1) issue_tile(kt + 1, opaque(tid) & 63);
       }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
