@@ -515,6 +515,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     const int ht = opaque(tid0) - 256, vrg = ht >> 6, cvg = ht & 63;
     fetch_rows<T>(a, src, b, min(cs, last_cs), 8 * vrg, 2 * a.H * kDK + h * kDV + 2 * cvg, xn);
   };
+  f4 wcv[2];  // the lane's two channels' conv taps, read from LDS once the taps are staged
   auto vconv = [&](int cs) {
     const int ht = opaque(tid0) - 256, vrg = ht >> 6, cvg = ht & 63;
     const int mv = min(kC, end - cs);
@@ -522,7 +523,7 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const int j = 2 * cvg + c;
-      const f4 wc = lds4(sm.cwv[j & 3][j >> 2]);
+      const f4 wc = wcv[c];
       h8 vt;
 #pragma unroll
       for (int r = 0; r < 8; r++) {
@@ -578,6 +579,11 @@ __device__ __forceinline__ void consume(const GdnArgs& a, int b, int h, Consumer
     // they do not need
     fetch_v(a.s0);
     __syncthreads();  // v conv taps visible (the state waves pass this barrier below)
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int j = 2 * (ht0 & 63) + c;
+      wcv[c] = lds4(sm.cwv[j & 3][j >> 2]);
+    }
 #pragma unroll
     for (int r = 0; r < kKC + 7; r++)
 #pragma unroll
