@@ -409,10 +409,13 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
   // ks 2/3 of the same lane and element), then f16(f16(.) / sqrt(HD)). A row past the end (t >= L) repeats row
   // L - 1: rows are independent and such a row is never stored, so every load here is unconditional.
   // qw (the stored 1 + w) is staged in LDS, in the tile buffer the first tile does not use (nothing is loaded into it
-  // before the loop): every lane needs 128 of the 256 weights, the same ones as every other lane of its half.
+  // before the loop): every lane needs 128 of the 256 weights, the same ones as every other lane of its half. Wave 0
+  // (always one with rows) loads them first and writes them to LDS once its Q loads are out, so that it does not wait
+  // for them before issuing those.
   // The first tile's K/V copy is issued once the lane's Q loads are out, so that those return first.
   float* qw_l = reinterpret_cast<float*>(lds_raw + (size_t)(((kt0 & 1) ^ 1) * 2) * kTileBytes);
-  if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = *(gptr<f4>)(gp<float>(a.qw) + 4 * tid);
+  f4 qwv = {};
+  if (tid < kHD / 4) qwv = *(gptr<f4>)(gp<float>(a.qw) + 4 * tid);
   // A wave whose 32 rows all lie past the call's end (the second half of a block with at most 32 rows) meets the
   // other waves' barriers (q's weights staged, first tile in, then one per tile), copying every tile in calls of at
   // most 32 rows (kIdleHalf: the first half's waves copy none) and nothing in longer ones (the first half's waves
@@ -476,6 +479,8 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
       h8 raw[16];
 #pragma unroll
       for (int ks = 0; ks < 16; ks++) raw[ks] = *(gptr<h8>)(src + 16 * ks + 8 * half);
+      // before the tile's DMA, after which the compiler would wait for every load (the DMA included) to write it
+      if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = qwv;
       issue(kt0, lane);
 #pragma unroll
       for (int ks = 0; ks < 16; ks++)
@@ -513,7 +518,10 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_attn_kernel(GqaArgs a, int pe
 #pragma unroll
           for (int e = 0; e < 8; e++) ss += qv[k][e] * qv[k][e];
         asm volatile("" : "+v"(ss)::"memory");
-        if (bt == 0) issue(kt0, lane);
+        if (bt == 0) {
+          if (tid < kHD / 4) *reinterpret_cast<f4*>(qw_l + 4 * tid) = qwv;  // before the tile's DMA (see f16 rows)
+          issue(kt0, lane);
+        }
       }
       const float inv = rsqrtf(sum_halves(ss) / kHD + 1e-6f);
       __syncthreads();  // qw staged
